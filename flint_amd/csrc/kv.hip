@@ -1,0 +1,378 @@
+// KV append/scatter (kv_store), gather, scatter and page copy kernels.
+//
+// All four move 16-byte vectors: one lane owns 8 consecutive head_dim
+// elements of one token of one head, so a wave touches whole 128-byte lines
+// of a token row and every store is a single global_store_dwordx4.
+#include <string>
+
+#include "pool.hpp"
+
+namespace thb {
+namespace {
+
+constexpr uint32_t kMaxGridY = 65535;
+
+// f32 -> f16 with round-to-nearest-even, subnormals, saturation to
+// infinity and NaN -> sign|0x7E00, in integer ops so the bits match the
+// reference codec (crates/thuban_num/src/lib.rs:25-60) for every input.
+__device__ __forceinline__ uint32_t f32_to_f16_bits(uint32_t bits) {
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const int32_t exp = static_cast<int32_t>((bits >> 23) & 0xffu);
+    const uint32_t mant = bits & 0x7fffffu;
+    if (exp == 0xff) return sign | (mant ? 0x7e00u : 0x7c00u);
+    const int32_t he = exp - 112;
+    if (he >= 31) return sign | 0x7c00u;
+    if (he <= 0) {
+        if (he < -10) return sign;
+        const uint32_t m = mant | 0x800000u;
+        const uint32_t shift = static_cast<uint32_t>(14 - he);
+        const uint32_t sh = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u);
+        const uint32_t half = 1u << (shift - 1u);
+        return sign | (sh + ((rem > half || (rem == half && (sh & 1u))) ? 1u : 0u));
+    }
+    const uint32_t frac = mant >> 13, rem = mant & 0x1fffu;
+    uint32_t r = sign | (static_cast<uint32_t>(he) << 10) | frac;
+    if (rem > 0x1000u || (rem == 0x1000u && (frac & 1u))) r += 1u;
+    return r & 0xffffu;
+}
+
+// f16 -> f32 bits exactly as crates/thuban_num/src/lib.rs:1-23.
+__device__ __forceinline__ uint32_t f16_to_f32_bits(uint32_t h) {
+    const uint32_t sign = (h >> 15) & 1u, exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
+    if (exp == 0) {
+        if (mant == 0) return sign << 31;
+        // normalise: leading one of the 10-bit mantissa
+        const uint32_t lz = __builtin_clz(mant) - 22;  // zeros above bit 9
+        const uint32_t m = (mant << (lz + 1)) & 0x3ffu;
+        const uint32_t e = 113u - (lz + 1);
+        return (sign << 31) | (e << 23) | (m << 13);
+    }
+    if (exp == 0x1f) return (sign << 31) | 0x7f800000u | (mant << 13);
+    return (sign << 31) | ((exp + 112u) << 23) | (mant << 13);
+}
+
+// Converts one 16-bit source word to the KV encoding.
+template <uint32_t SRC, uint32_t KV>
+__device__ __forceinline__ uint32_t conv16(uint32_t w) {
+    if constexpr (SRC == THB_DT_F16) {
+        if constexpr (KV == THB_KV_F16_RNE) return w;
+        return f16_to_f32_bits(w) >> 16;  // f16 -> f32 (exact) -> truncate
+    } else {  // bf16
+        if constexpr (KV == THB_KV_BF16_TRUNC) return w;
+        return f32_to_f16_bits(w << 16);
+    }
+}
+
+template <uint32_t KV>
+__device__ __forceinline__ uint32_t conv32(uint32_t bits) {
+    if constexpr (KV == THB_KV_F16_RNE) return f32_to_f16_bits(bits);
+    return bits >> 16;  // kv_store.wgsl:20-22
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (the source rows are read exactly once).
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Loads 8 source elements at element index e and returns them encoded.
+template <uint32_t SRC, uint32_t KV>
+__device__ __forceinline__ uint4 load_encode8(const void* src, uint64_t e) {
+    uint4 out;
+    if constexpr (SRC == THB_DT_F32) {
+        const float* p = static_cast<const float*>(src) + e;
+        const uint4 a = ld_stream16(p), b = ld_stream16(p + 4);
+        out.x = conv32<KV>(a.x) | (conv32<KV>(a.y) << 16);
+        out.y = conv32<KV>(a.z) | (conv32<KV>(a.w) << 16);
+        out.z = conv32<KV>(b.x) | (conv32<KV>(b.y) << 16);
+        out.w = conv32<KV>(b.z) | (conv32<KV>(b.w) << 16);
+    } else {
+        const uint4 a = ld_stream16(static_cast<const uint16_t*>(src) + e);
+        auto c2 = [](uint32_t w) { return conv16<SRC, KV>(w & 0xffffu) | (conv16<SRC, KV>(w >> 16) << 16); };
+        out.x = c2(a.x);
+        out.y = c2(a.y);
+        out.z = c2(a.z);
+        out.w = c2(a.w);
+    }
+    return out;
+}
+
+struct StoreArgs {
+    const void* k_src;
+    const void* v_src;
+    uint16_t* k;
+    uint16_t* v;
+    const uint32_t* meta;   // row meta at the first row of the call
+    const uint32_t* table;  // [seqs * max_pages]
+    uint64_t plane;         // elements per head plane
+    uint32_t max_pages, page_shift, head_dim, chunks;  // chunks = kv_heads * head_dim / 8
+};
+
+// kv_store.wgsl:24-46 with one lane per 8 elements.  Grid: (ceil(2 *
+// chunks / 256), m); lanes [0, chunks) write K, [chunks, 2 * chunks) V.
+template <uint32_t SRC, uint32_t KV>
+__global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
+    uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= 2 * a.chunks) return;
+    const uint32_t row = blockIdx.y;
+    const bool is_v = c >= a.chunks;
+    if (is_v) c -= a.chunks;
+    const uint32_t pos = a.meta[8 * row], seq = a.meta[8 * row + 1];
+    const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (pos >> a.page_shift)];
+    const uint64_t slot = (static_cast<uint64_t>(page) << a.page_shift) | (pos & ((1u << a.page_shift) - 1u));
+    const uint32_t cph = a.head_dim >> 3;
+    const uint32_t h = c / cph, d = (c - h * cph) << 3;
+    const uint64_t src_e = (static_cast<uint64_t>(row) * a.chunks + c) << 3;
+    const uint4 w = load_encode8<SRC, KV>(is_v ? a.v_src : a.k_src, src_e);
+    uint16_t* dst = (is_v ? a.v : a.k) + h * a.plane + slot * a.head_dim + d;
+    *reinterpret_cast<uint4*>(dst) = w;
+}
+
+struct GatherArgs {
+    uint16_t* k;
+    uint16_t* v;
+    uint16_t* k_flat;  // [kv_heads, n, head_dim]
+    uint16_t* v_flat;
+    const uint32_t* table_row;  // the sequence's block-table row
+    uint64_t plane;
+    uint32_t page_shift, head_dim, n, t0, cpt;  // cpt = chunks per token = kv_heads * head_dim / 8
+};
+
+// Gather (TO_FLAT) or scatter (!TO_FLAT) of tokens [t0, t0 + n) of one
+// sequence.  Grid: (ceil(n * cpt / 256), 2); y selects K or V.
+template <bool TO_FLAT>
+__global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
+    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (c >= static_cast<uint64_t>(a.n) * a.cpt) return;
+    const uint32_t t = static_cast<uint32_t>(c / a.cpt);
+    const uint32_t r = static_cast<uint32_t>(c - static_cast<uint64_t>(t) * a.cpt);
+    const uint32_t cph = a.head_dim >> 3;
+    const uint32_t h = r / cph, d = (r - h * cph) << 3;
+    const uint32_t pos = a.t0 + t;
+    const uint32_t page = a.table_row[pos >> a.page_shift];
+    const uint64_t slot = (static_cast<uint64_t>(page) << a.page_shift) | (pos & ((1u << a.page_shift) - 1u));
+    uint16_t* paged = (blockIdx.y ? a.v : a.k) + h * a.plane + slot * a.head_dim + d;
+    uint16_t* flat = (blockIdx.y ? a.v_flat : a.k_flat) + (static_cast<uint64_t>(h) * a.n + t) * a.head_dim + d;
+    if constexpr (TO_FLAT)
+        *reinterpret_cast<uint4*>(flat) = *reinterpret_cast<const uint4*>(paged);
+    else
+        *reinterpret_cast<uint4*>(paged) = *reinterpret_cast<const uint4*>(flat);
+}
+
+struct CopyArgs {
+    uint8_t* mem;
+    const DevLayer* layers;
+    const uint32_t* triples;  // (src_page, dst_page, tokens)
+    uint64_t pool_len;
+    uint32_t kv_heads, page_len;
+};
+
+// Page copy for every layer, K and V, every head.  Grid: (ceil(page_len *
+// max_head_dim / 8 / 256), n_triples, layers * 2 * kv_heads).
+__global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
+    const uint32_t z = blockIdx.z;
+    const uint32_t h = z % a.kv_heads;
+    const uint32_t which = (z / a.kv_heads) & 1u;
+    const uint32_t layer = z / (2 * a.kv_heads);
+    const DevLayer L = a.layers[layer];
+    const uint32_t src = a.triples[3 * blockIdx.y], dst = a.triples[3 * blockIdx.y + 1];
+    const uint32_t ntok = a.triples[3 * blockIdx.y + 2];
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (static_cast<uint64_t>(c) * 8 >= static_cast<uint64_t>(ntok) * L.head_dim) return;
+    uint16_t* base = reinterpret_cast<uint16_t*>(a.mem + (which ? L.v_off : L.k_off)) +
+                     static_cast<uint64_t>(h) * a.pool_len * L.head_dim;
+    const uint64_t off = static_cast<uint64_t>(c) * 8;
+    const uint4 w = *reinterpret_cast<const uint4*>(base + static_cast<uint64_t>(src) * a.page_len * L.head_dim + off);
+    *reinterpret_cast<uint4*>(base + static_cast<uint64_t>(dst) * a.page_len * L.head_dim + off) = w;
+}
+
+template <uint32_t SRC>
+void launch_store(uint32_t kv, dim3 grid, const StoreArgs& a, hipStream_t s) {
+    if (kv == THB_KV_F16_RNE)
+        hipLaunchKernelGGL((kv_store_kernel<SRC, THB_KV_F16_RNE>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((kv_store_kernel<SRC, THB_KV_BF16_TRUNC>), grid, dim3(256), 0, s, a);
+}
+
+int check_layer(const thb_pool* p, uint32_t layer) {
+    if (layer >= p->layers)
+        return fail(THB_ERR_INVALID, "layer " + std::to_string(layer) + " out of range (" +
+                                         std::to_string(p->layers) + " layers)");
+    return THB_OK;
+}
+
+// Host-side check that tokens [t0, t0 + n) of seq have pages.
+int check_cover(const thb_pool* p, uint32_t seq, uint64_t end) {
+    const Arena& a = p->arena.a;
+    if (seq >= a.seqs())
+        return fail(THB_ERR_INVALID, "sequence " + std::to_string(seq) + " out of range (" +
+                                         std::to_string(a.seqs()) + " sequences)");
+    if (!a.covers(seq, static_cast<uint32_t>(std::min<uint64_t>(end, 0xFFFFFFFFu))) || end > 0xFFFFFFFFull)
+        return fail(THB_ERR_MODEL, "pages must cover the chunk: sequence " + std::to_string(seq) + " holds " +
+                                       std::to_string(a.table_of(seq).size() * a.page_len()) + " slots, needs " +
+                                       std::to_string(end));
+    return THB_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+void launch_block_copy(thb_pool* p, const uint32_t* triples_dev, uint32_t n, uint32_t max_tokens,
+                       hipStream_t stream) {
+    if (n == 0 || max_tokens == 0) return;
+    uint32_t max_hd = 0;
+    for (const auto& g : p->geom) max_hd = std::max(max_hd, g.head_dim);
+    CopyArgs a{p->mem, static_cast<const DevLayer*>(p->geom_buf.get()), triples_dev,
+               static_cast<uint64_t>(p->arena.a.pages()) * p->page_len, p->kv_heads, p->page_len};
+    const uint32_t chunks = (max_tokens * max_hd / 8 + 255) / 256;
+    const uint32_t planes = p->layers * 2 * p->kv_heads;
+    if (planes > kMaxGridY) throw HipError{hipErrorInvalidConfiguration, "block copy: layers*2*kv_heads > 65535"};
+    for (uint32_t i0 = 0; i0 < n; i0 += kMaxGridY) {
+        CopyArgs b = a;
+        b.triples = triples_dev + 3 * static_cast<size_t>(i0);
+        hipLaunchKernelGGL(block_copy_kernel, dim3(chunks, std::min(kMaxGridY, n - i0), planes), dim3(256), 0, stream,
+                           b);
+        THB_HIP(hipGetLastError());
+    }
+}
+
+}  // namespace thb
+
+using namespace thb;
+
+extern "C" {
+
+int thb_kv_store(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src, uint32_t src_dtype,
+                 const thb_rows* rows, uint32_t row_off, uint32_t m, void* stream) {
+    if (!pool || !rows) return fail(THB_ERR_INVALID, "null pool or rows");
+    if (int rc = check_layer(pool, layer)) return rc;
+    if (m == 0) return THB_OK;
+    if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
+    if (src_dtype > THB_DT_BF16) return fail(THB_ERR_INVALID, "unknown src_dtype " + std::to_string(src_dtype));
+    if (!aligned16(k_src) || !aligned16(v_src)) return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
+    if (static_cast<uint64_t>(row_off) + m > rows->m)
+        return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(rows->m) + " rows, call needs " +
+                                         std::to_string(static_cast<uint64_t>(row_off) + m));
+    for (uint32_t r = row_off; r < row_off + m; r++) {
+        uint32_t pos = rows->host[8 * r], seq = rows->host[8 * r + 1];
+        if (int rc = check_cover(pool, seq, static_cast<uint64_t>(pos) + 1)) return rc;
+    }
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        const LayerGeom& g = pool->geom[layer];
+        StoreArgs a;
+        a.k_src = k_src;
+        a.v_src = v_src;
+        a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
+        a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
+        a.meta = rows->dev + 8 * static_cast<size_t>(row_off);
+        a.table = pool->table_dev;
+        a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * g.head_dim;
+        a.max_pages = pool->arena.a.max_pages();
+        a.page_shift = pool->page_shift;
+        a.head_dim = g.head_dim;
+        a.chunks = pool->kv_heads * g.head_dim / 8;
+        const size_t esize = src_dtype == THB_DT_F32 ? 4 : 2;
+        for (uint32_t r0 = 0; r0 < m; r0 += kMaxGridY) {  // grid.y limit
+            const uint32_t n = std::min(kMaxGridY, m - r0);
+            StoreArgs b = a;
+            b.meta = a.meta + 8 * static_cast<size_t>(r0);
+            b.k_src = static_cast<const uint8_t*>(k_src) + static_cast<size_t>(r0) * a.chunks * 8 * esize;
+            b.v_src = static_cast<const uint8_t*>(v_src) + static_cast<size_t>(r0) * a.chunks * 8 * esize;
+            dim3 grid((2 * a.chunks + 255) / 256, n);
+            switch (src_dtype) {
+                case THB_DT_F32: launch_store<THB_DT_F32>(pool->kv_dtype, grid, b, s); break;
+                case THB_DT_F16: launch_store<THB_DT_F16>(pool->kv_dtype, grid, b, s); break;
+                default: launch_store<THB_DT_BF16>(pool->kv_dtype, grid, b, s); break;
+            }
+            THB_HIP(hipGetLastError());
+        }
+        return THB_OK;
+    });
+}
+
+static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uint32_t n, void* k, void* v,
+                         void* stream, bool to_flat) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (int rc = check_layer(pool, layer)) return rc;
+    if (n == 0) return THB_OK;
+    if (!k || !v) return fail(THB_ERR_INVALID, "null buffer");
+    if (!aligned16(k) || !aligned16(v)) return fail(THB_ERR_INVALID, "buffers must be 16-byte aligned");
+    if (int rc = check_cover(pool, seq, static_cast<uint64_t>(t0) + n)) return rc;
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        const LayerGeom& g = pool->geom[layer];
+        GatherArgs a;
+        a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
+        a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
+        a.k_flat = static_cast<uint16_t*>(k);
+        a.v_flat = static_cast<uint16_t*>(v);
+        a.table_row = pool->table_dev + static_cast<size_t>(seq) * pool->arena.a.max_pages();
+        a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * g.head_dim;
+        a.page_shift = pool->page_shift;
+        a.head_dim = g.head_dim;
+        a.n = n;
+        a.t0 = t0;
+        a.cpt = pool->kv_heads * g.head_dim / 8;
+        const uint64_t total = static_cast<uint64_t>(n) * a.cpt;
+        dim3 grid(static_cast<uint32_t>((total + 255) / 256), 2);
+        if (to_flat)
+            hipLaunchKernelGGL(gather_kernel<true>, grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(gather_kernel<false>, grid, dim3(256), 0, s, a);
+        THB_HIP(hipGetLastError());
+        return THB_OK;
+    });
+}
+
+int thb_kv_gather(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uint32_t n, void* k_dst, void* v_dst,
+                  void* stream) {
+    return gather_common(pool, layer, seq, t0, n, k_dst, v_dst, stream, true);
+}
+
+int thb_kv_scatter(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uint32_t n, const void* k_src,
+                   const void* v_src, void* stream) {
+    return gather_common(pool, layer, seq, t0, n, const_cast<void*>(k_src), const_cast<void*>(v_src), stream, false);
+}
+
+int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* stream) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (n == 0) return THB_OK;
+    if (!triples) return fail(THB_ERR_INVALID, "triples is null");
+    const uint32_t pages = pool->arena.a.pages();
+    uint32_t max_tok = 0;
+    std::vector<uint32_t> seen;
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t s = triples[3 * i], d = triples[3 * i + 1], t = triples[3 * i + 2];
+        if (s >= pages || d >= pages)
+            return fail(THB_ERR_INVALID, "page copy " + std::to_string(s) + " -> " + std::to_string(d) +
+                                             " outside the pool of " + std::to_string(pages) + " pages");
+        if (t > pool->page_len)
+            return fail(THB_ERR_INVALID, "page copy of " + std::to_string(t) + " tokens exceeds page_len " +
+                                             std::to_string(pool->page_len));
+        max_tok = std::max(max_tok, t);
+        seen.push_back(s);
+        seen.push_back(d);
+    }
+    std::vector<uint32_t> sorted = seen;
+    std::sort(sorted.begin(), sorted.end());
+    for (size_t i = 1; i < sorted.size(); i++)
+        if (sorted[i] == sorted[i - 1])
+            return fail(THB_ERR_INVALID, "page " + std::to_string(sorted[i]) + " appears twice in one block copy");
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        void* dev = pool->copy_buf.reserve(static_cast<size_t>(n) * 12, false);
+        pool->stager.upload(dev, triples, static_cast<size_t>(n) * 12, s);
+        launch_block_copy(pool, static_cast<const uint32_t*>(dev), n, max_tok, s);
+        return THB_OK;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,458 @@
+// C ABI of the host allocator, the device pool and the row metadata.
+//
+// Device layout: one allocation holds, for every layer, K then V, each
+// [kv_heads, pool_len, head_dim] 16-bit words (the KvPool layout,
+// reference crates/thuban_model/src/pool.rs:131-153), every plane aligned
+// to 256 bytes.  The block table [seqs * max_pages] u32 lives in its own
+// allocation and is shared by all layers.
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <string>
+
+#include "pool.hpp"
+
+namespace thb {
+
+static thread_local std::string g_error;
+static std::atomic<uint64_t> g_version{0};
+
+uint64_t next_version() { return ++g_version; }
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+void clear_error() { g_error.clear(); }
+
+Stager::~Stager() {
+    for (auto& s : slots_) {
+        if (s.done) {
+            (void)hipEventSynchronize(s.done);
+            (void)hipEventDestroy(s.done);
+        }
+        if (s.host) (void)hipHostFree(s.host);
+    }
+}
+
+void Stager::upload(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return;
+    Slot& s = slots_[next_];
+    next_ = (next_ + 1) % kSlots;
+    if (s.pending) {
+        THB_HIP(hipEventSynchronize(s.done));
+        s.pending = false;
+    }
+    if (s.cap < bytes) {
+        if (s.host) THB_HIP(hipHostFree(s.host));
+        s.host = nullptr;
+        size_t cap = std::max<size_t>(bytes, 4096);
+        THB_HIP(hipHostMalloc(&s.host, cap, hipHostMallocDefault));
+        s.cap = cap;
+    }
+    if (!s.done) THB_HIP(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
+    std::memcpy(s.host, src, bytes);
+    THB_HIP(hipMemcpyAsync(dst, s.host, bytes, hipMemcpyHostToDevice, stream));
+    THB_HIP(hipEventRecord(s.done, stream));
+    s.pending = true;
+}
+
+DevBuf::~DevBuf() {
+    if (ptr_) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ptr_);
+    }
+}
+
+void* DevBuf::reserve(size_t bytes, bool zero) {
+    if (bytes <= cap_) return ptr_;
+    size_t cap = std::max<size_t>(bytes, cap_ * 2);
+    cap = (cap + 255) & ~size_t(255);
+    if (ptr_) {
+        // The old buffer may still be read by queued kernels.
+        THB_HIP(hipDeviceSynchronize());
+        THB_HIP(hipFree(ptr_));
+        ptr_ = nullptr;
+        cap_ = 0;
+    }
+    THB_HIP(hipMalloc(&ptr_, cap));
+    if (zero) THB_HIP(hipMemset(ptr_, 0, cap));
+    cap_ = cap;
+    return ptr_;
+}
+
+// Splits the pending copies into batches in which no page is both read and
+// written, uploads each batch and launches the copy kernel for it.
+static void run_copies(thb_pool* p, hipStream_t stream) {
+    auto& copies = p->arena.a.copies();
+    size_t i = 0;
+    std::vector<uint32_t> batch;
+    std::vector<uint32_t> touched;
+    while (i < copies.size()) {
+        batch.clear();
+        touched.clear();
+        uint32_t max_tok = 0;
+        for (; i < copies.size(); i++) {
+            const PageCopy& c = copies[i];
+            bool clash = std::find(touched.begin(), touched.end(), c.src) != touched.end() ||
+                         std::find(touched.begin(), touched.end(), c.dst) != touched.end();
+            if (clash) break;
+            batch.insert(batch.end(), {c.src, c.dst, c.tokens});
+            touched.push_back(c.src);
+            touched.push_back(c.dst);
+            max_tok = std::max(max_tok, c.tokens);
+        }
+        uint32_t n = static_cast<uint32_t>(batch.size() / 3);
+        void* dev = p->copy_buf.reserve(batch.size() * 4, false);
+        p->stager.upload(dev, batch.data(), batch.size() * 4, stream);
+        launch_block_copy(p, static_cast<const uint32_t*>(dev), n, max_tok, stream);
+    }
+    copies.clear();
+}
+
+void pool_flush(thb_pool* p, hipStream_t stream) {
+    Arena& a = p->arena.a;
+    if (!a.copies().empty()) run_copies(p, stream);
+    if (!a.any_dirty()) return;
+    const auto& dirty = a.dirty();
+    uint32_t lo = 0, hi = 0;
+    bool first = true;
+    for (uint32_t s = 0; s < a.seqs(); s++)
+        if (dirty[s]) {
+            if (first) lo = s;
+            hi = s + 1;
+            first = false;
+        }
+    const uint32_t mp = a.max_pages();
+    for (uint32_t s = lo; s < hi; s++) {
+        uint32_t* row = p->table_host.data() + static_cast<size_t>(s) * mp;
+        const auto& t = a.table_of(s);
+        std::fill(row, row + mp, THB_NO_PAGE);
+        std::copy(t.begin(), t.end(), row);
+    }
+    p->stager.upload(p->table_dev + static_cast<size_t>(lo) * mp, p->table_host.data() + static_cast<size_t>(lo) * mp,
+                     static_cast<size_t>(hi - lo) * mp * 4, stream);
+    a.clear_dirty();
+}
+
+}  // namespace thb
+
+using namespace thb;
+
+extern "C" {
+
+const char* thb_last_error(void) { return g_error.c_str(); }
+
+uint32_t thb_abi_version(void) { return THB_ABI_VERSION; }
+
+int thb_check_head_dim(uint32_t head_dim) {
+    // ops/attn.rs:83-90
+    if (head_dim < 64 || head_dim > 512)
+        return fail(THB_ERR_CONFIG, "head_dim " + std::to_string(head_dim) + " outside [64, 512]");
+    if (head_dim % 8 != 0)
+        return fail(THB_ERR_CONFIG, "head_dim " + std::to_string(head_dim) + " is not a multiple of 8");
+    return THB_OK;
+}
+
+// ---------------------------------------------------------------- arena
+static int check_seq(const Arena& a, uint32_t seq) {
+    if (seq >= a.seqs())
+        return fail(THB_ERR_INVALID, "sequence " + std::to_string(seq) + " out of range (" +
+                                         std::to_string(a.seqs()) + " sequences)");
+    return THB_OK;
+}
+
+int thb_arena_create(const uint32_t* seq_lens, uint32_t seqs, int64_t pages, uint32_t page_len, thb_arena** out) {
+    if (!out) return fail(THB_ERR_INVALID, "out is null");
+    *out = nullptr;
+    auto* h = new (std::nothrow) thb_arena;
+    if (!h) return fail(THB_ERR_GPU, "host out of memory");
+    std::string err = Arena::create(seq_lens, seqs, pages, page_len, h->a);
+    if (!err.empty()) {
+        delete h;
+        return fail(THB_ERR_MODEL, err);
+    }
+    *out = h;
+    return THB_OK;
+}
+
+void thb_arena_destroy(thb_arena* arena) { delete arena; }
+
+int thb_arena_alloc(thb_arena* arena, uint32_t seq, uint32_t pos, uint32_t tokens) {
+    if (!arena) return fail(THB_ERR_INVALID, "arena is null");
+    if (int rc = check_seq(arena->a, seq)) return rc;
+    std::string err = arena->a.alloc(seq, pos, tokens);
+    return err.empty() ? THB_OK : fail(THB_ERR_MODEL, err);
+}
+
+int thb_arena_free_seq(thb_arena* arena, uint32_t seq) {
+    if (!arena) return fail(THB_ERR_INVALID, "arena is null");
+    if (int rc = check_seq(arena->a, seq)) return rc;
+    arena->a.free_seq(seq);
+    return THB_OK;
+}
+
+int thb_arena_truncate(thb_arena* arena, uint32_t seq, uint32_t keep_tokens) {
+    if (!arena) return fail(THB_ERR_INVALID, "arena is null");
+    if (int rc = check_seq(arena->a, seq)) return rc;
+    arena->a.truncate(seq, keep_tokens);
+    return THB_OK;
+}
+
+int thb_arena_covers(const thb_arena* arena, uint32_t seq, uint32_t tokens) {
+    if (!arena) return fail(THB_ERR_INVALID, "arena is null");
+    if (int rc = check_seq(arena->a, seq)) return rc;
+    return arena->a.covers(seq, tokens) ? 1 : 0;
+}
+
+int thb_arena_fork(thb_arena* arena, uint32_t src, uint32_t dst, uint32_t tokens) {
+    if (!arena) return fail(THB_ERR_INVALID, "arena is null");
+    if (int rc = check_seq(arena->a, src)) return rc;
+    if (int rc = check_seq(arena->a, dst)) return rc;
+    if (src == dst) return fail(THB_ERR_INVALID, "fork source and target are the same sequence");
+    std::string err = arena->a.fork(src, dst, tokens);
+    return err.empty() ? THB_OK : fail(THB_ERR_MODEL, err);
+}
+
+int thb_arena_table(const thb_arena* arena, uint32_t* out, size_t n) {
+    if (!arena || !out) return fail(THB_ERR_INVALID, "null argument");
+    size_t want = static_cast<size_t>(arena->a.seqs()) * arena->a.max_pages();
+    if (n != want)
+        return fail(THB_ERR_INVALID, "block table must cover every sequence: " + std::to_string(n) +
+                                         " != " + std::to_string(want));
+    arena->a.table(out);
+    return THB_OK;
+}
+
+int thb_arena_table_of(const thb_arena* arena, uint32_t seq, uint32_t* out, size_t cap, uint32_t* len) {
+    if (!arena) return fail(THB_ERR_INVALID, "arena is null");
+    if (int rc = check_seq(arena->a, seq)) return rc;
+    const auto& t = arena->a.table_of(seq);
+    if (len) *len = static_cast<uint32_t>(t.size());
+    if (out) std::copy(t.begin(), t.begin() + std::min(cap, t.size()), out);
+    return THB_OK;
+}
+
+int thb_arena_seq_len(const thb_arena* arena, uint32_t seq, uint32_t* len) {
+    if (!arena || !len) return fail(THB_ERR_INVALID, "null argument");
+    if (int rc = check_seq(arena->a, seq)) return rc;
+    *len = arena->a.seq_len(seq);
+    return THB_OK;
+}
+
+int thb_arena_info_get(const thb_arena* arena, thb_arena_info* info) {
+    if (!arena || !info) return fail(THB_ERR_INVALID, "null argument");
+    info->pages = arena->a.pages();
+    info->used = arena->a.used();
+    info->max_pages = arena->a.max_pages();
+    info->seqs = arena->a.seqs();
+    info->page_len = arena->a.page_len();
+    info->pending_copies = static_cast<uint32_t>(const_cast<Arena&>(arena->a).copies().size());
+    return THB_OK;
+}
+
+int thb_arena_take_copies(thb_arena* arena, uint32_t* triples, size_t cap, uint32_t* n) {
+    if (!arena || !n) return fail(THB_ERR_INVALID, "null argument");
+    auto& c = arena->a.copies();
+    *n = static_cast<uint32_t>(c.size());
+    if (c.size() > cap) return fail(THB_ERR_INVALID, "copy buffer holds " + std::to_string(cap) + " < " +
+                                                         std::to_string(c.size()) + " triples");
+    for (size_t i = 0; i < c.size(); i++) {
+        triples[3 * i] = c[i].src;
+        triples[3 * i + 1] = c[i].dst;
+        triples[3 * i + 2] = c[i].tokens;
+    }
+    c.clear();
+    return THB_OK;
+}
+
+// ----------------------------------------------------------------- pool
+int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
+    if (!d || !out) return fail(THB_ERR_INVALID, "null argument");
+    *out = nullptr;
+    if (d->layers == 0) return fail(THB_ERR_CONFIG, "pool needs at least one layer");
+    if (d->kv_heads == 0) return fail(THB_ERR_CONFIG, "kv_heads must be positive");
+    if (d->kv_dtype != THB_KV_BF16_TRUNC && d->kv_dtype != THB_KV_F16_RNE)
+        return fail(THB_ERR_CONFIG, "unknown kv_dtype " + std::to_string(d->kv_dtype));
+    if (d->page_len < 8 || d->page_len > 256 || (d->page_len & (d->page_len - 1)))
+        return fail(THB_ERR_CONFIG, "page_len " + std::to_string(d->page_len) + " must be a power of two in [8, 256]");
+    uint32_t part = d->part_len ? d->part_len : 512;
+    if (part % 128 != 0 || part % d->page_len != 0 || part > 8192)
+        return fail(THB_ERR_CONFIG, "part_len " + std::to_string(part) +
+                                        " must be a multiple of 128 and of page_len, at most 8192");
+    for (uint32_t l = 0; l < d->layers; l++) {
+        uint32_t hd = d->head_dims ? d->head_dims[l] : d->head_dim;
+        if (int rc = thb_check_head_dim(hd)) return rc;
+    }
+    return guarded([&]() -> int {
+        auto p = std::make_unique<thb_pool>();
+        std::string err = Arena::create(d->seq_lens, d->seqs, d->pages, d->page_len, p->arena.a);
+        if (!err.empty()) return fail(THB_ERR_MODEL, err);
+        p->layers = d->layers;
+        p->kv_heads = d->kv_heads;
+        p->page_len = d->page_len;
+        p->page_shift = __builtin_ctz(d->page_len);
+        p->kv_dtype = d->kv_dtype;
+        p->part_len = part;
+        const uint64_t pool_len = static_cast<uint64_t>(p->arena.a.pages()) * d->page_len;
+        if (pool_len >= (1ull << 32)) return fail(THB_ERR_CONFIG, "pages * page_len must stay below 2^32 slots");
+        uint64_t off = 0;
+        for (uint32_t l = 0; l < d->layers; l++) {
+            uint32_t hd = d->head_dims ? d->head_dims[l] : d->head_dim;
+            uint64_t plane = (static_cast<uint64_t>(d->kv_heads) * pool_len * hd * 2 + 255) & ~uint64_t(255);
+            p->geom.push_back({hd, off, off + plane});
+            off += 2 * plane;
+        }
+        p->mem_bytes = off;
+        THB_HIP(hipGetDevice(&p->device));
+        if (d->arena_dev) {
+            if (d->arena_bytes < off)
+                return fail(THB_ERR_CONFIG, "external arena holds " + std::to_string(d->arena_bytes) +
+                                                " bytes, pool needs " + std::to_string(off));
+            if (reinterpret_cast<uintptr_t>(d->arena_dev) % 256 != 0)
+                return fail(THB_ERR_CONFIG, "external arena must be 256-byte aligned");
+            p->mem = static_cast<uint8_t*>(d->arena_dev);
+            p->owns_mem = false;
+        } else {
+            hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->mem), off);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                return fail(THB_ERR_GPU, "KV pool of " + std::to_string(off) + " bytes does not fit: " +
+                                             hipGetErrorString(e));
+            }
+            p->owns_mem = true;
+        }
+        THB_HIP(hipMemset(p->mem, 0, off));
+        const size_t tbl = static_cast<size_t>(p->arena.a.seqs()) * p->arena.a.max_pages();
+        THB_HIP(hipMalloc(reinterpret_cast<void**>(&p->table_dev), tbl * 4));
+        THB_HIP(hipMemset(p->table_dev, 0xFF, tbl * 4));
+        p->table_host.assign(tbl, THB_NO_PAGE);
+        std::vector<DevLayer> dl;
+        for (const auto& g : p->geom) dl.push_back({g.k_off, g.v_off, g.head_dim, 0});
+        void* gd = p->geom_buf.reserve(dl.size() * sizeof(DevLayer), false);
+        THB_HIP(hipMemcpy(gd, dl.data(), dl.size() * sizeof(DevLayer), hipMemcpyHostToDevice));
+        p->arena.a.clear_dirty();
+        THB_HIP(hipDeviceSynchronize());
+        *out = p.release();
+        return THB_OK;
+    });
+}
+
+void thb_pool_destroy(thb_pool* pool) {
+    if (!pool) return;
+    (void)hipDeviceSynchronize();
+    if (pool->owns_mem && pool->mem) (void)hipFree(pool->mem);
+    if (pool->table_dev) (void)hipFree(pool->table_dev);
+    delete pool;
+}
+
+int thb_pool_alloc(thb_pool* pool, uint32_t seq, uint32_t pos, uint32_t tokens) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    return thb_arena_alloc(&pool->arena, seq, pos, tokens);
+}
+
+int thb_pool_free_seq(thb_pool* pool, uint32_t seq) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    return thb_arena_free_seq(&pool->arena, seq);
+}
+
+int thb_pool_truncate(thb_pool* pool, uint32_t seq, uint32_t keep_tokens) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    return thb_arena_truncate(&pool->arena, seq, keep_tokens);
+}
+
+int thb_pool_fork(thb_pool* pool, uint32_t src, uint32_t dst, uint32_t tokens) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    return thb_arena_fork(&pool->arena, src, dst, tokens);
+}
+
+int thb_pool_sync(thb_pool* pool, void* stream) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    return guarded([&]() -> int {
+        pool_flush(pool, as_stream(stream));
+        return THB_OK;
+    });
+}
+
+const thb_arena* thb_pool_arena(const thb_pool* pool) { return pool ? &pool->arena : nullptr; }
+
+int thb_pool_layer(const thb_pool* pool, uint32_t layer, void** k_dev, void** v_dev, thb_layer_info* info) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (layer >= pool->layers)
+        return fail(THB_ERR_INVALID, "layer " + std::to_string(layer) + " out of range (" +
+                                         std::to_string(pool->layers) + " layers)");
+    const LayerGeom& g = pool->geom[layer];
+    if (k_dev) *k_dev = pool->mem + g.k_off;
+    if (v_dev) *v_dev = pool->mem + g.v_off;
+    if (info) {
+        info->kv_heads = pool->kv_heads;
+        info->head_dim = g.head_dim;
+        info->pool_len = pool->arena.a.pages() * pool->page_len;
+        info->max_pages = pool->arena.a.max_pages();
+        info->page_len = pool->page_len;
+        info->kv_dtype = pool->kv_dtype;
+        info->plane_elems = static_cast<uint64_t>(info->pool_len) * g.head_dim;
+    }
+    return THB_OK;
+}
+
+int thb_pool_block_table(const thb_pool* pool, const uint32_t** table_dev) {
+    if (!pool || !table_dev) return fail(THB_ERR_INVALID, "null argument");
+    *table_dev = pool->table_dev;
+    return THB_OK;
+}
+
+int thb_pool_memory(const thb_pool* pool, void** base_dev, uint64_t* bytes) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (base_dev) *base_dev = pool->mem;
+    if (bytes) *bytes = pool->mem_bytes;
+    return THB_OK;
+}
+
+// ----------------------------------------------------------------- rows
+int thb_rows_create(uint32_t max_m, thb_rows** out) {
+    if (!out) return fail(THB_ERR_INVALID, "out is null");
+    *out = nullptr;
+    if (max_m == 0) return fail(THB_ERR_INVALID, "max_m must be positive");
+    return guarded([&]() -> int {
+        auto r = std::make_unique<thb_rows>();
+        r->max_m = max_m;
+        THB_HIP(hipMalloc(reinterpret_cast<void**>(&r->dev), static_cast<size_t>(max_m) * 32));
+        THB_HIP(hipMemset(r->dev, 0, static_cast<size_t>(max_m) * 32));
+        r->host.assign(static_cast<size_t>(max_m) * 8, 0);
+        *out = r.release();
+        return THB_OK;
+    });
+}
+
+void thb_rows_destroy(thb_rows* rows) {
+    if (!rows) return;
+    (void)hipDeviceSynchronize();
+    if (rows->dev) (void)hipFree(rows->dev);
+    delete rows;
+}
+
+int thb_rows_write(thb_rows* rows, const uint32_t* positions, const uint32_t* seqs, uint32_t m, void* stream) {
+    // rows.rs:19-30
+    if (!rows || (m && (!positions || !seqs))) return fail(THB_ERR_INVALID, "null argument");
+    if (m > rows->max_m)
+        return fail(THB_ERR_INVALID, "row meta arrays must cover the chunk size: " + std::to_string(m) + " > " +
+                                         std::to_string(rows->max_m));
+    return guarded([&]() -> int {
+        std::fill(rows->host.begin(), rows->host.end(), 0u);
+        for (uint32_t i = 0; i < m; i++) {
+            rows->host[8 * i] = positions[i];
+            rows->host[8 * i + 1] = seqs[i];
+        }
+        rows->m = m;
+        rows->version = next_version();
+        rows->stager.upload(rows->dev, rows->host.data(), static_cast<size_t>(std::max<uint32_t>(m, 1)) * 32,
+                            as_stream(stream));
+        return THB_OK;
+    });
+}
+
+const uint32_t* thb_rows_device(const thb_rows* rows) { return rows ? rows->dev : nullptr; }
+
+}  // extern "C"

@@ -1,0 +1,82 @@
+// Internal layout of the device pool and the row-meta object, shared by the
+// translation units of the HIP backend.
+#pragma once
+
+#include <array>
+#include <cstdint>
+#include <memory>
+#include <vector>
+
+#include "arena.hpp"
+#include "common.hpp"
+
+namespace thb {
+
+// Per-layer record the block-copy kernel reads on the device.
+struct DevLayer {
+    uint64_t k_off, v_off;  // byte offsets into the arena
+    uint32_t head_dim, pad;
+};
+
+struct LayerGeom {
+    uint32_t head_dim;
+    uint64_t k_off;  // byte offsets into the arena
+    uint64_t v_off;
+};
+
+// One cached attention launch plan (see attention.hip).
+struct AttnPlan {
+    // key
+    const void* rows = nullptr;
+    uint64_t rows_version = ~0ull;
+    uint64_t arena_version = ~0ull;
+    uint32_t row_off = 0, m = 0, seq = 0, causal = 0, window = 0, q_heads = 0, head_dim = 0;
+    uint32_t variant = 0;
+    // value
+    uint32_t n_groups = 0, n_items = 0;
+    uint32_t qv_max = 0;
+    DevBuf dev;  // [groups | items | row ranges]
+    uint64_t last_use = 0;
+};
+
+}  // namespace thb
+
+struct thb_arena {
+    thb::Arena a;
+};
+
+struct thb_rows {
+    uint32_t max_m = 0;
+    uint32_t m = 0;
+    uint32_t* dev = nullptr;          // 8 * max_m u32
+    std::vector<uint32_t> host;       // mirror of what was last uploaded
+    uint64_t version = 0;
+    thb::Stager stager;
+};
+
+struct thb_pool {
+    thb_arena arena;
+    uint32_t layers = 0, kv_heads = 0, page_len = 0, page_shift = 0, kv_dtype = 0, part_len = 512;
+    std::vector<thb::LayerGeom> geom;
+    uint8_t* mem = nullptr;  // device arena
+    uint64_t mem_bytes = 0;
+    bool owns_mem = false;
+    uint32_t* table_dev = nullptr;   // [seqs * max_pages]
+    std::vector<uint32_t> table_host;
+    thb::Stager stager;
+    thb::DevBuf copy_buf;            // copy triples
+    thb::DevBuf geom_buf;            // per-layer DevLayer records
+    thb::DevBuf partials;            // split-K partial results
+    thb::DevBuf counters;            // split-K arrival counters (self-resetting)
+    std::array<thb::AttnPlan, 4> plans;
+    uint64_t plan_clock = 0;
+    int device = 0;
+};
+
+namespace thb {
+// Uploads dirty block-table rows and executes pending page copies.
+void pool_flush(thb_pool* p, hipStream_t stream);
+// Launches the block-copy kernel for non-chaining triples already on device.
+void launch_block_copy(thb_pool* p, const uint32_t* triples_dev, uint32_t n, uint32_t max_tokens,
+                       hipStream_t stream);
+}  // namespace thb

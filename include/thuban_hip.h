@@ -1,0 +1,237 @@
+/*
+ * thuban_hip.h -- C ABI of the MI355X-native paged KV-cache path.
+ *
+ * Drop-in replacement for the paged-KV part of the reference engine
+ * (formetaohy/Flint, crate family "Thuban").  Citations are path:line in the
+ * reference tree.  Every entry point returns an int status (THB_OK == 0,
+ * negative on error) and leaves a reference-style message in
+ * thb_last_error() (thread-local), e.g. "KV arena exhausted: 3 pages
+ * requested, 1 free" or "context limit 32 reached" (pool.rs:49-59).
+ *
+ * Pointers named *_dev are device pointers; every other pointer is host
+ * memory.  `stream` is a hipStream_t passed as void* (NULL = the null
+ * stream).  Device work of one pool is ordered on the stream the caller
+ * passes; a pool, like the reference's Backend (thuban_backend/src/lib.rs
+ * :57-69), has one owner and is not thread-safe.
+ */
+#ifndef THUBAN_HIP_H
+#define THUBAN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ----------------------------------------------------------- conventions */
+
+/* Status codes.  THB_ERR_MODEL / THB_ERR_CONFIG / THB_ERR_GPU correspond to
+ * thuban_error::Error::{Model, Config, Gpu} (thuban_error/src/lib.rs:5-21). */
+#define THB_OK 0
+#define THB_ERR_MODEL (-1)
+#define THB_ERR_CONFIG (-2)
+#define THB_ERR_GPU (-3)
+#define THB_ERR_INVALID (-4)
+
+/* Element types of source / query / output buffers. */
+#define THB_DT_F32 0u
+#define THB_DT_F16 1u
+#define THB_DT_BF16 2u
+
+/* KV storage types.  BF16_TRUNC is the reference's storage: bf16 by
+ * truncating an f32 (kv_store.wgsl:20-22, thuban_num/src/lib.rs:66-68).
+ * F16_RNE is IEEE half with round-to-nearest-even (thuban_num lib.rs:25-60). */
+#define THB_KV_BF16_TRUNC 0u
+#define THB_KV_F16_RNE 1u
+
+/* Block-table sentinel for a missing page (u32::MAX, pool.rs:85-93). */
+#define THB_NO_PAGE 0xFFFFFFFFu
+/* thb_attn_spec.seq value that takes each row's sequence from row meta. */
+#define THB_SEQ_PER_ROW 0xFFFFFFFFu
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* thb_last_error(void);
+/* ABI revision of this header. */
+uint32_t thb_abi_version(void);
+#define THB_ABI_VERSION 1u
+
+/* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90):
+ * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]".  This backend also needs
+ * head_dim % 8 == 0 (16-byte vector lanes). */
+int thb_check_head_dim(uint32_t head_dim);
+
+/* ------------------------------------------------ host page allocator */
+
+/* KvArena (pool.rs:11-118) with the page length as a parameter (the
+ * reference fixes PAGE_LEN = 32, thuban_kernel/src/lib.rs:9) and an
+ * extension for shared pages: fork() shares full pages between sequences
+ * with reference counts, and alloc() copies a shared page before a write
+ * lands in it (copy-on-write).  Pure host code: usable without a GPU. */
+typedef struct thb_arena thb_arena;
+
+typedef struct thb_arena_info {
+    uint32_t pages;     /* KvArena::pages (pool.rs:95-97) */
+    uint32_t used;      /* KvArena::used (pool.rs:99-101) */
+    uint32_t max_pages; /* KvArena::max_pages (pool.rs:103-105) */
+    uint32_t seqs;      /* KvArena::seqs (pool.rs:107-109) */
+    uint32_t page_len;
+    uint32_t pending_copies; /* copy-on-write copies not yet executed */
+} thb_arena_info;
+
+/* KvArena::new (pool.rs:20-45).  pages < 0 means ArenaSpec.pages = None
+ * (sum of ceil(seq_len / page_len)).  page_len must be a power of two in
+ * [1, 256]. */
+int thb_arena_create(const uint32_t* seq_lens, uint32_t seqs, int64_t pages, uint32_t page_len,
+                     thb_arena** out);
+void thb_arena_destroy(thb_arena* arena);
+/* KvArena::alloc (pool.rs:47-65), plus copy-on-write of shared pages that
+ * [pos, pos+tokens) touches. */
+int thb_arena_alloc(thb_arena* arena, uint32_t seq, uint32_t pos, uint32_t tokens);
+/* KvArena::free_seq (pool.rs:67-71). */
+int thb_arena_free_seq(thb_arena* arena, uint32_t seq);
+/* KvArena::truncate (pool.rs:73-79). */
+int thb_arena_truncate(thb_arena* arena, uint32_t seq, uint32_t keep_tokens);
+/* KvArena::covers (pool.rs:81-83): 1 or 0, negative on error. */
+int thb_arena_covers(const thb_arena* arena, uint32_t seq, uint32_t tokens);
+/* No reference counterpart: dst (empty) shares src's pages holding tokens
+ * [0, tokens); a partial last page is copied so that both can append. */
+int thb_arena_fork(thb_arena* arena, uint32_t src, uint32_t dst, uint32_t tokens);
+/* KvArena::table (pool.rs:85-93): n must be seqs * max_pages. */
+int thb_arena_table(const thb_arena* arena, uint32_t* out, size_t n);
+/* KvArena::table_of (pool.rs:115-117): writes min(cap, len) entries. */
+int thb_arena_table_of(const thb_arena* arena, uint32_t seq, uint32_t* out, size_t cap, uint32_t* len);
+/* KvArena::seq_len (pool.rs:111-113). */
+int thb_arena_seq_len(const thb_arena* arena, uint32_t seq, uint32_t* len);
+int thb_arena_info_get(const thb_arena* arena, thb_arena_info* info);
+/* Moves the pending copy-on-write copies (src_page, dst_page, tokens) out of
+ * the arena; a device pool executes them itself before its next kernel. */
+int thb_arena_take_copies(thb_arena* arena, uint32_t* triples, size_t cap, uint32_t* n);
+
+/* ---------------------------------------------------------- device pool */
+
+/* One hipMalloc'd arena holding K and V of every layer, each layer laid out
+ * as KvPool allocates it: [kv_heads, pages * page_len, head_dim]
+ * (pool.rs:131-153), plus one device block table [seqs * max_pages] shared
+ * by all layers (the reference keeps a copy per layer, model.rs:413-418). */
+typedef struct thb_pool thb_pool;
+
+typedef struct thb_pool_desc {
+    uint32_t layers;
+    uint32_t kv_heads;
+    uint32_t head_dim;          /* used when head_dims == NULL */
+    const uint32_t* head_dims;  /* optional per-layer head_dim [layers] */
+    uint32_t page_len;          /* power of two, 8..256; 16 and 32 are tuned */
+    uint32_t kv_dtype;          /* THB_KV_* */
+    uint32_t seqs;
+    const uint32_t* seq_lens;   /* ArenaSpec.seq_lens [seqs] */
+    int64_t pages;              /* ArenaSpec.pages; < 0 = None */
+    uint32_t part_len;          /* split-K partition in tokens (0 = 512);
+                                   multiple of 128 and of page_len */
+    void* arena_dev;            /* optional caller-owned device memory */
+    uint64_t arena_bytes;       /* its size; 0 = let the pool hipMalloc */
+} thb_pool_desc;
+
+typedef struct thb_layer_info {
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t pool_len;          /* KvPool::capacity = pages * page_len */
+    uint32_t max_pages;
+    uint32_t page_len;
+    uint32_t kv_dtype;
+    uint64_t plane_elems;       /* elements per head plane = pool_len * head_dim */
+} thb_layer_info;
+
+/* KvArena::new + KvPool::new for every layer (pool.rs:20-45,131-153).  The
+ * memory is zero-filled, as Backend::zero_tensor does (lib.rs:192-206). */
+int thb_pool_create(const thb_pool_desc* desc, thb_pool** out);
+void thb_pool_destroy(thb_pool* pool);
+/* Page API of LanguageModel::{alloc,free,truncate}_pages (traits.rs:39-41,
+ * transformer/forward.rs:534-550).  Host-side; the device block table and
+ * any copy-on-write copies are pushed on the next device call (or by
+ * thb_pool_sync), replacing upload_tables (model.rs:413-418). */
+int thb_pool_alloc(thb_pool* pool, uint32_t seq, uint32_t pos, uint32_t tokens);
+int thb_pool_free_seq(thb_pool* pool, uint32_t seq);
+int thb_pool_truncate(thb_pool* pool, uint32_t seq, uint32_t keep_tokens);
+/* No reference counterpart: fork with block sharing + partial-page copy. */
+int thb_pool_fork(thb_pool* pool, uint32_t src, uint32_t dst, uint32_t tokens);
+/* Uploads dirty block-table rows and runs pending page copies on stream. */
+int thb_pool_sync(thb_pool* pool, void* stream);
+/* The pool's allocator (queries; mutate through thb_pool_* instead). */
+const thb_arena* thb_pool_arena(const thb_pool* pool);
+/* Device pointers of layer `layer`'s K and V planes (KvPool::k / ::v). */
+int thb_pool_layer(const thb_pool* pool, uint32_t layer, void** k_dev, void** v_dev, thb_layer_info* info);
+/* Device block table [seqs * max_pages] (KvPool::block_table). */
+int thb_pool_block_table(const thb_pool* pool, const uint32_t** table_dev);
+/* Whole arena: base pointer and size in bytes. */
+int thb_pool_memory(const thb_pool* pool, void** base_dev, uint64_t* bytes);
+
+/* -------------------------------------------------------------- row meta */
+
+/* Row metadata, rows::row_meta / write_row_meta (rows.rs:11-30): 8 u32 per
+ * row, [pos, seq, 0 x 6].  The object keeps a host mirror of what it last
+ * wrote so that attention can plan its launch without reading the GPU. */
+typedef struct thb_rows thb_rows;
+int thb_rows_create(uint32_t max_m, thb_rows** out);
+void thb_rows_destroy(thb_rows* rows);
+/* rows::write_row_meta: uploads rows [0, m) on stream. */
+int thb_rows_write(thb_rows* rows, const uint32_t* positions, const uint32_t* seqs, uint32_t m, void* stream);
+/* Device pointer of the 8 x max_m u32 buffer. */
+const uint32_t* thb_rows_device(const thb_rows* rows);
+
+/* --------------------------------------------------------------- kernels */
+
+/* ops::kv_store (ops/attn.rs:53-81) / kv_store.wgsl:24-46: for each row r of
+ * [row_off, row_off + m): slot = block_table[seq][pos / page_len] * page_len
+ * + pos % page_len, and K/V[h][slot][:] = encode(src[r - row_off][h][:]) for
+ * every KV head.  src_dtype is THB_DT_*; src is [m, kv_heads, head_dim],
+ * 16-byte aligned.  Bit-exact: bf16 truncation or f16 RNE as thuban_num. */
+int thb_kv_store(thb_pool* pool, uint32_t layer, const void* k_src_dev, const void* v_src_dev, uint32_t src_dtype,
+                 const thb_rows* rows, uint32_t row_off, uint32_t m, void* stream);
+
+/* ops::AttnSpec (ops/attn.rs:8-16) plus the extensions of this backend. */
+typedef struct thb_attn_spec {
+    uint32_t q_heads;  /* AttnSpec.q_heads; multiple of kv_heads */
+    uint32_t window;   /* AttnSpec.window; 0 = none (causal only) */
+    float scale;       /* AttnSpec.scale */
+    uint32_t m;        /* AttnSpec.m: rows in this call */
+    uint32_t causal;   /* AttnSpec.causal */
+    uint32_t seq;      /* AttnSpec.seq, or THB_SEQ_PER_ROW (batched rows) */
+    uint32_t row_off;  /* first row in the row meta (the reference binds a
+                          slice at row_off * 32 bytes, forward.rs:332) */
+    float softcap;     /* extension: 0 = off, else s = cap * tanh(s / cap) */
+    uint32_t q_dtype;  /* THB_DT_F32 (reference) or THB_DT_F16 */
+    uint32_t y_dtype;  /* THB_DT_F32 (reference) or THB_DT_F16 */
+} thb_attn_spec;
+
+/* ops::attn (ops/attn.rs:18-51) / attn.wgsl:53-365.  q, y: [m, q_heads,
+ * head_dim].  Key ranges per row follow attn.wgsl:78-88,169 exactly.  One
+ * launch covers every row (batched over sequences), as a split-K decode with
+ * a deterministic log-sum-exp merge: output is independent of physical page
+ * placement and of the other rows in the batch.  f32 accumulation; within
+ * 2e-3 of an exact softmax. */
+int thb_attn(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
+             const thb_rows* rows, void* stream);
+
+/* No reference counterpart.  Copies tokens [t0, t0 + n) of seq, layer
+ * `layer`, into contiguous k_dst/v_dst [kv_heads, n, head_dim] in the KV type
+ * (bit copy). */
+int thb_kv_gather(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uint32_t n, void* k_dst_dev,
+                  void* v_dst_dev, void* stream);
+
+/* No reference counterpart.  Inverse of thb_kv_gather: writes contiguous
+ * [kv_heads, n, head_dim] words (KV type) into tokens [t0, t0 + n) of seq. */
+int thb_kv_scatter(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uint32_t n, const void* k_src_dev,
+                   const void* v_src_dev, void* stream);
+
+/* No reference counterpart.  For each host triple (src_page, dst_page,
+ * tokens) copies slots [0, tokens) of src_page to dst_page, K and V, every
+ * head of every layer.  Triples must not chain (no page both a source and a
+ * destination). */
+int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THUBAN_HIP_H */

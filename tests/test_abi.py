@@ -1,0 +1,79 @@
+"""The C-ABI library loads and exports every symbol the header declares.
+CPU only: no compute entry point is called."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    with open(os.path.join(ROOT, "include", "thuban_hip.h")) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(thb_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_are_exported():
+    from flint_amd import _lib
+
+    lib = _lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    bound = {n for n, _, _ in _lib.SIGNATURES}
+    assert set(names) == bound, set(names) ^ bound
+
+
+def test_abi_version_and_struct_layouts(tmp_path):
+    """The ctypes mirrors of the header's structs match what a C compiler
+    lays out (size and every field offset)."""
+    import subprocess
+
+    from flint_amd import _lib
+
+    assert _lib.lib().thb_abi_version() == 1
+    structs = {"thb_pool_desc": _lib.PoolDesc, "thb_attn_spec": _lib.AttnSpecC,
+               "thb_layer_info": _lib.LayerInfo, "thb_arena_info": _lib.ArenaInfo}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "thuban_hip.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                              check=True).stdout.splitlines())
+    for cname, cls in structs.items():
+        assert int(got[cname]) == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert int(got[f"{cname}.{fname}"]) == getattr(cls, fname).offset, (cname, fname)
+
+
+def test_check_head_dim():
+    from flint_amd import ThubanError, check_head_dim
+
+    for hd in (64, 80, 128, 256, 512):
+        check_head_dim(hd)
+    for hd, msg in ((32, "head_dim 32 outside [64, 512]"), (513, "outside"), (100, "multiple of 8")):
+        with pytest.raises(ThubanError) as e:
+            check_head_dim(hd)
+        assert msg in str(e.value)
+        assert e.value.kind == "Config"
+
+
+def test_product_does_not_reference_the_oracle():
+    """The product package never imports or loads the oracle."""
+    for base, _, files in os.walk(os.path.join(ROOT, "flint_amd")):
+        for fn in files:
+            if fn.endswith((".py", ".hip", ".cpp", ".hpp", ".h")) or fn == "Makefile":
+                with open(os.path.join(base, fn)) as f:
+                    src = f.read()
+                assert "oracle" not in src.lower(), os.path.join(base, fn)

@@ -1,0 +1,260 @@
+"""GPU parity of paged attention against the CPU oracle (exact softmax in
+double): within 2e-3 max abs (the north-star tolerance for f16 outputs of
+an fp32-accumulating reference), plus bit-exact invariants (paged ==
+contiguous, batch == solo, repeatability) from the reference's
+tests/batch.rs:163-347."""
+
+import math
+import random
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import fill, make_pool, oracle_layer, say, scattered_alloc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def run_attn(torch, pool, rows, q, positions, seqs, spec_seq=None, window=0, causal=True, softcap=0.0,
+             scale=None, y_dtype=None, layer=0, row_off=0):
+    from flint_amd import ops
+
+    m, nq, hd = q.shape
+    rows.write(positions, seqs, len(positions))
+    y = torch.empty(m, nq, hd, device="cuda", dtype=y_dtype or torch.float32)
+    spec = ops.AttnSpec(q_heads=nq, window=window, scale=scale or 1.0 / math.sqrt(hd), m=m, causal=causal,
+                        seq=spec_seq, args=rows, row_off=row_off, softcap=softcap)
+    ops.attn(q, pool, layer, y, spec)
+    torch.cuda.synchronize()
+    return y
+
+
+def check_parity(torch, pool, rows, q, positions, seqs, label, **kw):
+    y = run_attn(torch, pool, rows, q, positions, seqs, **kw)
+    ref = oracle_layer(torch, pool, kw.get("layer", 0))
+    m, nq, hd = q.shape
+    want = ref.attn(q.float().cpu().numpy(), oracle.row_meta(positions, seqs), m, nq,
+                    kw.get("scale") or 1.0 / math.sqrt(hd), window=kw.get("window", 0),
+                    causal=kw.get("causal", True), seq=kw.get("spec_seq"), softcap=kw.get("softcap", 0.0))
+    got = y.float().cpu().numpy()
+    err = float(np.max(np.abs(got - want)))
+    say(label, "max abs err", err)
+    assert np.all(np.isfinite(got)), label
+    assert err <= TOL, (label, err)
+    return y
+
+
+CASES = [
+    # name, nq, nkv, hd, page_len, kv, lens
+    ("qwen2-0.5b", 14, 2, 64, 16, "bf16", [128, 512, 300, 201]),
+    ("qwen2-0.5b-p32", 14, 2, 64, 32, "f16", [130, 420, 511, 256]),
+    ("llama3-8b", 32, 8, 128, 16, "f16", [1500, 513, 2048, 77]),
+    ("llama3-8b-bf16", 32, 8, 128, 16, "bf16", [900, 1025]),
+    ("qwen2.5-32b", 40, 8, 128, 16, "f16", [1200, 700]),
+    ("gemma2-9b", 16, 8, 256, 16, "f16", [1300, 600]),
+    ("hd80", 8, 2, 80, 16, "f16", [333, 40]),
+    ("hd512", 8, 2, 512, 16, "f16", [700, 100]),
+    ("mqa-g16", 16, 1, 128, 32, "f16", [640, 50]),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_decode_batched_parity(torch_cuda, case):
+    torch = torch_cuda
+    from flint_amd.pool import RowMeta
+
+    name, nq, nkv, hd, pl, kv, lens = case
+    say("decode", name)
+    rng = random.Random(hash(name) & 0xFFFF)
+    pool = make_pool(lens, kv_heads=nkv, head_dim=hd, page_len=pl, kv_dtype=kv, extra_pages=7)
+    scattered_alloc(pool, lens, rng, pl)
+    rows = RowMeta(256)
+    fill(torch, pool, rows, lens, seed=1)
+    B = len(lens)
+    q = torch.randn(B, nq, hd, device="cuda")
+    positions = [n - 1 for n in lens]
+    check_parity(torch, pool, rows, q, positions, list(range(B)), name)
+    # f16 in / f16 out
+    check_parity(torch, pool, rows, q.half(), positions, list(range(B)), name + "-f16io", y_dtype=torch.float16)
+
+
+def test_window_and_softcap_gemma(torch_cuda):
+    torch = torch_cuda
+    from flint_amd.pool import RowMeta
+
+    lens = [1500, 900]
+    pool = make_pool(lens, kv_heads=8, head_dim=256, page_len=16, kv_dtype="f16", extra_pages=4)
+    scattered_alloc(pool, lens, random.Random(2), 16)
+    rows = RowMeta(64)
+    fill(torch, pool, rows, lens, seed=2, scale=3.0)
+    q = torch.randn(2, 16, 256, device="cuda") * 2
+    for window in (0, 64, 700, 4096):
+        check_parity(torch, pool, rows, q, [1499, 899], [0, 1], f"gemma window={window}", window=window,
+                     softcap=50.0, scale=1.0 / 16)
+
+
+def test_speculative_verify_rows(torch_cuda):
+    """4 causal query rows per sequence (draft verify), batched."""
+    torch = torch_cuda
+    from flint_amd.pool import RowMeta
+
+    lens = [700, 1031, 64]
+    pool = make_pool(lens, kv_heads=8, head_dim=256, page_len=16, kv_dtype="f16", extra_pages=2)
+    scattered_alloc(pool, lens, random.Random(3), 16)
+    rows = RowMeta(64)
+    fill(torch, pool, rows, lens, seed=3)
+    positions, seqs = [], []
+    for s, n in enumerate(lens):
+        positions += [n - 4 + i for i in range(4)]
+        seqs += [s] * 4
+    q = torch.randn(len(seqs), 16, 256, device="cuda")
+    check_parity(torch, pool, rows, q, positions, seqs, "verify m=4", window=512)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_reference_mode_chunk(torch_cuda, causal):
+    """AttnSpec.seq fixed (one dispatch per sequence chunk, forward.rs:316-336):
+    a 40-row prefill chunk with the reference's 8-row kv_len rule."""
+    torch = torch_cuda
+    from flint_amd.pool import RowMeta
+
+    lens = [300, 520]
+    pool = make_pool(lens, kv_heads=2, head_dim=64, page_len=32, kv_dtype="bf16")
+    scattered_alloc(pool, lens, random.Random(4), 32)
+    rows = RowMeta(128)
+    fill(torch, pool, rows, lens, seed=4)
+    m = 40
+    positions = list(range(520 - m, 520))
+    q = torch.randn(m, 14, 64, device="cuda")
+    # the call's rows sit at row_off 5 of the row meta (forward.rs:332)
+    from flint_amd import ops
+
+    rows.write([0] * 5 + positions, [0] * 5 + [1] * m, 5 + m)
+    y = torch.empty_like(q)
+    ops.attn(q, pool, 0, y, ops.AttnSpec(q_heads=14, window=0, scale=0.125, m=m, causal=causal, seq=1,
+                                          args=rows, row_off=5))
+    torch.cuda.synchronize()
+    want = oracle_layer(torch, pool).attn(q.cpu().numpy(), oracle.row_meta(positions, [1] * m), m, 14, 0.125,
+                                          causal=causal, seq=1)
+    err = float(np.max(np.abs(y.cpu().numpy() - want)))
+    say("reference-mode chunk causal", causal, err)
+    assert err <= TOL
+
+
+def test_reference_anchor_through_gpu(torch_cuda, golden):
+    """anchor_attn_causal_and_window (kernels.rs:1439-1481) embedded in the
+    first two dims of a head_dim-64 pool: [2, 3] full, [3, 4] window 1."""
+    torch = torch_cuda
+    from flint_amd.pool import RowMeta
+
+    for case in golden("attn_cases.json"):
+        pool = make_pool([2], kv_heads=1, head_dim=64, page_len=16, kv_dtype="bf16")
+        pool.alloc(0, 0, 2)
+        rows = RowMeta(4)
+        rows.write([0, 1], [0, 0], 2)
+        k = torch.zeros(2, 1, 64, device="cuda")
+        v = torch.zeros(2, 1, 64, device="cuda")
+        k[:, 0, :2] = torch.tensor(case["k"]).view(2, 2)
+        v[:, 0, :2] = torch.tensor(case["v"]).view(2, 2)
+        from flint_amd import ops
+
+        ops.kv_store(k, v, pool, 0, 2, rows)
+        q = torch.zeros(1, 1, 64, device="cuda")
+        q[0, 0, :2] = torch.tensor(case["q"])
+        y = run_attn(torch, pool, rows, q, [case["pos"]], [0], window=case["window"], scale=1 / math.sqrt(2))
+        got = y[0, 0, :2].cpu().numpy()
+        say("anchor", case["name"], got)
+        assert np.allclose(got, case["expect"], atol=1e-6)
+
+
+def test_invariants_bit_exact(torch_cuda):
+    """paged == contiguous, batch == solo, identical sequences give identical
+    outputs, repeat runs are identical (batch.rs:163-347)."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    lens = [1800, 1800, 650]
+    rng = random.Random(9)
+    # pool A: scattered pages; pool B: same data, pages in a different order
+    A = make_pool(lens, kv_heads=8, head_dim=128, page_len=16, kv_dtype="f16", extra_pages=9)
+    B = make_pool(lens, kv_heads=8, head_dim=128, page_len=16, kv_dtype="f16", extra_pages=9)
+    scattered_alloc(A, lens, rng, 16)
+    B.alloc(2, 0, 650)  # different order, different physical pages
+    B.alloc(1, 0, 1800)
+    B.alloc(0, 0, 1800)
+    rows = RowMeta(256)
+    fill(torch, A, rows, [1800, 0, 650], seed=5)
+    fill(torch, B, rows, [1800, 0, 650], seed=5)
+    # seq 1 := copy of seq 0 (identical sequence), through gather/scatter
+    kd = torch.empty(8, 1800, 128, dtype=torch.int16, device="cuda")
+    vd = torch.empty_like(kd)
+    for P in (A, B):
+        ops.kv_gather(P, 0, 0, 0, 1800, kd, vd)
+        ops.kv_scatter(P, 0, 1, 0, 1800, kd, vd)
+    q = torch.randn(3, 32, 128, device="cuda")
+    q[1] = q[0]
+    pos, seqs = [1799, 1799, 649], [0, 1, 2]
+    ya = run_attn(torch, A, rows, q, pos, seqs)
+    yb = run_attn(torch, B, rows, q, pos, seqs)
+    assert torch.equal(ya, yb), "paged == contiguous"
+    assert torch.equal(ya[0], ya[1]), "identical sequences"
+    solo = run_attn(torch, A, rows, q[2:3].contiguous(), [649], [2])
+    assert torch.equal(solo[0], ya[2]), "batch == solo"
+    again = run_attn(torch, A, rows, q, pos, seqs)
+    assert torch.equal(again, ya), "repeatable"
+
+
+def test_llama3_full_shape_sampled(torch_cuda):
+    """BASELINE config 2 at full size (B=32, ctx 4096, 32q/8kv/hd128, f16 KV,
+    scattered block tables): the oracle checks 3 sequences in full, and every
+    output is a convex combination of V (|y| <= max |V|)."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    B, ctx = 32, 4096
+    lens = [ctx] * B
+    pool = make_pool(lens, kv_heads=8, head_dim=128, page_len=16, kv_dtype="f16")
+    scattered_alloc(pool, lens, random.Random(10), 16)
+    k, v = pool.layer_tensors(0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(10)
+    k.view(torch.float16).copy_(torch.randn(k.shape, device="cuda", generator=g).half())
+    v.view(torch.float16).copy_(torch.randn(v.shape, device="cuda", generator=g).half())
+    rows = RowMeta(64)
+    q = torch.randn(B, 32, 128, device="cuda")
+    say("llama3 full shape")
+    y = run_attn(torch, pool, rows, q, [ctx - 1] * B, list(range(B)))
+    assert float(y.abs().max()) <= float(v.view(torch.float16).abs().max()) + 1e-3
+    ref = oracle_layer(torch, pool)
+    for s in (0, 17, 31):
+        want = ref.attn(q[s:s + 1].cpu().numpy(), oracle.row_meta([ctx - 1], [s]), 1, 32, 1 / math.sqrt(128))
+        err = float(np.max(np.abs(y[s:s + 1].cpu().numpy() - want)))
+        say("llama3 full seq", s, err)
+        assert err <= TOL
+
+
+def test_attn_errors(torch_cuda):
+    torch = torch_cuda
+    from flint_amd import ThubanError, ops
+    from flint_amd.pool import RowMeta
+
+    pool = make_pool([100], kv_heads=2, head_dim=64, page_len=16)
+    pool.alloc(0, 0, 40)
+    rows = RowMeta(4)
+    q = torch.zeros(1, 4, 64, device="cuda")
+    y = torch.empty_like(q)
+    rows.write([60], [0], 1)
+    with pytest.raises(ThubanError) as e:
+        ops.attn(q, pool, 0, y, ops.AttnSpec(4, 0, 0.125, 1, True, None, rows))
+    assert "pages must cover" in str(e.value)
+    with pytest.raises(ThubanError):
+        ops.attn(q, pool, 0, y, ops.AttnSpec(3, 0, 0.125, 1, True, None, rows))  # 3 % 2 != 0
+    rows.write([39], [0], 1)
+    ops.attn(q, pool, 0, y, ops.AttnSpec(4, 0, 0.125, 1, True, None, rows))
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()

@@ -1,0 +1,203 @@
+"""GPU parity of append (kv_store), gather, scatter, block copy and fork:
+bit-exact against the CPU oracle on identical inputs."""
+
+import random
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import fill, make_pool, oracle_layer, say, scattered_alloc
+
+pytestmark = pytest.mark.gpu
+
+SRC = {"f32": oracle.SRC_F32, "f16": oracle.SRC_F16, "bf16": oracle.SRC_BF16}
+
+
+def _src_words(torch, t):
+    if t.dtype == torch.float32:
+        return t.cpu().numpy()
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "f16"])
+@pytest.mark.parametrize("src", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("page_len", [16, 32])
+def test_kv_store_bit_exact(torch_cuda, kv, src, page_len):
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    say("kv_store", kv, src, page_len)
+    rng = random.Random(11)
+    lens = [70, 33, 129]
+    pool = make_pool(lens, kv_heads=4, head_dim=128, page_len=page_len, kv_dtype=kv, extra_pages=3)
+    scattered_alloc(pool, lens, rng, page_len)
+    ref = oracle_layer(torch, pool)  # zero pool + the table
+    rows = RowMeta(64)
+    pairs = [(p, s) for s, n in enumerate(lens) for p in range(n)]
+    rng.shuffle(pairs)
+    dt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[src]
+    for i in range(0, len(pairs), 64):
+        chunk = pairs[i: i + 64]
+        m = len(chunk)
+        pos, seqs = [p for p, _ in chunk], [s for _, s in chunk]
+        rows.write(pos, seqs, m)
+        k = torch.randn(m, 4, 128, device="cuda").to(dt)
+        v = (torch.randn(m, 4, 128, device="cuda") * 1e3).to(dt)
+        ops.kv_store(k, v, pool, 0, m, rows)
+        ref.kv_store(_src_words(torch, k), _src_words(torch, v), oracle.row_meta(pos, seqs), m, SRC[src])
+    got = oracle_layer(torch, pool)
+    assert np.array_equal(got.k, ref.k)
+    assert np.array_equal(got.v, ref.v)
+
+
+def test_kv_store_special_values_bit_exact(torch_cuda):
+    """Every sign/exponent/top-10-mantissa pattern x rounding-relevant low
+    bits (incl. NaN, inf, subnormals, ties) through f32 -> f16 and -> bf16."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    hi = np.arange(1 << 19, dtype=np.uint32) << np.uint32(13)
+    low = np.array([0, 1, 0x0FFF, 0x1000, 0x1001, 0x1FFF, 0x0800, 0x1800], dtype=np.uint32)
+    bits = (hi[:, None] | low[None, :]).reshape(-1)  # 4 Mi values
+    nkv, hd = 8, 128
+    m = bits.size // (nkv * hd)  # 4096 rows
+    for kv in ("f16", "bf16"):
+        say("special values", kv)
+        pool = make_pool([m], kv_heads=nkv, head_dim=hd, page_len=32, kv_dtype=kv)
+        pool.alloc(0, 0, m)
+        rows = RowMeta(m)
+        rows.write(list(range(m)), [0] * m, m)
+        src = torch.from_numpy(bits.view(np.float32).reshape(m, nkv, hd).copy()).cuda()
+        ops.kv_store(src, src, pool, 0, m, rows)
+        k, v = pool.layer_tensors(0)
+        torch.cuda.synchronize()
+        table = np.array(pool.arena.table_of(0))
+        # slot of token t = table[t // 32] * 32 + t % 32; gather back in token order
+        slots = (table[np.arange(m) // 32] * 32 + np.arange(m) % 32)
+        got = k.cpu().numpy().view(np.uint16)[:, slots, :].transpose(1, 0, 2).reshape(-1)
+        want = (oracle.f32_to_f16 if kv == "f16" else oracle.f32_to_bf16)(bits.view(np.float32))
+        assert np.array_equal(got, want)
+        gotv = v.cpu().numpy().view(np.uint16)[:, slots, :].transpose(1, 0, 2).reshape(-1)
+        assert np.array_equal(gotv, want)
+
+
+def test_kv_store_reference_lcg_vector(torch_cuda, golden):
+    """kv_store_writes_both_caches (kernels.rs:1266-1308) embedded in the
+    first 4 dims of a head_dim-64 pool (the product needs head_dim >= 64)."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    case = [c for c in golden("kv_store_cases.json") if c["name"] == "kv_store_writes_both_caches"][0]
+    m, nkv, hd, pos = case["m"], case["kv_heads"], case["head_dim"], case["pos"]
+    say("reference kv_store vector")
+    pool = make_pool([case["max_seq"]], kv_heads=nkv, head_dim=64, page_len=8, kv_dtype="bf16")
+    pool.alloc(0, 0, case["max_seq"])
+    rows = RowMeta(8)
+    rows.write([pos + i for i in range(m)], [0] * m, m)
+    ks = np.zeros((m, nkv, 64), np.float32)
+    vs = np.zeros((m, nkv, 64), np.float32)
+    ks[:, :, :hd] = np.array(case["k_src"], np.uint32).view(np.float32).reshape(m, nkv, hd)
+    vs[:, :, :hd] = np.array(case["v_src"], np.uint32).view(np.float32).reshape(m, nkv, hd)
+    ops.kv_store(torch.from_numpy(ks).cuda(), torch.from_numpy(vs).cuda(), pool, 0, m, rows)
+    k, v = pool.layer_tensors(0)
+    torch.cuda.synchronize()
+    got_k = k.cpu().numpy().view(np.uint16)[:, :, :hd].reshape(-1)
+    got_v = v.cpu().numpy().view(np.uint16)[:, :, :hd].reshape(-1)
+    assert np.array_equal(got_k, np.array(case["expect_k"], np.uint16))
+    assert np.array_equal(got_v, np.array(case["expect_v"], np.uint16))
+
+
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_gather_scatter_round_trip(torch_cuda, hd):
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    say("gather/scatter", hd)
+    rng = random.Random(hd)
+    lens = [100, 47]
+    pool = make_pool(lens, kv_heads=2, head_dim=hd, page_len=16, kv_dtype="f16", layers=2, extra_pages=4)
+    scattered_alloc(pool, lens, rng, 16)
+    rows = RowMeta(128)
+    fill(torch, pool, rows, lens, layer=1, seed=3)
+    ref = oracle_layer(torch, pool, layer=1)
+    kd = torch.empty(2, 61, hd, dtype=torch.int16, device="cuda")
+    vd = torch.empty_like(kd)
+    ops.kv_gather(pool, 1, 0, 30, 61, kd, vd)
+    torch.cuda.synchronize()
+    rk, rv = ref.gather(0, 30, 61)
+    assert np.array_equal(kd.cpu().numpy().view(np.uint16), rk)
+    assert np.array_equal(vd.cpu().numpy().view(np.uint16), rv)
+    # scatter new words into seq 1 tokens [5, 40), gather back
+    nk = torch.randint(-30000, 30000, (2, 35, hd), dtype=torch.int16, device="cuda")
+    nv = torch.randint(-30000, 30000, (2, 35, hd), dtype=torch.int16, device="cuda")
+    ops.kv_scatter(pool, 1, 1, 5, 35, nk, nv)
+    ops.kv_gather(pool, 1, 1, 5, 35, kd[:, :35].contiguous(), vd[:, :35].contiguous())
+    k2 = torch.empty(2, 35, hd, dtype=torch.int16, device="cuda")
+    v2 = torch.empty_like(k2)
+    ops.kv_gather(pool, 1, 1, 5, 35, k2, v2)
+    torch.cuda.synchronize()
+    assert torch.equal(k2, nk) and torch.equal(v2, nv)
+    # layer 0 untouched by layer-1 traffic
+    k0, _ = pool.layer_tensors(0)
+    assert int(k0.abs().sum()) == 0
+
+
+def test_block_copy_and_fork_copy_on_write(torch_cuda):
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    say("block copy / fork")
+    rng = random.Random(5)
+    lens = [90, 0, 0]
+    pool = make_pool(lens, kv_heads=2, head_dim=128, page_len=16, kv_dtype="bf16", layers=3, extra_pages=20,
+                     seq_lens=[200, 200, 200])
+    scattered_alloc(pool, [90], rng, 16)
+    rows = RowMeta(128)
+    for layer in range(3):
+        fill(torch, pool, rows, [90], layer=layer, seed=layer)
+    before = [oracle_layer(torch, pool, layer) for layer in range(3)]
+    pool.fork(0, 1, 90)  # 5 full pages shared, page 5 (10 tokens) copied
+    t0, t1 = pool.arena.table_of(0), pool.arena.table_of(1)
+    assert t1[:5] == t0[:5] and t1[5] != t0[5]
+    pool.sync()
+    for layer in range(3):
+        after = oracle_layer(torch, pool, layer)
+        want = before[layer]
+        want.block_copy([[t0[5], t1[5], 10]])
+        assert np.array_equal(after.k, want.k) and np.array_equal(after.v, want.v)
+        ka, va = after.gather(0, 0, 90)
+        kb, vb = after.gather(1, 0, 90)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    # explicit block copy: page of seq 0 -> a free page, all layers
+    free_page = [p for p in range(pool.arena.pages()) if p not in t0 + t1][0]
+    ops.block_copy(pool, [[t0[1], free_page, 16]])
+    pool.sync()
+    for layer in range(3):
+        after = oracle_layer(torch, pool, layer)
+        assert np.array_equal(after.k[:, free_page * 16:(free_page + 1) * 16], after.k[:, t0[1] * 16:(t0[1] + 1) * 16])
+
+
+def test_kv_store_errors(torch_cuda):
+    torch = torch_cuda
+    from flint_amd import ThubanError, ops
+    from flint_amd.pool import RowMeta
+
+    pool = make_pool([40], kv_heads=2, head_dim=64, page_len=16)
+    pool.alloc(0, 0, 16)
+    rows = RowMeta(4)
+    rows.write([20], [0], 1)
+    k = torch.zeros(1, 2, 64, device="cuda")
+    with pytest.raises(ThubanError) as e:
+        ops.kv_store(k, k, pool, 0, 1, rows)
+    assert "pages must cover" in str(e.value) and e.value.kind == "Model"
+    rows.write([3], [0], 1)
+    ops.kv_store(k, k, pool, 0, 0, rows)  # m == 0 is a no-op
+    with pytest.raises(ThubanError):
+        ops.kv_store(k, k, pool, 1, 1, rows)  # no layer 1
+    torch.cuda.synchronize()

@@ -1,0 +1,231 @@
+"""Pins the CPU oracle (oracle/) against the reference's own known answers
+and against closed forms.  CPU only."""
+
+import math
+import struct
+
+import numpy as np
+import pytest
+
+
+def f32(bits):
+    return struct.unpack("<f", struct.pack("<I", bits))[0]
+
+
+def bits32(x):
+    return struct.unpack("<I", struct.pack("<f", x))[0]
+
+
+# ------------------------------------------------------------------ codecs
+def test_codec_known_answers(orc, golden):
+    g = golden("codec_cases.json")
+    L = orc.lib()
+    for h, fb in g["f16_to_f32"]:
+        assert bits32(L.orc_f16_to_f32(h)) == fb, hex(h)
+    for fb, h in g["f32_to_f16"]:
+        assert L.orc_f32_to_f16(f32(fb)) == h, (hex(fb), hex(h))
+    for fb in g["f16_round_trip"]:
+        assert bits32(L.orc_f16_to_f32(L.orc_f32_to_f16(f32(fb)))) == fb
+    for fb in g["bf16_round_trip"]:
+        assert bits32(L.orc_bf16_to_f32(L.orc_f32_to_bf16(f32(fb)))) == fb
+
+
+def test_f16_decode_exhaustive_matches_ieee(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    ours = orc.f16_to_f32(h).view(np.uint32)
+    ieee = h.view(np.float16).astype(np.float32).view(np.uint32)
+    assert np.array_equal(ours, ieee)
+
+
+def special_f32_bits():
+    """Every sign/exponent/top-10-mantissa pattern crossed with the low-13-bit
+    patterns that decide rounding (tie, just below, just above, ...)."""
+    hi = np.arange(1 << 19, dtype=np.uint32) << np.uint32(13)
+    low = np.array([0, 1, 0x0FFF, 0x1000, 0x1001, 0x1FFF, 0x0800, 0x1800], dtype=np.uint32)
+    return (hi[:, None] | low[None, :]).reshape(-1)
+
+
+def test_f16_encode_matches_ieee_rne(orc):
+    # f32 -> f16 RNE is the IEEE conversion numpy implements, except that the
+    # reference turns every NaN into sign|0x7E00 (thuban_num lib.rs:30-35).
+    b = special_f32_bits()
+    ours = orc.f32_to_f16(b.view(np.float32))
+    x = b.view(np.float32)
+    nan = np.isnan(x)
+    with np.errstate(over="ignore"):
+        ieee = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours[~nan], ieee[~nan])
+    sign = ((b[nan] >> 16) & 0x8000).astype(np.uint16)
+    assert np.array_equal(ours[nan], sign | np.uint16(0x7E00))
+
+
+def test_bf16_is_truncation(orc):
+    b = special_f32_bits()
+    assert np.array_equal(orc.f32_to_bf16(b.view(np.float32)), (b >> 16).astype(np.uint16))
+
+
+# --------------------------------------------------------------- kv_store
+def _identity_layer(orc, case, page_len):
+    # cpu_ref's contiguous cache [kv_heads, max_seq, hd] equals a paged pool
+    # whose pages are laid out in order (identity block table).
+    pages = case["max_seq"] // page_len
+    return orc.Layer(case["kv_heads"], case["head_dim"], pages, page_len, np.arange(pages, dtype=np.uint32),
+                     pages, orc.KV_BF16)
+
+
+@pytest.mark.parametrize("page_len", [1, 2])
+def test_kv_store_reference_vectors(orc, golden, page_len):
+    for case in golden("kv_store_cases.json"):
+        L = _identity_layer(orc, case, page_len)
+        m = case["m"]
+        args = orc.row_meta([case["pos"] + i for i in range(m)], [0] * m)
+        k = np.array(case["k_src"], np.uint32).view(np.float32)
+        v = np.array(case["v_src"], np.uint32).view(np.float32)
+        L.kv_store(k, v, args, m)
+        assert np.array_equal(L.k.reshape(-1), np.array(case["expect_k"], np.uint16)), case["name"]
+        assert np.array_equal(L.v.reshape(-1), np.array(case["expect_v"], np.uint16)), case["name"]
+
+
+def test_kv_store_scatters_through_block_table(orc):
+    rng = np.random.default_rng(7)
+    nkv, hd, page_len, pages = 2, 8, 4, 6
+    perm = rng.permutation(pages).astype(np.uint32)
+    bt = perm.reshape(2, 3)  # 2 sequences x 3 pages
+    L = orc.Layer(nkv, hd, pages, page_len, bt.reshape(-1), 3, orc.KV_F16)
+    pos = [5, 0, 11]
+    seqs = [1, 0, 0]
+    src = rng.standard_normal((3, nkv, hd)).astype(np.float32)
+    L.kv_store(src, -src, orc.row_meta(pos, seqs), 3)
+    for r in range(3):
+        slot = bt[seqs[r], pos[r] // page_len] * page_len + pos[r] % page_len
+        assert np.array_equal(L.k[:, slot, :], orc.f32_to_f16(src[r]))
+        assert np.array_equal(L.v[:, slot, :], orc.f32_to_f16(-src[r]))
+    assert np.count_nonzero(L.k.reshape(-1, hd).any(axis=1)) == 3 * nkv
+
+
+# ------------------------------------------------------------------- attn
+def test_attn_reference_anchors(orc, golden):
+    for case in golden("attn_cases.json"):
+        L = orc.Layer(1, 2, 1, 2, np.array([0], np.uint32), 1, orc.KV_BF16)
+        L.k[:] = orc.f32_to_bf16(np.array(case["k"], np.float32)).reshape(L.k.shape)
+        L.v[:] = orc.f32_to_bf16(np.array(case["v"], np.float32)).reshape(L.v.shape)
+        y = L.attn(np.array(case["q"], np.float32), orc.row_meta([case["pos"]], [0]), 1, 1,
+                   1.0 / math.sqrt(case["head_dim"]), window=case["window"], causal=case["causal"], seq=0)
+        assert np.allclose(y.reshape(-1), case["expect"], atol=case["tol"]), case["name"]
+
+
+def _random_pool(orc, rng, nkv=2, hd=16, page_len=4, seqs=3, max_pages=8, kv=None, extra_pages=5):
+    kv = orc.KV_F16 if kv is None else kv
+    pages = seqs * max_pages + extra_pages
+    perm = rng.permutation(pages)[: seqs * max_pages].astype(np.uint32)
+    L = orc.Layer(nkv, hd, pages, page_len, perm, max_pages, kv)
+    L.k[:] = orc.encode_kv(rng.standard_normal(L.k.shape).astype(np.float32), kv)
+    L.v[:] = orc.encode_kv(rng.standard_normal(L.v.shape).astype(np.float32), kv)
+    return L
+
+
+def test_attn_ranges_follow_wgsl(orc):
+    # 10 rows of one sequence at positions 20..29, causal, window 4:
+    # kv_len of rows 0-7 is pos[7]+1 = 28, of rows 8-9 pos[9]+1 = 30.
+    args = orc.row_meta(list(range(20, 30)), [0] * 10)
+    lo, hi, _ = orc.attn_ranges(args, 10, seq=0, causal=True, window=4)
+    assert list(lo) == [p + 1 - 4 for p in range(20, 30)]
+    assert list(hi) == [p + 1 for p in range(20, 30)]
+    lo, hi, _ = orc.attn_ranges(args, 10, seq=0, causal=False, window=4)
+    assert list(lo) == [0] * 10 and list(hi) == [30] * 10  # window needs causal (attn.wgsl:80)
+    # non-monotonic positions: the 8-row block's last row caps kv_len
+    args = orc.row_meta([9, 3, 1], [0, 0, 0])
+    lo, hi, _ = orc.attn_ranges(args, 3, seq=0, causal=True, window=0)
+    assert list(hi) == [2, 2, 2]
+
+
+def test_attn_single_key_returns_its_value(orc):
+    rng = np.random.default_rng(1)
+    L = _random_pool(orc, rng)
+    q = rng.standard_normal((1, 4, 16)).astype(np.float32)
+    y = L.attn(q, orc.row_meta([9], [1]), 1, 4, 0.25, window=1, causal=True)
+    slot = L.block_table[1 * L.max_pages + 9 // 4] * 4 + 9 % 4
+    for h in range(4):
+        assert np.array_equal(y[0, h], orc.decode_kv(L.v[h // 2, slot], L.kv_dtype).astype(np.float64))
+
+
+def test_attn_zero_query_averages_values(orc):
+    rng = np.random.default_rng(2)
+    L = _random_pool(orc, rng)
+    q = np.zeros((1, 2, 16), np.float32)
+    y = L.attn(q, orc.row_meta([13], [2]), 1, 2, 0.25, window=6, causal=True)
+    vals = []
+    for j in range(13 + 1 - 6, 14):
+        slot = L.block_table[2 * L.max_pages + j // 4] * 4 + j % 4
+        vals.append(orc.decode_kv(L.v[:, slot], L.kv_dtype))
+    mean = np.mean(np.array(vals, np.float64), axis=0)
+    assert np.allclose(y[0], mean, atol=1e-12)
+
+
+def test_attn_paged_equals_contiguous(orc):
+    # batch.rs:302-347 invariant, here exactly (same arithmetic, other pages).
+    rng = np.random.default_rng(3)
+    L = _random_pool(orc, rng, seqs=2)
+    perm2 = rng.permutation(L.pool_len // L.page_len)[: 2 * L.max_pages].astype(np.uint32)
+    L2 = orc.Layer(L.kv_heads, L.head_dim, L.pool_len // L.page_len, L.page_len, perm2, L.max_pages, L.kv_dtype)
+    for s in range(2):
+        for j in range(L.max_pages * L.page_len):
+            a = L.block_table[s * L.max_pages + j // 4] * 4 + j % 4
+            b = perm2[s * L.max_pages + j // 4] * 4 + j % 4
+            L2.k[:, b] = L.k[:, a]
+            L2.v[:, b] = L.v[:, a]
+    q = rng.standard_normal((3, 4, 16)).astype(np.float32)
+    args = orc.row_meta([5, 30, 31], [0, 1, 1])
+    assert np.array_equal(L.attn(q, args, 3, 4, 0.25), L2.attn(q, args, 3, 4, 0.25))
+
+
+def test_attn_window_beyond_context_is_no_window(orc):
+    rng = np.random.default_rng(4)
+    L = _random_pool(orc, rng)
+    q = rng.standard_normal((2, 2, 16)).astype(np.float32)
+    args = orc.row_meta([17, 18], [0, 0])
+    assert np.array_equal(L.attn(q, args, 2, 2, 0.3, window=0, seq=0), L.attn(q, args, 2, 2, 0.3, window=19, seq=0))
+    assert not np.array_equal(L.attn(q, args, 2, 2, 0.3, window=0, seq=0),
+                              L.attn(q, args, 2, 2, 0.3, window=18, seq=0))
+
+
+def test_attn_softcap_closed_form(orc):
+    # one row, two keys: weights are softmax of cap*tanh(s/cap)
+    L = orc.Layer(1, 8, 1, 8, np.array([0], np.uint32), 1, orc.KV_F16)
+    k = np.zeros((2, 8), np.float32)
+    k[0, 0], k[1, 1] = 3.0, -2.0
+    v = np.eye(2, 8, dtype=np.float32)
+    L.k[0, :2] = orc.f32_to_f16(k)
+    L.v[0, :2] = orc.f32_to_f16(v)
+    q = np.zeros((1, 1, 8), np.float32)
+    q[0, 0, :2] = [10.0, 10.0]
+    cap = 5.0
+    y = L.attn(q, orc.row_meta([1], [0]), 1, 1, 0.5, softcap=cap)
+    s = cap * np.tanh(np.array([30.0 * 0.5, -20.0 * 0.5]) / cap)
+    w = np.exp(s - s.max())
+    w /= w.sum()
+    assert np.allclose(y[0, 0, :2], w, atol=1e-12)
+
+
+def test_attn_f32_mode_matches_double(orc):
+    rng = np.random.default_rng(5)
+    L = _random_pool(orc, rng, hd=64, page_len=8, max_pages=40, kv=orc.KV_BF16)
+    q = rng.standard_normal((4, 4, 64)).astype(np.float32)
+    args = orc.row_meta([300, 301, 40, 250], [0, 0, 1, 2])
+    y64 = L.attn(q, args, 4, 4, 0.125, window=128)
+    y32 = L.attn(q, args, 4, 4, 0.125, window=128, precision=1)
+    assert np.max(np.abs(y64 - y32)) < 1e-5
+
+
+def test_gather_and_block_copy_closed_form(orc):
+    rng = np.random.default_rng(6)
+    L = _random_pool(orc, rng)
+    k, v = L.gather(1, 3, 9)
+    for t in range(9):
+        j = 3 + t
+        slot = L.block_table[L.max_pages + j // 4] * 4 + j % 4
+        assert np.array_equal(k[:, t], L.k[:, slot]) and np.array_equal(v[:, t], L.v[:, slot])
+    before = L.k.copy()
+    L.block_copy([[2, 5, 3]])
+    assert np.array_equal(L.k[:, 20:23], before[:, 8:11])
+    assert np.array_equal(L.k[:, 23], before[:, 23])
