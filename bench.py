@@ -64,11 +64,10 @@ def cpu_baseline(torch, pool, q0, y0, cfg, scale, seconds):
 
     import oracle
 
-    kw, vw = pool.layer_tensors(0)
+    kw, vw = pool.read_layer(0)
     info = pool.arena.info()
     ref = oracle.Layer(cfg["kv_heads"], cfg["head_dim"], info.pages, cfg["page_len"],
-                       np.array(pool.arena.table(), np.uint32), info.max_pages, oracle.KV_F16,
-                       k=kw.cpu().numpy().view(np.uint16), v=vw.cpu().numpy().view(np.uint16))
+                       np.array(pool.arena.table(), np.uint32), info.max_pages, oracle.KV_F16, k=kw, v=vw)
     B, ctx = cfg["batch"], cfg["ctx"]
     args = oracle.row_meta([ctx - 1] * B, list(range(B)))
     qn = q0.float().cpu().numpy()
@@ -191,7 +190,7 @@ def main():
         "config": {"workload": f"{args.config}-decode: {L} layers, batch {B}, ctx {ctx}, {nq}q/{nkv}kv, "
                                f"hd {hd}, page {pl}, f16 KV; step = append 1 token/seq/layer + paged decode",
                    "layers": L, "batch": B, "ctx": ctx, "q_heads": nq, "kv_heads": nkv, "head_dim": hd,
-                   "page_len": pl, "kv_dtype": "f16", "part_len": args.part_len or 512},
+                   "page_len": pl, "kv_dtype": "f16", "part_len": args.part_len or 4096},
         "us_per_step": round(ms_step * 1e3, 1),
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 1),
         "decode": {"us_per_layer": round(attn_us, 2), "GBps": round(achieved, 1),
@@ -200,7 +199,7 @@ def main():
                    "bytes_per_launch": append_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
-                     "kernel": "attn_splitk<128,4,f16>", "algorithmic_bytes": attn_bytes},
+                     "kernel": "attn_mfma<128,f16,8 waves>", "algorithmic_bytes": attn_bytes},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -12,6 +12,8 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libthuban_hip.so")
 
+ABI_VERSION = 2  # THB_ABI_VERSION of include/thuban_hip.h
+
 THB_OK = 0
 THB_ERR_MODEL = -1
 THB_ERR_CONFIG = -2
@@ -65,6 +67,7 @@ class LayerInfo(ctypes.Structure):
         ("page_len", ctypes.c_uint32),
         ("kv_dtype", ctypes.c_uint32),
         ("plane_elems", ctypes.c_uint64),
+        ("v_page_transposed", ctypes.c_uint32),
     ]
 
 

@@ -1,31 +1,36 @@
-// Paged attention: one launch per call over every row of the batch.
+// Paged attention on gfx950: one launch over every row of the batch.
 //
-// Semantics follow the reference kernel attn.wgsl:53-365: per row i, key j
+// Semantics follow the reference kernel attn.wgsl:53-365: for row i, key j
 // is valid iff (!causal || j <= pos_i) && j >= window_start_i && j < kv_len,
 // with kv_len and window_start exactly as attn.wgsl:78-88 (computed on the
 // host into per-row [lo, hi) ranges).  Softmax in f32, base 2 internally.
 //
-// Work decomposition (MI355X):
-//  * A "group" is a set of query vectors that read the same keys: R rows of
-//    one sequence x H query heads of one KV head (GQA packing: every K/V
-//    byte is read once for all NQ_PER_KV heads).  QV = R*H <= QVM.
-//  * Keys are split into fixed logical partitions of part_len tokens
-//    (split-K).  One workgroup (4 waves) handles one (group, partition, KV
-//    head); each wave a quarter of the partition.  Partition boundaries are
-//    fixed in logical token space, so the arithmetic of a row depends only on
-//    that row: batch == solo and paged == contiguous hold bit-exactly.
-//  * Inside a wave, DL lanes share one token: each lane loads 16 bytes per
-//    token per 64*DL/8 dims (coalesced 128-byte segments), computes partial
-//    dot products, and a DPP butterfly sums them across the DL lanes.
-//  * f16 KV: q is rounded to f16 and QK^T uses v_dot2_f32_f16; PV packs two
-//    tokens' probabilities into one f16x2 and uses v_dot2_f32_f16 as well.
-//    bf16 KV (reference parity): plain f32 FMA after the exact bf16->f32 shift.
-//  * Online softmax with a lazy rescale: the running max only moves when a
-//    score exceeds it by more than 2^8 in probability space.
-//  * The four waves' 4*T partial states are merged through LDS; with more
-//    than one partition the workgroup writes (m, l, o) to scratch and the
-//    last workgroup of the group (atomic arrival counter) merges all
-//    partitions in partition order and writes y.  Counters reset themselves.
+// Work decomposition:
+//  * A "group" holds up to 16 query vectors that read the same keys: R rows
+//    of one sequence x H query heads of one KV head.  Every K/V byte of a
+//    group is loaded once for all of its query vectors (GQA packing).
+//  * Keys are cut into fixed logical partitions of part_len tokens.  One
+//    workgroup of W waves handles one (group, partition, KV head); the waves
+//    split the partition into W contiguous runs of 16-token tiles.  All
+//    boundaries depend only on the group's own key range, so a row's
+//    arithmetic is the same whatever else is in the batch and wherever its
+//    pages sit: batch == solo and paged == contiguous hold bit-exactly.
+//  * Scores come from MFMA: S^T[16 tokens x 16 columns] = K Q^T with
+//    v_mfma_f32_16x16x32_{f16,bf16}.  The A operand is 16 bytes of one key
+//    row per lane (a plain vector load), the B operand is Q^T held in
+//    registers.  Q is split into a high and a low half-precision part and
+//    both are multiplied, which keeps the products at f32 accuracy.
+//  * S^T leaves lane (a, c) holding tokens 4a..4a+3 of column c.  That is
+//    exactly the B-operand layout of v_mfma_f32_16x16x16 for P^T, so the
+//    probabilities feed the PV product without any lane exchange.  The A
+//    operand is V^T: the pool stores V transposed inside each page
+//    ([head_dim][page_len]), so 4 consecutive tokens of one dimension are 8
+//    contiguous bytes.  P is split into high and low halves as well.
+//  * Online softmax per column with a lazy rescale (the running max moves
+//    only when a score beats it by more than 2^8).  The waves' states are
+//    merged through LDS in a fixed tree.  A group split over several
+//    partitions writes (m, l, o) per partition and a second kernel merges
+//    them in partition order; there are no device-wide fences or atomics.
 #include <algorithm>
 #include <string>
 
@@ -34,53 +39,38 @@
 namespace thb {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
 constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units)
 constexpr float kFloor = -1.0e30f;    // initial running max (finite on purpose)
 constexpr uint32_t kGroupWords = 10;  // r0, R, h0, H, seq, lo, hi, n_parts, part0, item0
-constexpr uint32_t kMaxPartPages = 256;
-// Floats in the LDS o-buffer of every variant (SLOTS * QVM * HD == 16384).
-constexpr uint32_t kMergeFloats = 16384;
+constexpr uint32_t kMaxPartPages = 1024;
+constexpr uint32_t kMaxParts = 512;   // partitions of one group the merge kernel takes
+constexpr uint32_t kCols = 16;        // query vectors per group (MFMA N)
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct AttnArgs {
     const void* q;
     void* y;
     const uint32_t* groups;
-    const uint32_t* items;
+    const uint32_t* items;   // work item -> group
     const uint32_t* ranges;  // [m][2]: lo, hi
     const uint32_t* table;
     const uint16_t* k;
     const uint16_t* v;
-    float* part_o;   // [n_items][n_kvh][QVM][hd]
-    float* part_ml;  // [n_items][n_kvh][QVM][2]
-    uint32_t* counters;  // [n_groups][n_kvh]
-    uint64_t plane;  // elements per head plane
+    float* part_o;   // [n_items][n_kvh][16][hd_t]
+    float* part_ml;  // [n_items][n_kvh][16][2]
+    uint64_t plane;  // 16-bit elements per head plane
     uint32_t max_pages, page_shift, q_heads, nq_per_kv, head_dim, part_len, n_kvh;
     float qscale;  // scale * log2(e), or scale / softcap
     float cap2;    // softcap * log2(e), 0 = no soft-cap
     uint32_t q_f16, y_f16;
 };
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float x) {
-    return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF,
-                                                                     false));
-}
-
-// Sum over the DL consecutive lanes that share a token (DL in 8..64).
-template <int DL>
-__device__ __forceinline__ float group_sum(float x) {
-    x = dpp_add<0xB1>(x);   // quad_perm [1,0,3,2]: xor 1
-    x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]: xor 2
-    x = dpp_add<0x141>(x);  // row_half_mirror: sums 8 lanes
-    if constexpr (DL >= 16) x = dpp_add<0x140>(x);  // row_mirror: 16 lanes
-    if constexpr (DL >= 32) x += __shfl_xor(x, 16);
-    if constexpr (DL >= 64) x += __shfl_xor(x, 32);
-    return x;
-}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -90,428 +80,409 @@ __device__ __forceinline__ float tanh_approx(float x) {
     return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
 }
 
-__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
-    half2_t h = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
-    return __builtin_bit_cast(uint32_t, h);
+// Max / sum over the four lanes c, c+16, c+32, c+48 (one MFMA column).
+__device__ __forceinline__ float col_max(float x) {
+    x = fmaxf(x, __shfl_xor(x, 16));
+    return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float col_sum(float x) {
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
 }
 
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c, false);
-}
+// Operand types of one KV encoding.
+template <bool F16>
+struct Ops;
 
-__device__ __forceinline__ float bf_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
-
-__device__ __forceinline__ uint32_t w4(const uint4& v, int i) {
-    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
-
-template <int HD, int QVM, bool F16>
-struct Cfg {
-    static constexpr int DL = HD * QVM / 64;  // lanes per token
-    static constexpr int T = 64 / DL;         // token slots per wave
-    static constexpr int NR = HD / (8 * DL);  // 16-byte chunks per lane per token
-    static constexpr int U = F16 ? 4 : 2;     // tokens per slot per iteration
-    static constexpr int TPI = T * U;         // tokens per wave iteration
-    static constexpr int SLOTS = kWaves * T;  // partial states per workgroup
-    static_assert(NR * QVM == 8, "register budget: o holds 8*NR*QVM/8 floats per lane");
-    static_assert(T * DL == 64, "wave64");
-    static_assert(SLOTS * QVM * HD == kMergeFloats, "LDS o-buffer size");
+template <>
+struct Ops<true> {
+    typedef f16x8 in8;
+    typedef f16x4 in4;
+    // hi + lo split of an f32 (hi = RNE(x), lo = RNE(x - hi)).
+    __device__ static void split(float x, _Float16& h, _Float16& l) {
+        h = static_cast<_Float16>(x);
+        l = static_cast<_Float16>(x - static_cast<float>(h));
+    }
+    __device__ static f32x4 qk(const u32x4& k, const in8& q, f32x4 acc) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(in8, k), q, acc, 0, 0, 0);
+    }
+    __device__ static f32x4 pv(const u32x2& v, const in4& p, f32x4 acc) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(in4, v), p, acc, 0, 0, 0);
+    }
+    __device__ static void split4(const float* p, in4& h, in4& l) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            _Float16 a, b;
+            split(p[e], a, b);
+            h[e] = a;
+            l[e] = b;
+        }
+    }
+    __device__ static void split8(const float* x, in8& h, in8& l) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            _Float16 a, b;
+            split(x[e], a, b);
+            h[e] = a;
+            l[e] = b;
+        }
+    }
 };
 
-template <int HD, int QVM, bool F16>
-__global__ __launch_bounds__(kThreads, 2) void attn_splitk(AttnArgs a) {
-    using C = Cfg<HD, QVM, F16>;
-    constexpr int DL = C::DL, T = C::T, NR = C::NR, U = C::U, TPI = C::TPI, SLOTS = C::SLOTS;
+template <>
+struct Ops<false> {
+    typedef bf16x8 in8;
+    typedef i16x4 in4;
+    __device__ static void split(float x, __bf16& h, __bf16& l) {
+        h = static_cast<__bf16>(x);
+        l = static_cast<__bf16>(x - static_cast<float>(h));
+    }
+    __device__ static f32x4 qk(const u32x4& k, const in8& q, f32x4 acc) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(in8, k), q, acc, 0, 0, 0);
+    }
+    __device__ static f32x4 pv(const u32x2& v, const in4& p, f32x4 acc) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(in4, v), p, acc, 0, 0, 0);
+    }
+    __device__ static void split4(const float* p, in4& h, in4& l) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            __bf16 a, b;
+            split(p[e], a, b);
+            h[e] = __builtin_bit_cast(short, a);
+            l[e] = __builtin_bit_cast(short, b);
+        }
+    }
+    __device__ static void split8(const float* x, in8& h, in8& l) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            __bf16 a, b;
+            split(x[e], a, b);
+            h[e] = a;
+            l[e] = b;
+        }
+    }
+};
 
-    __shared__ float s_o[SLOTS * QVM * HD];
-    __shared__ float s_m[SLOTS * QVM];
-    __shared__ float s_l[SLOTS * QVM];
-    __shared__ float s_w[SLOTS * QVM];
-    __shared__ float s_red[2 * QVM];
+// One (group, partition, KV head) per workgroup of W waves.  DB: the next
+// tile's loads are issued before the current tile is computed.
+template <int HD, bool F16, int W, bool DB>
+__global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
+    using O = Ops<F16>;
+    typedef typename O::in8 in8;
+    typedef typename O::in4 in4;
+    constexpr int KS = HD / 32;  // QK k-steps of 32 dimensions
+    constexpr int MT = HD / 16;  // PV tiles of 16 dimensions
+    constexpr int HALF = W / 2 > 0 ? W / 2 : 1;
+
     __shared__ uint32_t s_page[kMaxPartPages];
-    __shared__ uint32_t s_last;
+    __shared__ f32x4 s_o[HALF][MT][64];
+    __shared__ float s_m[HALF][64];
+    __shared__ float s_l[HALF][64];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
-    const uint32_t slot = lane / DL, li = lane % DL;
+    const uint32_t a4 = lane >> 4, c = lane & 15u;
     const uint32_t item = blockIdx.x, kvh = blockIdx.y;
 
-    const uint32_t gi = a.items[item];
-    const uint32_t* G = a.groups + gi * kGroupWords;
+    const uint32_t* G = a.groups + a.items[item] * kGroupWords;
     const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3], seq = G[4];
     const uint32_t glo = G[5], ghi = G[6], n_parts = G[7], part0 = G[8], item0 = G[9];
     const uint32_t part = part0 + (item - item0);
     const uint32_t P = a.part_len;
     const uint32_t pbeg = part * P;
     const uint32_t tb = max(glo, pbeg), te = min(ghi, pbeg + P);
-    const uint32_t QV = R * H;
     const uint32_t hd = a.head_dim;
-    const uint32_t pmask = (1u << a.page_shift) - 1u;
+    const uint32_t pshift = a.page_shift;
+    const uint32_t pmask = (1u << pshift) - 1u;
 
-    // Block-table entries of this partition (only pages that hold keys).
+    // Physical pages of this partition that hold keys of the group.
     {
-        const uint32_t npg = P >> a.page_shift;
-        const uint32_t lp0 = pbeg >> a.page_shift;
+        const uint32_t npg = P >> pshift;
+        const uint32_t lp0 = pbeg >> pshift;
         const uint32_t* trow = a.table + static_cast<uint64_t>(seq) * a.max_pages;
-        for (uint32_t i = tid; i < npg; i += kThreads) {
+        for (uint32_t i = tid; i < npg; i += 64 * W) {
             const uint32_t lp = lp0 + i;
-            const bool used = tb < te && (lp << a.page_shift) < te && ((lp + 1) << a.page_shift) > tb;
+            const bool used = tb < te && (lp << pshift) < te && ((lp + 1) << pshift) > tb;
             s_page[i] = used ? trow[lp] : 0u;
         }
     }
 
-    // Query vectors and row ranges of this lane's QV slots.
-    uint32_t rlo[QVM], rhi[QVM];
-    uint32_t qh[F16 ? QVM : 1][NR][4];
-    float qf[F16 ? 1 : QVM][NR][8];
-#pragma unroll
-    for (int qv = 0; qv < QVM; qv++) {
-        const bool on = static_cast<uint32_t>(qv) < QV;
-        const uint32_t rr = on ? static_cast<uint32_t>(qv) / H : 0u;
-        const uint32_t hh = on ? static_cast<uint32_t>(qv) - rr * H : 0u;
-        const uint32_t row = r0 + rr;
-        rlo[qv] = on ? a.ranges[2 * row] : 0u;
-        rhi[qv] = on ? a.ranges[2 * row + 1] : 0u;
-        const uint32_t head = kvh * a.nq_per_kv + h0 + hh;
+    // Column c of this lane: row r0 + c / H, head h0 + c % H of the KV head.
+    const uint32_t ncols = R * H;
+    const bool con = c < ncols;
+    const uint32_t rr = con ? c / H : 0u;
+    const uint32_t row = r0 + rr;
+    const uint32_t head = kvh * a.nq_per_kv + h0 + (con ? c - rr * H : 0u);
+    uint32_t clo = 0, chi = 0;
+    if (con) {
+        clo = max(a.ranges[2 * row], tb);
+        chi = min(a.ranges[2 * row + 1], te);
+    }
+
+    // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8] * qscale, split.
+    in8 qh[KS], ql[KS];
+    {
         const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
 #pragma unroll
-        for (int c = 0; c < NR; c++) {
-            const uint32_t d0 = 8u * li + 8u * DL * c;
+        for (int j = 0; j < KS; j++) {
+            const uint32_t d0 = 32u * j + 8u * a4;
             float x[8];
-            if (on && d0 < hd) {
+            if (con && d0 < hd) {
                 if (a.q_f16) {
-                    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qbase + d0);
+                    const f16x8 w = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.q) + qbase + d0);
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        half2_t h2 = __builtin_bit_cast(half2_t, w4(w, j));
-                        x[2 * j] = static_cast<float>(h2.x);
-                        x[2 * j + 1] = static_cast<float>(h2.y);
-                    }
+                    for (int e = 0; e < 8; e++) x[e] = static_cast<float>(w[e]);
                 } else {
-                    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.q) + qbase + d0);
-                    const float4 u0 = p[0], u1 = p[1];
-                    x[0] = u0.x; x[1] = u0.y; x[2] = u0.z; x[3] = u0.w;
-                    x[4] = u1.x; x[5] = u1.y; x[6] = u1.z; x[7] = u1.w;
+                    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + qbase + d0);
+                    const f32x4 u0 = p[0], u1 = p[1];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        x[e] = u0[e];
+                        x[4 + e] = u1[e];
+                    }
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < 8; j++) x[j] = 0.0f;
+                for (int e = 0; e < 8; e++) x[e] = 0.0f;
             }
-            if constexpr (F16) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) qh[qv][c][j] = pack_f16(x[2 * j] * a.qscale, x[2 * j + 1] * a.qscale);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; j++) qf[qv][c][j] = x[j] * a.qscale;
-            }
+            for (int e = 0; e < 8; e++) x[e] *= a.qscale;
+            O::split8(x, qh[j], ql[j]);
         }
     }
     __syncthreads();
 
-    float mq[QVM], lq[QVM], o[QVM][NR * 8];
+    float m = kFloor, l = 0.0f;
+    f32x4 o[MT];
 #pragma unroll
-    for (int qv = 0; qv < QVM; qv++) {
-        mq[qv] = kFloor;
-        lq[qv] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NR * 8; j++) o[qv][j] = 0.0f;
-    }
+    for (int i = 0; i < MT; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // This wave's quarter of the partition, clipped to [tb, te).
-    const uint32_t wq = P / kWaves;
-    const uint32_t wbeg = pbeg + wave * wq, wend = wbeg + wq;
-    const uint32_t lo_c = max(tb, wbeg), hi_c = min(te, wend);
-    const uint32_t it_first = lo_c < hi_c ? (lo_c - wbeg) / TPI : 0u;
-    const uint32_t it_end = lo_c < hi_c ? (hi_c - wbeg + TPI - 1) / TPI : 0u;
+    // This wave's run of 16-token tiles inside [tb, te).
+    const uint32_t tb16 = tb & ~15u;
+    const uint32_t span = te > tb16 ? te - tb16 : 0u;
+    const uint32_t run = ((span + W - 1) / W + 15u) & ~15u;
+    const uint32_t ws = tb16 + wave * run;
+    const uint32_t we = min(ws + run, te);
     const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
     const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
+    const uint32_t last = te > 0 ? te - 1 : 0;
 
-    for (uint32_t it = it_first; it < it_end; it++) {
-        const uint32_t t0 = wbeg + it * TPI;
-        uint4 kr[U][NR], vr[U][NR];
+    // Loads one 16-token tile.  Tokens outside [tb, te) are clamped into
+    // it (their scores are masked), so every address is inside a page of
+    // the sequence.
+    auto load = [&](uint32_t t0, u32x4 (&kr)[KS], u32x2 (&vr)[MT]) {
+        const uint32_t tk = min(max(t0 + c, tb), last);
+        const uint32_t kpage = s_page[(tk - pbeg) >> pshift];
+        const uint16_t* krow = kplane + ((static_cast<uint64_t>(kpage) << pshift) | (tk & pmask)) * hd;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint32_t tok = t0 + u * T + slot;
-            const bool valid = tok >= tb && tok < te;
-            const uint32_t page = s_page[(tok - pbeg) >> a.page_shift];
-            const uint64_t base = ((static_cast<uint64_t>(page) << a.page_shift) | (tok & pmask)) * hd;
+        for (int j = 0; j < KS; j++) {
+            const uint32_t d0 = 32u * j + 8u * a4;
+            kr[j] = d0 < hd ? *reinterpret_cast<const u32x4*>(krow + d0) : u32x4{0u, 0u, 0u, 0u};
+        }
+        const uint32_t tv = min(max(t0 + 4u * a4, tb & ~3u), last & ~3u);
+        const uint32_t vpage = s_page[(tv - pbeg) >> pshift];
+        const uint16_t* vbase = vplane + (static_cast<uint64_t>(vpage) * hd << pshift) + (tv & pmask);
 #pragma unroll
-            for (int c = 0; c < NR; c++) {
-                const uint32_t d0 = 8u * li + 8u * DL * c;
-                if (valid && d0 < hd) {
-                    kr[u][c] = *reinterpret_cast<const uint4*>(kplane + base + d0);
-                    vr[u][c] = *reinterpret_cast<const uint4*>(vplane + base + d0);
-                } else {
-                    kr[u][c] = make_uint4(0, 0, 0, 0);
-                    vr[u][c] = make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < MT; i++) {
+            const uint32_t d = 16u * i + c;
+            vr[i] = d < hd ? *reinterpret_cast<const u32x2*>(vbase + (static_cast<uint64_t>(d) << pshift))
+                           : u32x2{0u, 0u};
+        }
+    };
+
+    auto compute = [&](uint32_t t0, const u32x4 (&kr)[KS], const u32x2 (&vr)[MT]) {
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            s = O::qk(kr[j], qh[j], s);
+            s = O::qk(kr[j], ql[j], s);
+        }
+        float sv[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float x = s[e];
+            if (a.cap2 != 0.0f) x = a.cap2 * tanh_approx(x);
+            const uint32_t t = t0 + 4u * a4 + e;
+            x = (t >= clo && t < chi) ? x : -INFINITY;
+            sv[e] = x;
+            mx = fmaxf(mx, x);
+        }
+        mx = col_max(mx);
+        if (mx > m + kTau) {
+            const float alpha = fast_exp2(m - mx);
+            l *= alpha;
+#pragma unroll
+            for (int i = 0; i < MT; i++) o[i] *= alpha;
+            m = mx;
+        }
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            p[e] = fast_exp2(sv[e] - m);
+            l += p[e];
+        }
+        in4 ph, pl;
+        O::split4(p, ph, pl);
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            o[i] = O::pv(vr[i], ph, o[i]);
+            o[i] = O::pv(vr[i], pl, o[i]);
+        }
+    };
+
+    if constexpr (DB) {
+        if (ws < we) {
+            u32x4 kA[KS], kB[KS];
+            u32x2 vA[MT], vB[MT];
+            load(ws, kA, vA);
+            if (ws + 16 < we) load(ws + 16, kB, vB);
+            for (uint32_t t0 = ws; t0 < we; t0 += 32) {
+                compute(t0, kA, vA);
+                if (t0 + 32 < we) load(t0 + 32, kA, vA);
+                if (t0 + 16 < we) {
+                    compute(t0 + 16, kB, vB);
+                    if (t0 + 48 < we) load(t0 + 48, kB, vB);
                 }
             }
         }
-
-        // Scores s[u][qv] (log2 domain), summed over the DL lanes of a token.
-        float s[U][QVM];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-#pragma unroll
-            for (int qv = 0; qv < QVM; qv++) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int c = 0; c < NR; c++) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        if constexpr (F16) {
-                            acc = dot2(qh[qv][c][j], w4(kr[u][c], j), acc);
-                        } else {
-                            const uint32_t w = w4(kr[u][c], j);
-                            acc = fmaf(qf[qv][c][2 * j], bf_lo(w), acc);
-                            acc = fmaf(qf[qv][c][2 * j + 1], bf_hi(w), acc);
-                        }
-                    }
-                }
-                s[u][qv] = group_sum<DL>(acc);
-            }
-        }
-
-        float p[U][QVM];
-#pragma unroll
-        for (int qv = 0; qv < QVM; qv++) {
-            float mx = kFloor;
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const uint32_t tok = t0 + u * T + slot;
-                float x = s[u][qv];
-                if (a.cap2 != 0.0f) x = a.cap2 * tanh_approx(x);
-                const bool ok = tok >= rlo[qv] && tok < rhi[qv];
-                x = ok ? x : -INFINITY;
-                s[u][qv] = x;
-                mx = fmaxf(mx, x);
-            }
-            if (mx > mq[qv] + kTau) {
-                const float alpha = fast_exp2(mq[qv] - mx);
-                lq[qv] *= alpha;
-#pragma unroll
-                for (int j = 0; j < NR * 8; j++) o[qv][j] *= alpha;
-                mq[qv] = mx;
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) p[u][qv] = fast_exp2(s[u][qv] - mq[qv]);
-        }
-
-        if constexpr (F16) {
-#pragma unroll
-            for (int pr = 0; pr < U / 2; pr++) {
-                uint32_t pp[QVM];
-#pragma unroll
-                for (int qv = 0; qv < QVM; qv++) {
-                    pp[qv] = pack_f16(p[2 * pr][qv], p[2 * pr + 1][qv]);
-                    lq[qv] = dot2(pp[qv], 0x3C003C00u, lq[qv]);  // + both rounded weights
-                }
-#pragma unroll
-                for (int c = 0; c < NR; c++) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const uint32_t va = w4(vr[2 * pr][c], j), vb = w4(vr[2 * pr + 1][c], j);
-                        const uint32_t vlo = __builtin_amdgcn_perm(vb, va, 0x05040100u);  // (va.lo, vb.lo)
-                        const uint32_t vhi = __builtin_amdgcn_perm(vb, va, 0x07060302u);  // (va.hi, vb.hi)
-#pragma unroll
-                        for (int qv = 0; qv < QVM; qv++) {
-                            o[qv][c * 8 + 2 * j] = dot2(pp[qv], vlo, o[qv][c * 8 + 2 * j]);
-                            o[qv][c * 8 + 2 * j + 1] = dot2(pp[qv], vhi, o[qv][c * 8 + 2 * j + 1]);
-                        }
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-#pragma unroll
-                for (int qv = 0; qv < QVM; qv++) lq[qv] += p[u][qv];
-#pragma unroll
-                for (int c = 0; c < NR; c++) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const uint32_t w = w4(vr[u][c], j);
-                        const float v0 = bf_lo(w), v1 = bf_hi(w);
-#pragma unroll
-                        for (int qv = 0; qv < QVM; qv++) {
-                            o[qv][c * 8 + 2 * j] = fmaf(p[u][qv], v0, o[qv][c * 8 + 2 * j]);
-                            o[qv][c * 8 + 2 * j + 1] = fmaf(p[u][qv], v1, o[qv][c * 8 + 2 * j + 1]);
-                        }
-                    }
-                }
-            }
+    } else {
+        for (uint32_t t0 = ws; t0 < we; t0 += 16) {
+            u32x4 kA[KS];
+            u32x2 vA[MT];
+            load(t0, kA, vA);
+            compute(t0, kA, vA);
         }
     }
+    l = col_sum(l);
 
-    // ---- merge the workgroup's SLOTS partial states through LDS ----------
-    const uint32_t sidx = wave * T + slot;
+    // ---- merge the W waves' states through LDS (fixed tree) -------------
+    for (uint32_t half = W / 2; half >= 1; half >>= 1) {
+        if (wave >= half && wave < 2 * half) {
+            const uint32_t sl = wave - half;
 #pragma unroll
-    for (int qv = 0; qv < QVM; qv++) {
-        if (li == 0) {
-            s_m[sidx * QVM + qv] = mq[qv];
-            s_l[sidx * QVM + qv] = lq[qv];
+            for (int i = 0; i < MT; i++) s_o[sl][i][lane] = o[i];
+            s_m[sl][lane] = m;
+            s_l[sl][lane] = l;
         }
+        __syncthreads();
+        if (wave < half) {
+            const float m2 = s_m[wave][lane], l2 = s_l[wave][lane];
+            const float M = fmaxf(m, m2);
+            const float f1 = fast_exp2(m - M), f2 = fast_exp2(m2 - M);
 #pragma unroll
-        for (int c = 0; c < NR; c++) {
-            const uint32_t d0 = 8u * li + 8u * DL * c;
-            float4* dst = reinterpret_cast<float4*>(s_o + (sidx * QVM + qv) * HD + d0);
-            dst[0] = make_float4(o[qv][c * 8 + 0], o[qv][c * 8 + 1], o[qv][c * 8 + 2], o[qv][c * 8 + 3]);
-            dst[1] = make_float4(o[qv][c * 8 + 4], o[qv][c * 8 + 5], o[qv][c * 8 + 6], o[qv][c * 8 + 7]);
+            for (int i = 0; i < MT; i++) o[i] = o[i] * f1 + s_o[wave][i][lane] * f2;
+            l = l * f1 + l2 * f2;
+            m = M;
         }
+        __syncthreads();
     }
-    __syncthreads();
-    if (tid < static_cast<uint32_t>(QVM)) {
-        float M = kFloor;
-        for (int sl = 0; sl < SLOTS; sl++) M = fmaxf(M, s_m[sl * QVM + tid]);
-        float L = 0.0f;
-        for (int sl = 0; sl < SLOTS; sl++) {
-            const float w = fast_exp2(s_m[sl * QVM + tid] - M);
-            s_w[sl * QVM + tid] = w;
-            L += w * s_l[sl * QVM + tid];
-        }
-        s_red[2 * tid] = M;
-        s_red[2 * tid + 1] = L;
-    }
-    __syncthreads();
+    if (wave != 0 || !con) return;
 
-    const uint32_t nout = QV * hd;
     if (n_parts == 1) {
-        for (uint32_t idx = tid; idx < nout; idx += kThreads) {
-            const uint32_t qv = idx / hd, d = idx - qv * hd;
-            float acc = 0.0f;
-            for (int sl = 0; sl < SLOTS; sl++) acc += s_w[sl * QVM + qv] * s_o[(sl * QVM + qv) * HD + d];
-            const float yv = acc / s_red[2 * qv + 1];
-            const uint32_t rr = qv / H, hh = qv - rr * H;
-            const uint64_t yi = (static_cast<uint64_t>(r0 + rr) * a.q_heads + kvh * a.nq_per_kv + h0 + hh) * hd + d;
-            if (a.y_f16)
-                static_cast<_Float16*>(a.y)[yi] = static_cast<_Float16>(yv);
-            else
-                static_cast<float*>(a.y)[yi] = yv;
+        const float inv = 1.0f / l;
+        const uint64_t ybase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            const uint32_t d = 16u * i + 4u * a4;
+            if (d >= hd) continue;
+            const f32x4 yv = o[i] * inv;
+            if (a.y_f16) {
+                f16x4 h;
+#pragma unroll
+                for (int e = 0; e < 4; e++) h[e] = static_cast<_Float16>(yv[e]);
+                *reinterpret_cast<f16x4*>(static_cast<_Float16*>(a.y) + ybase + d) = h;
+            } else {
+                *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + ybase + d) = yv;
+            }
         }
         return;
     }
+    // Several partitions: publish this one's (m, l, o); the merge kernel
+    // combines them after this kernel has finished.
+    const uint64_t pb = (static_cast<uint64_t>(item) * a.n_kvh + kvh) * kCols + c;
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+        *reinterpret_cast<f32x4*>(a.part_o + pb * HD + 16u * i + 4u * a4) = o[i];
+    if (a4 == 0) {
+        a.part_ml[2 * pb] = m;
+        a.part_ml[2 * pb + 1] = l;
+    }
+}
 
-    // ---- several partitions: publish (m, l, o), last arrival merges -------
-    const uint64_t pbase = (static_cast<uint64_t>(item) * a.n_kvh + kvh) * QVM;
-    for (uint32_t idx = tid; idx < nout; idx += kThreads) {
-        const uint32_t qv = idx / hd, d = idx - qv * hd;
-        float acc = 0.0f;
-        for (int sl = 0; sl < SLOTS; sl++) acc += s_w[sl * QVM + qv] * s_o[(sl * QVM + qv) * HD + d];
-        a.part_o[(pbase + qv) * hd + d] = acc;
-    }
-    if (tid < QV) {
-        a.part_ml[2 * (pbase + tid)] = s_red[2 * tid];
-        a.part_ml[2 * (pbase + tid) + 1] = s_red[2 * tid + 1];
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(a.counters + static_cast<uint64_t>(gi) * a.n_kvh + kvh, 1u);
-        s_last = prev == n_parts - 1 ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    // Merge every partition of the group in partition order.  Partition pi
-    // is read by thread pi % 256; the max and the sum are reduced with a
-    // fixed shuffle tree, so the result is deterministic.
-    float* s_pw = s_o;                      // [n_parts][QVM] weights
-    float* s_wr = s_o + kMergeFloats - kWaves * QVM;  // [kWaves][QVM]
-    const uint64_t gbase = static_cast<uint64_t>(item0) * a.n_kvh;
-    auto ml_at = [&](uint32_t pi, uint32_t qv) {
-        return ((gbase + static_cast<uint64_t>(pi) * a.n_kvh + kvh) * QVM + qv) * 2;
-    };
-    float red[QVM];
-#pragma unroll
-    for (int qv = 0; qv < QVM; qv++) red[qv] = kFloor;
-    for (uint32_t pi = tid; pi < n_parts; pi += kThreads)
-#pragma unroll
-        for (int qv = 0; qv < QVM; qv++)
-            if (static_cast<uint32_t>(qv) < QV) red[qv] = fmaxf(red[qv], __builtin_nontemporal_load(a.part_ml + ml_at(pi, qv)));
-#pragma unroll
-    for (int qv = 0; qv < QVM; qv++) {
-        float x = red[qv];
-        for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-        if (lane == 0) s_wr[wave * QVM + qv] = x;
-    }
-    __syncthreads();
-    float Mq[QVM];
-#pragma unroll
-    for (int qv = 0; qv < QVM; qv++) {
-        Mq[qv] = fmaxf(fmaxf(s_wr[qv], s_wr[QVM + qv]), fmaxf(s_wr[2 * QVM + qv], s_wr[3 * QVM + qv]));
-        red[qv] = 0.0f;
-    }
-    __syncthreads();
-    for (uint32_t pi = tid; pi < n_parts; pi += kThreads)
-#pragma unroll
-        for (int qv = 0; qv < QVM; qv++) {
-            float w = 0.0f;
-            if (static_cast<uint32_t>(qv) < QV) {
-                const uint64_t b = ml_at(pi, qv);
-                w = fast_exp2(__builtin_nontemporal_load(a.part_ml + b) - Mq[qv]);
-                red[qv] += w * __builtin_nontemporal_load(a.part_ml + b + 1);
-            }
-            s_pw[pi * QVM + qv] = w;
+// Merges the partitions of every group that has more than one, in
+// partition order.  One workgroup per (group, KV head).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
+    __shared__ float s_w[kMaxParts * kCols];
+    __shared__ float s_inv[kCols];
+    const uint32_t g = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const uint32_t* G = a.groups + g * kGroupWords;
+    const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3];
+    const uint32_t n_parts = G[7], item0 = G[9];
+    if (n_parts <= 1) return;
+    const uint32_t ncols = R * H;
+    const uint32_t hd = a.head_dim;
+    const uint64_t base = static_cast<uint64_t>(item0) * a.n_kvh + kvh;  // partition pi: base + pi * n_kvh
+    if (tid < ncols) {
+        float M = kFloor;
+        for (uint32_t pi = 0; pi < n_parts; pi++)
+            M = fmaxf(M, a.part_ml[2 * ((base + static_cast<uint64_t>(pi) * a.n_kvh) * kCols + tid)]);
+        float L = 0.0f;
+        for (uint32_t pi = 0; pi < n_parts; pi++) {
+            const uint64_t b = 2 * ((base + static_cast<uint64_t>(pi) * a.n_kvh) * kCols + tid);
+            const float w = fast_exp2(a.part_ml[b] - M);
+            s_w[pi * kCols + tid] = w;
+            L += w * a.part_ml[b + 1];
         }
-#pragma unroll
-    for (int qv = 0; qv < QVM; qv++) {
-        float x = red[qv];
-        for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-        if (lane == 0) s_wr[wave * QVM + qv] = x;
+        s_inv[tid] = 1.0f / L;
     }
     __syncthreads();
-    for (uint32_t idx = tid; idx < nout; idx += kThreads) {
-        const uint32_t qv = idx / hd, d = idx - qv * hd;
-        const float L = ((s_wr[qv] + s_wr[QVM + qv]) + s_wr[2 * QVM + qv]) + s_wr[3 * QVM + qv];
-        const float* src = a.part_o + (gbase * QVM + kvh * QVM + qv) * hd + d;
-        const uint64_t step = static_cast<uint64_t>(a.n_kvh) * QVM * hd;
+    const uint64_t step = static_cast<uint64_t>(a.n_kvh) * kCols * HD;
+    for (uint32_t idx = tid; idx < ncols * hd; idx += 256) {
+        const uint32_t c = idx / hd, d = idx - c * hd;
+        const float* src = a.part_o + (base * kCols + c) * HD + d;
         float acc = 0.0f;
-        uint32_t pi = 0;
-        for (; pi + 8 <= n_parts; pi += 8) {
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) x[j] = __builtin_nontemporal_load(src + (pi + j) * step);
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc += s_pw[(pi + j) * QVM + qv] * x[j];
-        }
-        for (; pi < n_parts; pi++) acc += s_pw[pi * QVM + qv] * __builtin_nontemporal_load(src + pi * step);
-        const float yv = acc / L;
-        const uint32_t rr = qv / H, hh = qv - rr * H;
+        for (uint32_t pi = 0; pi < n_parts; pi++) acc += s_w[pi * kCols + c] * src[pi * step];
+        const float yv = acc * s_inv[c];
+        const uint32_t rr = c / H, hh = c - rr * H;
         const uint64_t yi = (static_cast<uint64_t>(r0 + rr) * a.q_heads + kvh * a.nq_per_kv + h0 + hh) * hd + d;
         if (a.y_f16)
             static_cast<_Float16*>(a.y)[yi] = static_cast<_Float16>(yv);
         else
             static_cast<float*>(a.y)[yi] = yv;
     }
-    if (tid == 0) a.counters[static_cast<uint64_t>(gi) * a.n_kvh + kvh] = 0u;
 }
 
 // ------------------------------------------------------------ host side
-struct Variant {
-    uint32_t hd_t, qvm;
-};
-
 uint32_t template_hd(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : hd <= 256 ? 256 : 512; }
 
-template <int HD, int QVM>
-void launch_one(bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
-    if (f16)
-        hipLaunchKernelGGL((attn_splitk<HD, QVM, true>), grid, dim3(kThreads), 0, s, a);
-    else
-        hipLaunchKernelGGL((attn_splitk<HD, QVM, false>), grid, dim3(kThreads), 0, s, a);
+// Waves per workgroup of each head_dim template: 8 waves (2 per SIMD, 256
+// registers each) up to head_dim 128; 4 waves (512 registers each) above,
+// where the query, output and load registers grow with head_dim.
+constexpr int waves_for(int hd) { return hd >= 256 ? 4 : 8; }
+
+template <int HD, bool F16>
+void launch_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
+    constexpr int W = waves_for(HD);
+    hipLaunchKernelGGL((attn_mfma<HD, F16, W, (HD <= 256)>), grid, dim3(64 * W), 0, s, a);
 }
 
-void launch(const Variant& v, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
-    switch (v.hd_t * 16 + v.qvm) {
-        case 64 * 16 + 8: launch_one<64, 8>(f16, grid, a, s); break;
-        case 128 * 16 + 4: launch_one<128, 4>(f16, grid, a, s); break;
-        case 128 * 16 + 8: launch_one<128, 8>(f16, grid, a, s); break;
-        case 256 * 16 + 4: launch_one<256, 4>(f16, grid, a, s); break;
-        case 256 * 16 + 8: launch_one<256, 8>(f16, grid, a, s); break;
-        case 512 * 16 + 4: launch_one<512, 4>(f16, grid, a, s); break;
-        default: launch_one<512, 8>(f16, grid, a, s); break;
+void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
+    switch (hd_t) {
+        case 64: f16 ? launch_hd<64, true>(grid, a, s) : launch_hd<64, false>(grid, a, s); break;
+        case 128: f16 ? launch_hd<128, true>(grid, a, s) : launch_hd<128, false>(grid, a, s); break;
+        case 256: f16 ? launch_hd<256, true>(grid, a, s) : launch_hd<256, false>(grid, a, s); break;
+        default: f16 ? launch_hd<512, true>(grid, a, s) : launch_hd<512, false>(grid, a, s); break;
+    }
+}
+
+void launch_merge(uint32_t hd_t, dim3 grid, const AttnArgs& a, hipStream_t s) {
+    switch (hd_t) {
+        case 64: hipLaunchKernelGGL(attn_merge<64>, grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL(attn_merge<128>, grid, dim3(256), 0, s, a); break;
+        case 256: hipLaunchKernelGGL(attn_merge<256>, grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(attn_merge<512>, grid, dim3(256), 0, s, a); break;
     }
 }
 
@@ -579,15 +550,10 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
                                            std::to_string(rp.hi[r]));
     }
 
-    // Variant: QVM = 4 when every group is a single decode row with G <= 4.
-    const uint32_t hd_t = template_hd(hd);
-    uint32_t max_chunk = 0;
-    for (auto& c : rp.chunks) max_chunk = std::max(max_chunk, c.second - c.first);
-    uint32_t qvm = (max_chunk == 1 && G <= 4 && hd_t >= 128) ? 4u : 8u;
-
     std::vector<uint32_t> groups, items;
     const uint32_t P = pool->part_len;
     uint32_t max_parts = 0;
+    bool any_split = false;
     auto add_group = [&](uint32_t r0, uint32_t R, uint32_t h0, uint32_t H, uint32_t seq) {
         uint32_t lo = 0xFFFFFFFFu, hi = 0;
         for (uint32_t r = r0; r < r0 + R; r++) {
@@ -597,7 +563,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         }
         uint32_t part0, n_parts;
         if (hi <= lo || lo == 0xFFFFFFFFu) {
-            lo = hi = 0;  // no keys: one empty partition, output 0/0 like the reference
+            lo = hi = 0;  // no keys: one empty partition, output 0/0 = NaN
             part0 = 0;
             n_parts = 1;
         } else {
@@ -605,6 +571,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
             n_parts = (hi - 1) / P - part0 + 1;
         }
         max_parts = std::max(max_parts, n_parts);
+        any_split = any_split || n_parts > 1;
         const uint32_t gidx = static_cast<uint32_t>(groups.size() / kGroupWords);
         const uint32_t item0 = static_cast<uint32_t>(items.size());
         groups.insert(groups.end(), {r0, R, h0, H, seq, lo, hi, n_parts, part0, item0});
@@ -612,19 +579,21 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     };
     for (auto& c : rp.chunks) {
         const uint32_t seq = rp.seq[c.first];
-        if (G <= qvm) {
-            const uint32_t rg = qvm / G;
+        if (G <= kCols) {
+            const uint32_t rg = kCols / G;
             for (uint32_t r = c.first; r < c.second; r += rg) add_group(r, std::min(rg, c.second - r), 0, G, seq);
         } else {
             for (uint32_t r = c.first; r < c.second; r++)
-                for (uint32_t h0 = 0; h0 < G; h0 += qvm) add_group(r, 1, h0, std::min(qvm, G - h0), seq);
+                for (uint32_t h0 = 0; h0 < G; h0 += kCols) add_group(r, 1, h0, std::min(kCols, G - h0), seq);
         }
     }
+    if (max_parts > kMaxParts)
+        return fail(THB_ERR_CONFIG, "context of " + std::to_string(static_cast<uint64_t>(max_parts) * P) +
+                                        " tokens exceeds " + std::to_string(kMaxParts) + " partitions of " +
+                                        std::to_string(P) + " tokens");
     const uint32_t n_groups = static_cast<uint32_t>(groups.size() / kGroupWords);
     const uint32_t n_items = static_cast<uint32_t>(items.size());
-    if ((static_cast<uint64_t>(max_parts) + kWaves) * qvm > kMergeFloats)
-        return fail(THB_ERR_CONFIG, "context of " + std::to_string(static_cast<uint64_t>(max_parts) * P) +
-                                        " tokens exceeds the merge capacity of this part_len");
+    if (n_items > 0x7FFFFFFFu || n_groups > 0x7FFFFFFFu) return fail(THB_ERR_CONFIG, "attention call too large");
 
     std::vector<uint32_t> blob;
     blob.reserve(groups.size() + items.size() + 2 * m);
@@ -638,8 +607,8 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     pool->stager.upload(dev, blob.data(), blob.size() * 4, stream);
     plan.n_groups = n_groups;
     plan.n_items = n_items;
-    plan.qv_max = qvm;
-    plan.variant = hd_t * 16 + qvm;
+    plan.split = any_split;
+    plan.hd_t = template_hd(hd);
     return THB_OK;
 }
 
@@ -662,8 +631,8 @@ extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, 
                                         std::to_string(pool->kv_heads));
     if (sp.q_dtype > THB_DT_F16 || sp.y_dtype > THB_DT_F16)
         return fail(THB_ERR_INVALID, "q_dtype and y_dtype must be THB_DT_F32 or THB_DT_F16");
-    if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(y) & 3u))
-        return fail(THB_ERR_INVALID, "q must be 16-byte aligned and y 4-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u))
+        return fail(THB_ERR_INVALID, "q and y must be 16-byte aligned");
     if (static_cast<uint64_t>(sp.row_off) + sp.m > rows->m)
         return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(rows->m) + " rows, call needs " +
                                          std::to_string(static_cast<uint64_t>(sp.row_off) + sp.m));
@@ -706,12 +675,17 @@ extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, 
         }
         plan->last_use = ++pool->plan_clock;
 
-        const uint32_t qvm = plan->qv_max;
-        const uint64_t n_part = static_cast<uint64_t>(plan->n_items) * pool->kv_heads * qvm;
-        const uint64_t o_bytes = n_part * hd * 4, ml_bytes = n_part * 8;
-        uint8_t* part = static_cast<uint8_t*>(pool->partials.reserve(o_bytes + ml_bytes + 256, false));
-        uint32_t* cnt = static_cast<uint32_t*>(
-            pool->counters.reserve(static_cast<uint64_t>(plan->n_groups) * pool->kv_heads * 4, true));
+        const uint32_t hd_t = plan->hd_t;
+        const bool split = plan->split;
+        float* part_o = nullptr;
+        float* part_ml = nullptr;
+        if (split) {
+            const uint64_t n_part = static_cast<uint64_t>(plan->n_items) * pool->kv_heads * kCols;
+            const uint64_t o_bytes = (n_part * hd_t * 4 + 255) & ~uint64_t(255), ml_bytes = n_part * 8;
+            uint8_t* part = static_cast<uint8_t*>(pool->partials.reserve(o_bytes + ml_bytes, false));
+            part_o = reinterpret_cast<float*>(part);
+            part_ml = reinterpret_cast<float*>(part + o_bytes);
+        }
 
         const uint32_t* blob = static_cast<const uint32_t*>(plan->dev.get());
         const LayerGeom& g = pool->geom[layer];
@@ -724,9 +698,8 @@ extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, 
         a.table = pool->table_dev;
         a.k = reinterpret_cast<const uint16_t*>(pool->mem + g.k_off);
         a.v = reinterpret_cast<const uint16_t*>(pool->mem + g.v_off);
-        a.part_o = reinterpret_cast<float*>(part);
-        a.part_ml = reinterpret_cast<float*>(part + ((o_bytes + 255) & ~uint64_t(255)));
-        a.counters = cnt;
+        a.part_o = part_o;
+        a.part_ml = part_ml;
         a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
         a.max_pages = pool->arena.a.max_pages();
         a.page_shift = pool->page_shift;
@@ -745,9 +718,13 @@ extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, 
         }
         a.q_f16 = sp.q_dtype == THB_DT_F16;
         a.y_f16 = sp.y_dtype == THB_DT_F16;
-        Variant v{template_hd(hd), qvm};
-        launch(v, pool->kv_dtype == THB_KV_F16_RNE, dim3(plan->n_items, pool->kv_heads), a, s);
+        const bool f16 = pool->kv_dtype == THB_KV_F16_RNE;
+        launch(hd_t, f16, dim3(plan->n_items, pool->kv_heads), a, s);
         THB_HIP(hipGetLastError());
+        if (split) {
+            launch_merge(hd_t, dim3(plan->n_groups, pool->kv_heads), a, s);
+            THB_HIP(hipGetLastError());
+        }
         return THB_OK;
     });
 }

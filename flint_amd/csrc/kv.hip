@@ -1,8 +1,10 @@
 // KV append/scatter (kv_store), gather, scatter and page copy kernels.
 //
-// All four move 16-byte vectors: one lane owns 8 consecutive head_dim
-// elements of one token of one head, so a wave touches whole 128-byte lines
-// of a token row and every store is a single global_store_dwordx4.
+// One lane owns 8 consecutive head_dim elements of one token of one head.
+// K rows are token-major, so a K access is one 16-byte vector.  V pages are
+// stored transposed ([head_dim][page_len] per page, the operand layout of
+// the attention kernel's PV product), so the lane's 8 V elements are 8
+// 16-bit accesses page_len elements apart.
 #include <string>
 
 #include "pool.hpp"
@@ -127,8 +129,20 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
     const uint32_t h = c / cph, d = (c - h * cph) << 3;
     const uint64_t src_e = (static_cast<uint64_t>(row) * a.chunks + c) << 3;
     const uint4 w = load_encode8<SRC, KV>(is_v ? a.v_src : a.k_src, src_e);
-    uint16_t* dst = (is_v ? a.v : a.k) + h * a.plane + slot * a.head_dim + d;
-    *reinterpret_cast<uint4*>(dst) = w;
+    if (!is_v) {
+        *reinterpret_cast<uint4*>(a.k + h * a.plane + slot * a.head_dim + d) = w;
+        return;
+    }
+    // V^T: element (slot, d + e) of the page lives at (page * hd + d + e) *
+    // page_len + slot % page_len.
+    uint16_t* dst = a.v + h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + d) << a.page_shift) +
+                    (pos & ((1u << a.page_shift) - 1u));
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t x = e == 0 ? w.x : e == 1 ? w.y : e == 2 ? w.z : w.w;
+        dst[static_cast<uint64_t>(2 * e) << a.page_shift] = static_cast<uint16_t>(x & 0xffffu);
+        dst[static_cast<uint64_t>(2 * e + 1) << a.page_shift] = static_cast<uint16_t>(x >> 16);
+    }
 }
 
 struct GatherArgs {
@@ -153,13 +167,35 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     const uint32_t h = r / cph, d = (r - h * cph) << 3;
     const uint32_t pos = a.t0 + t;
     const uint32_t page = a.table_row[pos >> a.page_shift];
-    const uint64_t slot = (static_cast<uint64_t>(page) << a.page_shift) | (pos & ((1u << a.page_shift) - 1u));
-    uint16_t* paged = (blockIdx.y ? a.v : a.k) + h * a.plane + slot * a.head_dim + d;
-    uint16_t* flat = (blockIdx.y ? a.v_flat : a.k_flat) + (static_cast<uint64_t>(h) * a.n + t) * a.head_dim + d;
-    if constexpr (TO_FLAT)
-        *reinterpret_cast<uint4*>(flat) = *reinterpret_cast<const uint4*>(paged);
-    else
-        *reinterpret_cast<uint4*>(paged) = *reinterpret_cast<const uint4*>(flat);
+    const uint32_t j = pos & ((1u << a.page_shift) - 1u);
+    const uint64_t slot = (static_cast<uint64_t>(page) << a.page_shift) | j;
+    if (blockIdx.y == 0) {
+        uint16_t* paged = a.k + h * a.plane + slot * a.head_dim + d;
+        uint16_t* flat = a.k_flat + (static_cast<uint64_t>(h) * a.n + t) * a.head_dim + d;
+        if constexpr (TO_FLAT)
+            *reinterpret_cast<uint4*>(flat) = *reinterpret_cast<const uint4*>(paged);
+        else
+            *reinterpret_cast<uint4*>(paged) = *reinterpret_cast<const uint4*>(flat);
+        return;
+    }
+    uint16_t* paged = a.v + h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + d) << a.page_shift) + j;
+    uint16_t* flat = a.v_flat + (static_cast<uint64_t>(h) * a.n + t) * a.head_dim + d;
+    if constexpr (TO_FLAT) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            w[e] = static_cast<uint32_t>(paged[static_cast<uint64_t>(2 * e) << a.page_shift]) |
+                   (static_cast<uint32_t>(paged[static_cast<uint64_t>(2 * e + 1) << a.page_shift]) << 16);
+        *reinterpret_cast<uint4*>(flat) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(flat);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t x = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+            paged[static_cast<uint64_t>(2 * e) << a.page_shift] = static_cast<uint16_t>(x & 0xffffu);
+            paged[static_cast<uint64_t>(2 * e + 1) << a.page_shift] = static_cast<uint16_t>(x >> 16);
+        }
+    }
 }
 
 struct CopyArgs {
@@ -170,8 +206,10 @@ struct CopyArgs {
     uint32_t kv_heads, page_len;
 };
 
-// Page copy for every layer, K and V, every head.  Grid: (ceil(page_len *
-// max_head_dim / 8 / 256), n_triples, layers * 2 * kv_heads).
+// Copy of slots [0, ntok) of a page for every layer, K and V, every head.
+// Grid: (ceil(page_len * max_head_dim / 256), n_triples, layers * 2 *
+// kv_heads).  A K page and a whole V page are contiguous and move as 16-byte
+// vectors; a partial V page moves element by element ([head_dim][page_len]).
 __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
     const uint32_t z = blockIdx.z;
     const uint32_t h = z % a.kv_heads;
@@ -181,12 +219,21 @@ __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
     const uint32_t src = a.triples[3 * blockIdx.y], dst = a.triples[3 * blockIdx.y + 1];
     const uint32_t ntok = a.triples[3 * blockIdx.y + 2];
     const uint32_t c = blockIdx.x * 256 + threadIdx.x;
-    if (static_cast<uint64_t>(c) * 8 >= static_cast<uint64_t>(ntok) * L.head_dim) return;
     uint16_t* base = reinterpret_cast<uint16_t*>(a.mem + (which ? L.v_off : L.k_off)) +
                      static_cast<uint64_t>(h) * a.pool_len * L.head_dim;
-    const uint64_t off = static_cast<uint64_t>(c) * 8;
-    const uint4 w = *reinterpret_cast<const uint4*>(base + static_cast<uint64_t>(src) * a.page_len * L.head_dim + off);
-    *reinterpret_cast<uint4*>(base + static_cast<uint64_t>(dst) * a.page_len * L.head_dim + off) = w;
+    const uint64_t page_elems = static_cast<uint64_t>(a.page_len) * L.head_dim;
+    const uint16_t* sp = base + static_cast<uint64_t>(src) * page_elems;
+    uint16_t* dp = base + static_cast<uint64_t>(dst) * page_elems;
+    if (which == 0 || ntok == a.page_len) {
+        if (static_cast<uint64_t>(c) * 8 >= static_cast<uint64_t>(ntok) * L.head_dim) return;
+        const uint64_t off = static_cast<uint64_t>(c) * 8;
+        *reinterpret_cast<uint4*>(dp + off) = *reinterpret_cast<const uint4*>(sp + off);
+        return;
+    }
+    if (c >= ntok * L.head_dim) return;
+    const uint32_t d = c / ntok, j = c - d * ntok;
+    const uint64_t off = static_cast<uint64_t>(d) * a.page_len + j;
+    dp[off] = sp[off];
 }
 
 template <uint32_t SRC>
@@ -228,7 +275,7 @@ void launch_block_copy(thb_pool* p, const uint32_t* triples_dev, uint32_t n, uin
     for (const auto& g : p->geom) max_hd = std::max(max_hd, g.head_dim);
     CopyArgs a{p->mem, static_cast<const DevLayer*>(p->geom_buf.get()), triples_dev,
                static_cast<uint64_t>(p->arena.a.pages()) * p->page_len, p->kv_heads, p->page_len};
-    const uint32_t chunks = (max_tokens * max_hd / 8 + 255) / 256;
+    const uint32_t chunks = (max_tokens * max_hd + 255) / 256;
     const uint32_t planes = p->layers * 2 * p->kv_heads;
     if (planes > kMaxGridY) throw HipError{hipErrorInvalidConfiguration, "block copy: layers*2*kv_heads > 65535"};
     for (uint32_t i0 = 0; i0 < n; i0 += kMaxGridY) {

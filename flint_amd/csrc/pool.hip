@@ -1,10 +1,13 @@
 // C ABI of the host allocator, the device pool and the row metadata.
 //
-// Device layout: one allocation holds, for every layer, K then V, each
-// [kv_heads, pool_len, head_dim] 16-bit words (the KvPool layout,
-// reference crates/thuban_model/src/pool.rs:131-153), every plane aligned
-// to 256 bytes.  The block table [seqs * max_pages] u32 lives in its own
-// allocation and is shared by all layers.
+// Device layout: one allocation holds, for every layer, K then V.  K is
+// [kv_heads, pool_len, head_dim] 16-bit words, the KvPool layout of the
+// reference (crates/thuban_model/src/pool.rs:131-153).  V holds the same
+// elements with each page transposed, [kv_heads, pages, head_dim, page_len],
+// so that consecutive tokens of one dimension are contiguous (the operand
+// layout of the PV matrix product).  Every plane is aligned to 256 bytes.
+// The block table [seqs * max_pages] u32 lives in its own allocation and is
+// shared by all layers.
 #include <algorithm>
 #include <atomic>
 #include <cstdio>
@@ -277,10 +280,10 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
         return fail(THB_ERR_CONFIG, "unknown kv_dtype " + std::to_string(d->kv_dtype));
     if (d->page_len < 8 || d->page_len > 256 || (d->page_len & (d->page_len - 1)))
         return fail(THB_ERR_CONFIG, "page_len " + std::to_string(d->page_len) + " must be a power of two in [8, 256]");
-    uint32_t part = d->part_len ? d->part_len : 512;
-    if (part % 128 != 0 || part % d->page_len != 0 || part > 8192)
+    uint32_t part = d->part_len ? d->part_len : 4096;
+    if (part % 16 != 0 || part % d->page_len != 0 || part / d->page_len > 1024)
         return fail(THB_ERR_CONFIG, "part_len " + std::to_string(part) +
-                                        " must be a multiple of 128 and of page_len, at most 8192");
+                                        " must be a multiple of 16 and of page_len, at most 1024 pages");
     for (uint32_t l = 0; l < d->layers; l++) {
         uint32_t hd = d->head_dims ? d->head_dims[l] : d->head_dim;
         if (int rc = thb_check_head_dim(hd)) return rc;
@@ -393,6 +396,7 @@ int thb_pool_layer(const thb_pool* pool, uint32_t layer, void** k_dev, void** v_
         info->page_len = pool->page_len;
         info->kv_dtype = pool->kv_dtype;
         info->plane_elems = static_cast<uint64_t>(info->pool_len) * g.head_dim;
+        info->v_page_transposed = 1;
     }
     return THB_OK;
 }

@@ -31,10 +31,10 @@ struct AttnPlan {
     uint64_t rows_version = ~0ull;
     uint64_t arena_version = ~0ull;
     uint32_t row_off = 0, m = 0, seq = 0, causal = 0, window = 0, q_heads = 0, head_dim = 0;
-    uint32_t variant = 0;
     // value
     uint32_t n_groups = 0, n_items = 0;
-    uint32_t qv_max = 0;
+    uint32_t hd_t = 0;   // head_dim template of the kernel
+    bool split = false;  // some group spans several partitions: merge kernel runs
     DevBuf dev;  // [groups | items | row ranges]
     uint64_t last_use = 0;
 };
@@ -56,7 +56,7 @@ struct thb_rows {
 
 struct thb_pool {
     thb_arena arena;
-    uint32_t layers = 0, kv_heads = 0, page_len = 0, page_shift = 0, kv_dtype = 0, part_len = 512;
+    uint32_t layers = 0, kv_heads = 0, page_len = 0, page_shift = 0, kv_dtype = 0, part_len = 4096;
     std::vector<thb::LayerGeom> geom;
     uint8_t* mem = nullptr;  // device arena
     uint64_t mem_bytes = 0;
@@ -67,7 +67,6 @@ struct thb_pool {
     thb::DevBuf copy_buf;            // copy triples
     thb::DevBuf geom_buf;            // per-layer DevLayer records
     thb::DevBuf partials;            // split-K partial results
-    thb::DevBuf counters;            // split-K arrival counters (self-resetting)
     std::array<thb::AttnPlan, 4> plans;
     uint64_t plan_clock = 0;
     int device = 0;

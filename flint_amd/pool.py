@@ -210,14 +210,46 @@ class KvPool:
         return p.value, n.value
 
     def layer_tensors(self, layer: int):
-        """torch views (uint16 words) of the layer's K and V planes,
-        [kv_heads, pool_len, head_dim], without copying."""
+        """torch views (16-bit words, no copy) of the layer's device planes:
+        K as [kv_heads, pool_len, head_dim] and V as stored, page-transposed
+        [kv_heads, pages, head_dim, page_len]."""
         import torch
 
         info = self.layer_info(layer)
         k, v = self.layer_ptrs(layer)
-        shape = (info.kv_heads, info.pool_len, info.head_dim)
-        return _device_view(k, shape, torch.int16), _device_view(v, shape, torch.int16)
+        pages = info.pool_len // info.page_len
+        return (_device_view(k, (info.kv_heads, info.pool_len, info.head_dim), torch.int16),
+                _device_view(v, (info.kv_heads, pages, info.head_dim, info.page_len), torch.int16))
+
+    def read_layer(self, layer: int):
+        """Host copies (numpy uint16) of the layer's K and V in the
+        reference's KvPool layout [kv_heads, pool_len, head_dim]
+        (pool.rs:131-153), V un-transposed."""
+        import torch
+
+        k, v = self.layer_tensors(layer)
+        torch.cuda.synchronize()
+        info = self.layer_info(layer)
+        kn = k.cpu().numpy().view("uint16")
+        vn = v.cpu().numpy().view("uint16").transpose(0, 1, 3, 2).reshape(info.kv_heads, info.pool_len,
+                                                                          info.head_dim)
+        return kn, vn.copy()
+
+    def write_layer(self, layer: int, k_words, v_words) -> None:
+        """Uploads K and V words given in the reference layout [kv_heads,
+        pool_len, head_dim] (numpy uint16), transposing V pages."""
+        import numpy as np
+        import torch
+
+        info = self.layer_info(layer)
+        k, v = self.layer_tensors(layer)
+        pages = info.pool_len // info.page_len
+        kw = np.ascontiguousarray(k_words, np.uint16).reshape(info.kv_heads, info.pool_len, info.head_dim)
+        vw = np.ascontiguousarray(np.asarray(v_words, np.uint16).reshape(
+            info.kv_heads, pages, info.page_len, info.head_dim).transpose(0, 1, 3, 2))
+        k.copy_(torch.from_numpy(kw.view(np.int16)))
+        v.copy_(torch.from_numpy(vw.view(np.int16)))
+        torch.cuda.synchronize()
 
     def block_table_tensor(self):
         import torch

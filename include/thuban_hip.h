@@ -54,7 +54,7 @@ extern "C" {
 const char* thb_last_error(void);
 /* ABI revision of this header. */
 uint32_t thb_abi_version(void);
-#define THB_ABI_VERSION 1u
+#define THB_ABI_VERSION 2u
 
 /* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90):
  * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]".  This backend also needs
@@ -110,10 +110,15 @@ int thb_arena_take_copies(thb_arena* arena, uint32_t* triples, size_t cap, uint3
 
 /* ---------------------------------------------------------- device pool */
 
-/* One hipMalloc'd arena holding K and V of every layer, each layer laid out
- * as KvPool allocates it: [kv_heads, pages * page_len, head_dim]
- * (pool.rs:131-153), plus one device block table [seqs * max_pages] shared
- * by all layers (the reference keeps a copy per layer, model.rs:413-418). */
+/* One hipMalloc'd arena holding K and V of every layer, plus one device
+ * block table [seqs * max_pages] shared by all layers (the reference keeps a
+ * copy per layer, model.rs:413-418).  K is laid out as KvPool allocates it:
+ * [kv_heads, pages * page_len, head_dim] (pool.rs:131-153).  V holds the
+ * same elements with every page transposed: [kv_heads, pages, head_dim,
+ * page_len], i.e. element (head h, slot s, dim d) sits at
+ * ((h * pages + s / page_len) * head_dim + d) * page_len + s % page_len.
+ * That is the operand layout of the attention kernel's PV matrix product;
+ * thb_kv_gather returns V in the reference's token-major layout. */
 typedef struct thb_pool thb_pool;
 
 typedef struct thb_pool_desc {
@@ -126,8 +131,9 @@ typedef struct thb_pool_desc {
     uint32_t seqs;
     const uint32_t* seq_lens;   /* ArenaSpec.seq_lens [seqs] */
     int64_t pages;              /* ArenaSpec.pages; < 0 = None */
-    uint32_t part_len;          /* split-K partition in tokens (0 = 512);
-                                   multiple of 128 and of page_len */
+    uint32_t part_len;          /* split-K partition in tokens (0 = 4096);
+                                   multiple of 16 and of page_len, at most
+                                   1024 pages */
     void* arena_dev;            /* optional caller-owned device memory */
     uint64_t arena_bytes;       /* its size; 0 = let the pool hipMalloc */
 } thb_pool_desc;
@@ -140,6 +146,7 @@ typedef struct thb_layer_info {
     uint32_t page_len;
     uint32_t kv_dtype;
     uint64_t plane_elems;       /* elements per head plane = pool_len * head_dim */
+    uint32_t v_page_transposed; /* 1: V pages are [head_dim][page_len] */
 } thb_layer_info;
 
 /* KvArena::new + KvPool::new for every layer (pool.rs:20-45,131-153).  The
@@ -159,7 +166,8 @@ int thb_pool_fork(thb_pool* pool, uint32_t src, uint32_t dst, uint32_t tokens);
 int thb_pool_sync(thb_pool* pool, void* stream);
 /* The pool's allocator (queries; mutate through thb_pool_* instead). */
 const thb_arena* thb_pool_arena(const thb_pool* pool);
-/* Device pointers of layer `layer`'s K and V planes (KvPool::k / ::v). */
+/* Device pointers of layer `layer`'s K and V planes (KvPool::k / ::v; V in
+ * the page-transposed layout above). */
 int thb_pool_layer(const thb_pool* pool, uint32_t layer, void** k_dev, void** v_dev, thb_layer_info* info);
 /* Device block table [seqs * max_pages] (KvPool::block_table). */
 int thb_pool_block_table(const thb_pool* pool, const uint32_t** table_dev);
@@ -205,11 +213,13 @@ typedef struct thb_attn_spec {
 } thb_attn_spec;
 
 /* ops::attn (ops/attn.rs:18-51) / attn.wgsl:53-365.  q, y: [m, q_heads,
- * head_dim].  Key ranges per row follow attn.wgsl:78-88,169 exactly.  One
- * launch covers every row (batched over sequences), as a split-K decode with
- * a deterministic log-sum-exp merge: output is independent of physical page
- * placement and of the other rows in the batch.  f32 accumulation; within
- * 2e-3 of an exact softmax. */
+ * head_dim], 16-byte aligned.  Key ranges per row follow attn.wgsl:78-88,169
+ * exactly.  One launch covers every row (batched over sequences), as a
+ * split-K pass with a deterministic log-sum-exp merge (a second kernel when a
+ * row's keys span several part_len partitions): output is independent of
+ * physical page placement and of the other rows in the batch.  Products on
+ * the matrix cores with q and p split into high and low halves, f32
+ * accumulation; within 2e-3 of an exact softmax. */
 int thb_attn(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
              const thb_rows* rows, void* stream);
 

@@ -51,12 +51,10 @@ def fill(torch, pool: KvPool, rows: RowMeta, lens, layer=0, src_dtype=None, seed
 
 def oracle_layer(torch, pool: KvPool, layer=0) -> oracle.Layer:
     info = pool.layer_info(layer)
-    k, v = pool.layer_tensors(layer)
-    torch.cuda.synchronize()
+    k, v = pool.read_layer(layer)  # reference layout, V pages un-transposed
     a = pool.arena.info()
     return oracle.Layer(info.kv_heads, info.head_dim, a.pages, info.page_len,
-                        np.array(pool.arena.table(), np.uint32), a.max_pages, KV_CODE[pool.kv_dtype],
-                        k=k.cpu().numpy().view(np.uint16), v=v.cpu().numpy().view(np.uint16))
+                        np.array(pool.arena.table(), np.uint32), a.max_pages, KV_CODE[pool.kv_dtype], k=k, v=v)
 
 
 def make_pool(lens, kv_heads, head_dim, page_len=16, kv_dtype="f16", layers=1, extra_pages=0, part_len=0,

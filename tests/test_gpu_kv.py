@@ -72,15 +72,14 @@ def test_kv_store_special_values_bit_exact(torch_cuda):
         rows.write(list(range(m)), [0] * m, m)
         src = torch.from_numpy(bits.view(np.float32).reshape(m, nkv, hd).copy()).cuda()
         ops.kv_store(src, src, pool, 0, m, rows)
-        k, v = pool.layer_tensors(0)
-        torch.cuda.synchronize()
+        k, v = pool.read_layer(0)
         table = np.array(pool.arena.table_of(0))
         # slot of token t = table[t // 32] * 32 + t % 32; gather back in token order
         slots = (table[np.arange(m) // 32] * 32 + np.arange(m) % 32)
-        got = k.cpu().numpy().view(np.uint16)[:, slots, :].transpose(1, 0, 2).reshape(-1)
+        got = k[:, slots, :].transpose(1, 0, 2).reshape(-1)
         want = (oracle.f32_to_f16 if kv == "f16" else oracle.f32_to_bf16)(bits.view(np.float32))
         assert np.array_equal(got, want)
-        gotv = v.cpu().numpy().view(np.uint16)[:, slots, :].transpose(1, 0, 2).reshape(-1)
+        gotv = v[:, slots, :].transpose(1, 0, 2).reshape(-1)
         assert np.array_equal(gotv, want)
 
 
@@ -103,10 +102,9 @@ def test_kv_store_reference_lcg_vector(torch_cuda, golden):
     ks[:, :, :hd] = np.array(case["k_src"], np.uint32).view(np.float32).reshape(m, nkv, hd)
     vs[:, :, :hd] = np.array(case["v_src"], np.uint32).view(np.float32).reshape(m, nkv, hd)
     ops.kv_store(torch.from_numpy(ks).cuda(), torch.from_numpy(vs).cuda(), pool, 0, m, rows)
-    k, v = pool.layer_tensors(0)
-    torch.cuda.synchronize()
-    got_k = k.cpu().numpy().view(np.uint16)[:, :, :hd].reshape(-1)
-    got_v = v.cpu().numpy().view(np.uint16)[:, :, :hd].reshape(-1)
+    k, v = pool.read_layer(0)
+    got_k = k[:, :, :hd].reshape(-1)
+    got_v = v[:, :, :hd].reshape(-1)
     assert np.array_equal(got_k, np.array(case["expect_k"], np.uint16))
     assert np.array_equal(got_v, np.array(case["expect_v"], np.uint16))
 
