@@ -10,9 +10,12 @@ HBM before the timed region.
 
 Prints one JSON line.  value = achieved HBM GB/s of the whole step
 (algorithmic bytes: every K/V byte once + Q, O, block table, appended rows)
-/ step time.  roofline = the attention kernel (HIP events around layer 0's
-launch in every timed step).  cpu_baseline = the CPU oracle (restatement of
-the reference's f32 online-softmax algorithm) on layer 0 of the same step.
+/ step time.  roofline = the attention kernel: HIP events on the launch
+stream around every attention launch of layers 1..L-1 in the timed steps
+(layer 0 also carries the step's row-meta plan upload, which the step time
+includes).  traffic = HBM bytes per launch from the committed rocprofv3
+counter summary.  cpu_baseline = the CPU oracle (restatement of the
+reference's f32 online-softmax algorithm) on layer 0 of the same step.
 """
 
 from __future__ import annotations
@@ -93,6 +96,9 @@ def main():
     ap.add_argument("--part-len", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="after the timed steps, run 3 device copies of this many MiB (scale factor for the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -132,19 +138,21 @@ def main():
     spec = ops.AttnSpec(q_heads=nq, window=0, scale=scale, m=B, causal=True, seq=None, args=rows)
     torch.cuda.synchronize()
 
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # events[i][layer] = (before kv_store, after kv_store, after attention)
+    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(L)] for _ in range(args.steps)]
 
     def step(i=None):
         rows.write(positions, seqs, B)
         for layer in range(L):
-            if i is not None and layer == 0:
-                ev[i][0].record()
+            e = ev[i][layer] if i is not None else None
+            if e:
+                e[0].record()
             ops.kv_store(k_new[layer], v_new[layer], pool, layer, B, rows)
-            if i is not None and layer == 0:
-                ev[i][1].record()
+            if e:
+                e[1].record()
             ops.attn(q[layer], pool, layer, y[layer], spec)
-            if i is not None and layer == 0:
-                ev[i][2].record()
+            if e:
+                e[2].record()
 
     for _ in range(args.warmup):
         step()
@@ -159,10 +167,11 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = t_start.elapsed_time(t_end) / args.steps
-    append_us = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps * 1e3
-    attn_us = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps * 1e3
-    log(f"step {ms_step:.3f} ms (host wall {wall / args.steps * 1e3:.3f} ms); attn {attn_us:.1f} us/layer; "
-        f"append {append_us:.2f} us/layer")
+    timed = [ev[i][layer] for i in range(args.steps) for layer in range(1, L)]
+    append_us = sum(e[0].elapsed_time(e[1]) for e in timed) / len(timed) * 1e3
+    attn_us = sum(e[1].elapsed_time(e[2]) for e in timed) / len(timed) * 1e3
+    log(f"step {ms_step:.3f} ms (host wall {wall / args.steps * 1e3:.3f} ms); attn {attn_us:.1f} us/launch; "
+        f"append {append_us:.2f} us/launch")
 
     kv_bytes = B * nkv * ctx * hd * 2 * 2
     qo_bytes = 2 * B * nq * hd * 2
@@ -172,7 +181,7 @@ def main():
     step_bytes = L * (attn_bytes + append_bytes)
     value = step_bytes / (ms_step * 1e-3) / 1e9
     achieved = attn_bytes / (attn_us * 1e-6) / 1e9
-    traffic = load_traffic(f"attn_splitk_{args.config}_traffic.json")
+    traffic = load_traffic(f"attn_mfma_{args.config}-decode_traffic.json")
 
     out = {
         "metric": "paged decode us/step + achieved HBM GB/s (% peak); KV append GB/s @Llama-3-8B",
@@ -199,9 +208,17 @@ def main():
                    "bytes_per_launch": append_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
-                     "kernel": "attn_mfma<128,f16,8 waves>", "algorithmic_bytes": attn_bytes},
+                     "kernel": "attn_mfma<128,f16,8 waves,ring 2>", "algorithmic_bytes": attn_bytes,
+                     "launches_timed": len(timed)},
         "cpu_baseline": None,
     }
+    if args.calibrate_copy_mib:
+        src = torch.empty(args.calibrate_copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration: 3 copies of {args.calibrate_copy_mib} MiB")
     if not args.no_cpu_baseline:
         per_run, runs, err = cpu_baseline(torch, pool, q[0], y[0], cfg, scale, args.cpu_seconds)
         threads = __import__("oracle").num_threads()

@@ -163,9 +163,10 @@ struct Ops<false> {
     }
 };
 
-// One (group, partition, KV head) per workgroup of W waves.  DB: the next
-// tile's loads are issued before the current tile is computed.
-template <int HD, bool F16, int W, bool DB>
+// One (group, partition, KV head) per workgroup of W waves.  NB tiles of
+// loads are kept in flight per wave: tile i + NB is requested as soon as
+// tile i has been consumed.
+template <int HD, bool F16, int W, int NB>
 __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
@@ -331,27 +332,21 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
         }
     };
 
-    if constexpr (DB) {
-        if (ws < we) {
-            u32x4 kA[KS], kB[KS];
-            u32x2 vA[MT], vB[MT];
-            load(ws, kA, vA);
-            if (ws + 16 < we) load(ws + 16, kB, vB);
-            for (uint32_t t0 = ws; t0 < we; t0 += 32) {
-                compute(t0, kA, vA);
-                if (t0 + 32 < we) load(t0 + 32, kA, vA);
-                if (t0 + 16 < we) {
-                    compute(t0 + 16, kB, vB);
-                    if (t0 + 48 < we) load(t0 + 48, kB, vB);
+    {
+        u32x4 kr[NB][KS];
+        u32x2 vr[NB][MT];
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            if (ws + 16u * b < we) load(ws + 16u * b, kr[b], vr[b]);
+        for (uint32_t t0 = ws; t0 < we; t0 += 16u * NB) {
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                const uint32_t t = t0 + 16u * b;
+                if (t < we) {
+                    compute(t, kr[b], vr[b]);
+                    if (t + 16u * NB < we) load(t + 16u * NB, kr[b], vr[b]);
                 }
             }
-        }
-    } else {
-        for (uint32_t t0 = ws; t0 < we; t0 += 16) {
-            u32x4 kA[KS];
-            u32x2 vA[MT];
-            load(t0, kA, vA);
-            compute(t0, kA, vA);
         }
     }
     l = col_sum(l);
@@ -457,15 +452,23 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
 // ------------------------------------------------------------ host side
 uint32_t template_hd(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : hd <= 256 ? 256 : 512; }
 
-// Waves per workgroup of each head_dim template: 8 waves (2 per SIMD, 256
-// registers each) up to head_dim 128; 4 waves (512 registers each) above,
-// where the query, output and load registers grow with head_dim.
-constexpr int waves_for(int hd) { return hd >= 256 ? 4 : 8; }
+// Waves per workgroup and tiles in flight per wave of each head_dim
+// template: up to head_dim 128, 8 waves (2 per SIMD, 256 registers each);
+// above, 4 waves (512 registers each), because the query, output and load
+// registers grow with head_dim.
+#ifndef THB_ATTN_WAVES
+#define THB_ATTN_WAVES 8
+#endif
+#ifndef THB_ATTN_RING
+#define THB_ATTN_RING 2
+#endif
+constexpr int waves_for(int hd) { return hd >= 256 ? 4 : THB_ATTN_WAVES; }
+constexpr int ring_for(int hd) { return hd >= 512 ? 1 : hd >= 256 ? 2 : THB_ATTN_RING; }
 
 template <int HD, bool F16>
 void launch_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
     constexpr int W = waves_for(HD);
-    hipLaunchKernelGGL((attn_mfma<HD, F16, W, (HD <= 256)>), grid, dim3(64 * W), 0, s, a);
+    hipLaunchKernelGGL((attn_mfma<HD, F16, W, ring_for(HD)>), grid, dim3(64 * W), 0, s, a);
 }
 
 void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
