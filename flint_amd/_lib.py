@@ -67,7 +67,7 @@ class LayerInfo(ctypes.Structure):
         ("page_len", ctypes.c_uint32),
         ("kv_dtype", ctypes.c_uint32),
         ("plane_elems", ctypes.c_uint64),
-        ("v_page_transposed", ctypes.c_uint32),
+        ("page_layout", ctypes.c_uint32),
     ]
 
 

@@ -17,8 +17,9 @@
 //    pages sit: batch == solo and paged == contiguous hold bit-exactly.
 //  * Scores come from MFMA: S^T[16 tokens x 16 columns] = K Q^T with
 //    v_mfma_f32_16x16x32_{f16,bf16}.  The A operand is 16 bytes of one key
-//    row per lane (a plain vector load), the B operand is Q^T held in
-//    registers.  Q is split into a high and a low half-precision part and
+//    per lane; the pool keeps K pages chunk-major ([head_dim/8][page_len][8])
+//    so that one load instruction covers 1 KiB of contiguous memory.  The B
+//    operand is Q^T held in registers.  Q is split into a high and a low half-precision part and
 //    both are multiplied, which keeps the products at f32 accuracy.
 //  * S^T leaves lane (a, c) holding tokens 4a..4a+3 of column c.  That is
 //    exactly the B-operand layout of v_mfma_f32_16x16x16 for P^T, so the
@@ -271,14 +272,19 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     // Loads one 16-token tile.  Tokens outside [tb, te) are clamped into
     // it (their scores are masked), so every address is inside a page of
     // the sequence.
+    // K pages are [hd/8][page_len][8]: for a fixed k-step j the 64 lanes read
+    // 4 chunk rows x 16 tokens x 16 bytes, 1 KiB contiguous when page_len is
+    // 16.  The loads are non-temporal: every byte is read once.
     auto load = [&](uint32_t t0, u32x4 (&kr)[KS], u32x2 (&vr)[MT]) {
         const uint32_t tk = min(max(t0 + c, tb), last);
         const uint32_t kpage = s_page[(tk - pbeg) >> pshift];
-        const uint16_t* krow = kplane + ((static_cast<uint64_t>(kpage) << pshift) | (tk & pmask)) * hd;
+        const uint16_t* kbase = kplane + (static_cast<uint64_t>(kpage) * hd << pshift) + ((tk & pmask) << 3);
 #pragma unroll
         for (int j = 0; j < KS; j++) {
             const uint32_t d0 = 32u * j + 8u * a4;
-            kr[j] = d0 < hd ? *reinterpret_cast<const u32x4*>(krow + d0) : u32x4{0u, 0u, 0u, 0u};
+            kr[j] = d0 < hd ? __builtin_nontemporal_load(
+                                  reinterpret_cast<const u32x4*>(kbase + (static_cast<uint64_t>(d0) << pshift)))
+                            : u32x4{0u, 0u, 0u, 0u};
         }
         const uint32_t tv = min(max(t0 + 4u * a4, tb & ~3u), last & ~3u);
         const uint32_t vpage = s_page[(tv - pbeg) >> pshift];
@@ -286,7 +292,8 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < MT; i++) {
             const uint32_t d = 16u * i + c;
-            vr[i] = d < hd ? *reinterpret_cast<const u32x2*>(vbase + (static_cast<uint64_t>(d) << pshift))
+            vr[i] = d < hd ? __builtin_nontemporal_load(
+                                 reinterpret_cast<const u32x2*>(vbase + (static_cast<uint64_t>(d) << pshift)))
                            : u32x2{0u, 0u};
         }
     };

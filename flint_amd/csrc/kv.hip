@@ -1,10 +1,12 @@
 // KV append/scatter (kv_store), gather, scatter and page copy kernels.
 //
 // One lane owns 8 consecutive head_dim elements of one token of one head.
-// K rows are token-major, so a K access is one 16-byte vector.  V pages are
-// stored transposed ([head_dim][page_len] per page, the operand layout of
-// the attention kernel's PV product), so the lane's 8 V elements are 8
-// 16-bit accesses page_len elements apart.
+// K pages are chunk-major ([head_dim / 8][page_len][8] per page), so a lane's
+// 8 K elements are one 16-byte vector.  V pages are transposed ([head_dim]
+// [page_len] per page, the operand layout of the attention kernel's PV
+// product), so the lane's 8 V elements are 8 16-bit accesses page_len
+// elements apart.  In both, element (slot s, dim d) of page p starts from
+// the offset (p * head_dim + d) * page_len.
 #include <string>
 
 #include "pool.hpp"
@@ -130,7 +132,8 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
     const uint64_t src_e = (static_cast<uint64_t>(row) * a.chunks + c) << 3;
     const uint4 w = load_encode8<SRC, KV>(is_v ? a.v_src : a.k_src, src_e);
     if (!is_v) {
-        *reinterpret_cast<uint4*>(a.k + h * a.plane + slot * a.head_dim + d) = w;
+        *reinterpret_cast<uint4*>(a.k + h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + d) << a.page_shift) +
+                                  ((pos & ((1u << a.page_shift) - 1u)) << 3)) = w;
         return;
     }
     // V^T: element (slot, d + e) of the page lives at (page * hd + d + e) *
@@ -168,9 +171,8 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     const uint32_t pos = a.t0 + t;
     const uint32_t page = a.table_row[pos >> a.page_shift];
     const uint32_t j = pos & ((1u << a.page_shift) - 1u);
-    const uint64_t slot = (static_cast<uint64_t>(page) << a.page_shift) | j;
     if (blockIdx.y == 0) {
-        uint16_t* paged = a.k + h * a.plane + slot * a.head_dim + d;
+        uint16_t* paged = a.k + h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + d) << a.page_shift) + (j << 3);
         uint16_t* flat = a.k_flat + (static_cast<uint64_t>(h) * a.n + t) * a.head_dim + d;
         if constexpr (TO_FLAT)
             *reinterpret_cast<uint4*>(flat) = *reinterpret_cast<const uint4*>(paged);
@@ -208,8 +210,9 @@ struct CopyArgs {
 
 // Copy of slots [0, ntok) of a page for every layer, K and V, every head.
 // Grid: (ceil(page_len * max_head_dim / 256), n_triples, layers * 2 *
-// kv_heads).  A K page and a whole V page are contiguous and move as 16-byte
-// vectors; a partial V page moves element by element ([head_dim][page_len]).
+// kv_heads).  A whole page moves as contiguous 16-byte vectors; a partial K
+// page as 16-byte chunks of its chunk rows; a partial V page element by
+// element ([head_dim][page_len]).
 __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
     const uint32_t z = blockIdx.z;
     const uint32_t h = z % a.kv_heads;
@@ -224,9 +227,17 @@ __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
     const uint64_t page_elems = static_cast<uint64_t>(a.page_len) * L.head_dim;
     const uint16_t* sp = base + static_cast<uint64_t>(src) * page_elems;
     uint16_t* dp = base + static_cast<uint64_t>(dst) * page_elems;
-    if (which == 0 || ntok == a.page_len) {
-        if (static_cast<uint64_t>(c) * 8 >= static_cast<uint64_t>(ntok) * L.head_dim) return;
+    if (ntok == a.page_len) {  // whole page, K or V: contiguous
+        if (static_cast<uint64_t>(c) * 8 >= page_elems) return;
         const uint64_t off = static_cast<uint64_t>(c) * 8;
+        *reinterpret_cast<uint4*>(dp + off) = *reinterpret_cast<const uint4*>(sp + off);
+        return;
+    }
+    if (which == 0) {  // K: the first ntok 16-byte chunks of every chunk row
+        const uint32_t rows = L.head_dim >> 3;
+        if (c >= rows * ntok) return;
+        const uint32_t r = c / ntok, j = c - r * ntok;
+        const uint64_t off = (static_cast<uint64_t>(r) * a.page_len + j) * 8;
         *reinterpret_cast<uint4*>(dp + off) = *reinterpret_cast<const uint4*>(sp + off);
         return;
     }

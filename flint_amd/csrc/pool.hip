@@ -1,11 +1,11 @@
 // C ABI of the host allocator, the device pool and the row metadata.
 //
-// Device layout: one allocation holds, for every layer, K then V.  K is
-// [kv_heads, pool_len, head_dim] 16-bit words, the KvPool layout of the
-// reference (crates/thuban_model/src/pool.rs:131-153).  V holds the same
-// elements with each page transposed, [kv_heads, pages, head_dim, page_len],
-// so that consecutive tokens of one dimension are contiguous (the operand
-// layout of the PV matrix product).  Every plane is aligned to 256 bytes.
+// Device layout: one allocation holds, for every layer, K then V, each
+// [kv_heads, pages, <page>] 16-bit words: the elements of the reference's
+// KvPool planes [kv_heads, pool_len, head_dim] (crates/thuban_model/src/
+// pool.rs:131-153) with each page reordered for the attention kernel.  A K
+// page is chunk-major, [head_dim / 8][page_len][8]; a V page is transposed,
+// [head_dim][page_len].  Every plane is aligned to 256 bytes.
 // The block table [seqs * max_pages] u32 lives in its own allocation and is
 // shared by all layers.
 #include <algorithm>
@@ -396,7 +396,7 @@ int thb_pool_layer(const thb_pool* pool, uint32_t layer, void** k_dev, void** v_
         info->page_len = pool->page_len;
         info->kv_dtype = pool->kv_dtype;
         info->plane_elems = static_cast<uint64_t>(info->pool_len) * g.head_dim;
-        info->v_page_transposed = 1;
+        info->page_layout = THB_PAGE_LAYOUT_MFMA;
     }
     return THB_OK;
 }

@@ -210,43 +210,46 @@ class KvPool:
         return p.value, n.value
 
     def layer_tensors(self, layer: int):
-        """torch views (16-bit words, no copy) of the layer's device planes:
-        K as [kv_heads, pool_len, head_dim] and V as stored, page-transposed
-        [kv_heads, pages, head_dim, page_len]."""
+        """torch views (16-bit words, no copy) of the layer's device planes as
+        stored: K pages chunk-major [kv_heads, pages, head_dim/8, page_len,
+        8], V pages transposed [kv_heads, pages, head_dim, page_len]."""
         import torch
 
         info = self.layer_info(layer)
         k, v = self.layer_ptrs(layer)
         pages = info.pool_len // info.page_len
-        return (_device_view(k, (info.kv_heads, info.pool_len, info.head_dim), torch.int16),
-                _device_view(v, (info.kv_heads, pages, info.head_dim, info.page_len), torch.int16))
+        hd, P = info.head_dim, info.page_len
+        return (_device_view(k, (info.kv_heads, pages, hd // 8, P, 8), torch.int16),
+                _device_view(v, (info.kv_heads, pages, hd, P), torch.int16))
 
     def read_layer(self, layer: int):
         """Host copies (numpy uint16) of the layer's K and V in the
         reference's KvPool layout [kv_heads, pool_len, head_dim]
-        (pool.rs:131-153), V un-transposed."""
+        (pool.rs:131-153)."""
         import torch
 
         k, v = self.layer_tensors(layer)
         torch.cuda.synchronize()
         info = self.layer_info(layer)
-        kn = k.cpu().numpy().view("uint16")
-        vn = v.cpu().numpy().view("uint16").transpose(0, 1, 3, 2).reshape(info.kv_heads, info.pool_len,
-                                                                          info.head_dim)
-        return kn, vn.copy()
+        shape = (info.kv_heads, info.pool_len, info.head_dim)
+        kn = k.cpu().numpy().view("uint16").transpose(0, 1, 3, 2, 4).reshape(shape)
+        vn = v.cpu().numpy().view("uint16").transpose(0, 1, 3, 2).reshape(shape)
+        return kn.copy(), vn.copy()
 
     def write_layer(self, layer: int, k_words, v_words) -> None:
         """Uploads K and V words given in the reference layout [kv_heads,
-        pool_len, head_dim] (numpy uint16), transposing V pages."""
+        pool_len, head_dim] (numpy uint16) into the device page layout."""
         import numpy as np
         import torch
 
         info = self.layer_info(layer)
         k, v = self.layer_tensors(layer)
         pages = info.pool_len // info.page_len
-        kw = np.ascontiguousarray(k_words, np.uint16).reshape(info.kv_heads, info.pool_len, info.head_dim)
+        hd, P = info.head_dim, info.page_len
+        kw = np.ascontiguousarray(np.asarray(k_words, np.uint16).reshape(
+            info.kv_heads, pages, P, hd // 8, 8).transpose(0, 1, 3, 2, 4))
         vw = np.ascontiguousarray(np.asarray(v_words, np.uint16).reshape(
-            info.kv_heads, pages, info.page_len, info.head_dim).transpose(0, 1, 3, 2))
+            info.kv_heads, pages, P, hd).transpose(0, 1, 3, 2))
         k.copy_(torch.from_numpy(kw.view(np.int16)))
         v.copy_(torch.from_numpy(vw.view(np.int16)))
         torch.cuda.synchronize()

@@ -112,13 +112,16 @@ int thb_arena_take_copies(thb_arena* arena, uint32_t* triples, size_t cap, uint3
 
 /* One hipMalloc'd arena holding K and V of every layer, plus one device
  * block table [seqs * max_pages] shared by all layers (the reference keeps a
- * copy per layer, model.rs:413-418).  K is laid out as KvPool allocates it:
- * [kv_heads, pages * page_len, head_dim] (pool.rs:131-153).  V holds the
- * same elements with every page transposed: [kv_heads, pages, head_dim,
- * page_len], i.e. element (head h, slot s, dim d) sits at
- * ((h * pages + s / page_len) * head_dim + d) * page_len + s % page_len.
- * That is the operand layout of the attention kernel's PV matrix product;
- * thb_kv_gather returns V in the reference's token-major layout. */
+ * copy per layer, model.rs:413-418).  Each plane holds the elements of the
+ * reference's KvPool tensors [kv_heads, pages * page_len, head_dim]
+ * (pool.rs:131-153) with every page reordered for the attention kernel's
+ * matrix-core operands (THB_PAGE_LAYOUT_MFMA).  With P = page_len, page
+ * base B = (h * pages + s / P) * head_dim * P and j = s % P, element
+ * (head h, slot s, dim d) sits at
+ *   K: B + (d / 8) * P * 8 + j * 8 + d % 8   (chunk-major [head_dim/8][P][8])
+ *   V: B + d * P + j                           (transposed   [head_dim][P])
+ * thb_kv_gather returns both in the reference's token-major layout. */
+#define THB_PAGE_LAYOUT_MFMA 1u
 typedef struct thb_pool thb_pool;
 
 typedef struct thb_pool_desc {
@@ -146,7 +149,7 @@ typedef struct thb_layer_info {
     uint32_t page_len;
     uint32_t kv_dtype;
     uint64_t plane_elems;       /* elements per head plane = pool_len * head_dim */
-    uint32_t v_page_transposed; /* 1: V pages are [head_dim][page_len] */
+    uint32_t page_layout;       /* THB_PAGE_LAYOUT_* of the K and V pages */
 } thb_layer_info;
 
 /* KvArena::new + KvPool::new for every layer (pool.rs:20-45,131-153).  The
@@ -166,8 +169,8 @@ int thb_pool_fork(thb_pool* pool, uint32_t src, uint32_t dst, uint32_t tokens);
 int thb_pool_sync(thb_pool* pool, void* stream);
 /* The pool's allocator (queries; mutate through thb_pool_* instead). */
 const thb_arena* thb_pool_arena(const thb_pool* pool);
-/* Device pointers of layer `layer`'s K and V planes (KvPool::k / ::v; V in
- * the page-transposed layout above). */
+/* Device pointers of layer `layer`'s K and V planes (KvPool::k / ::v, in the
+ * page layout above). */
 int thb_pool_layer(const thb_pool* pool, uint32_t layer, void** k_dev, void** v_dev, thb_layer_info* info);
 /* Device block table [seqs * max_pages] (KvPool::block_table). */
 int thb_pool_block_table(const thb_pool* pool, const uint32_t** table_dev);

@@ -199,3 +199,35 @@ def test_kv_store_errors(torch_cuda):
     with pytest.raises(ThubanError):
         ops.kv_store(k, k, pool, 1, 1, rows)  # no layer 1
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("page_len,hd", [(16, 128), (32, 64), (8, 256)])
+def test_page_layout_matches_header(torch_cuda, page_len, hd):
+    """Words written in the reference layout [kv_heads, pool_len, head_dim]
+    through KvPool.write_layer come back unchanged through read_layer and,
+    token by token, through the gather kernel (which addresses the device
+    page layout documented in include/thuban_hip.h)."""
+    torch = torch_cuda
+    from flint_amd import ops
+
+    say("page layout", page_len, hd)
+    rng = np.random.default_rng(page_len * hd)
+    lens = [3 * page_len + 5, 2 * page_len]
+    pool = make_pool(lens, kv_heads=3, head_dim=hd, page_len=page_len, kv_dtype="f16", extra_pages=2)
+    scattered_alloc(pool, lens, random.Random(7), page_len)
+    info = pool.layer_info(0)
+    k = rng.integers(0, 1 << 16, size=(3, info.pool_len, hd), dtype=np.uint16)
+    v = rng.integers(0, 1 << 16, size=(3, info.pool_len, hd), dtype=np.uint16)
+    pool.write_layer(0, k, v)
+    k2, v2 = pool.read_layer(0)
+    assert np.array_equal(k2, k) and np.array_equal(v2, v)
+    ref = oracle.Layer(3, hd, pool.arena.pages(), page_len, np.array(pool.arena.table(), np.uint32),
+                       pool.arena.max_pages(), oracle.KV_F16, k=k, v=v)
+    for s, n in enumerate(lens):
+        kd = torch.empty(3, n, hd, dtype=torch.int16, device="cuda")
+        vd = torch.empty_like(kd)
+        ops.kv_gather(pool, 0, s, 0, n, kd, vd)
+        torch.cuda.synchronize()
+        rk, rv = ref.gather(s, 0, n)
+        assert np.array_equal(kd.cpu().numpy().view(np.uint16), rk)
+        assert np.array_equal(vd.cpu().numpy().view(np.uint16), rv)
