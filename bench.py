@@ -11,9 +11,12 @@ HBM before the timed region.
 Prints one JSON line.  value = achieved HBM GB/s of the whole step
 (algorithmic bytes: every K/V byte once + Q, O, block table, appended rows)
 / step time.  roofline = the attention kernel: HIP events on the launch
-stream around every attention launch of layers 1..L-1 in the timed steps
+stream around the run of layers 1..L-1 of every timed step, divided by L-1
 (layer 0 also carries the step's row-meta plan upload, which the step time
-includes).  traffic = HBM bytes per launch from the committed rocprofv3
+includes; two events per step keep the instrumentation out of the step
+time).  The standalone append kernel is timed from a captured HIP graph of
+back-to-back launches (Python cannot enqueue 5-us kernels fast enough to
+keep the GPU busy).  traffic = HBM bytes per launch from the committed rocprofv3
 counter summary.  cpu_baseline = the CPU oracle (restatement of the
 reference's f32 online-softmax algorithm) on layer 0 of the same step.
 """
@@ -59,6 +62,35 @@ def load_traffic(name):
         return None
     with open(path) as f:
         return json.load(f).get("hbm_bytes_per_launch")
+
+
+def time_append_graph(torch, ops, pool, rows, k, v, layer, m, launches=50, replays=5):
+    """Average duration of the standalone append kernel (ops.kv_store), from
+    a HIP graph of back-to-back launches replayed with events around it.
+    Returns None if the graph cannot be captured."""
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            ops.kv_store(k, v, pool, layer, m, rows)  # warm: nothing left to upload
+            side.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(launches):
+                    ops.kv_store(k, v, pool, layer, m, rows)
+        torch.cuda.current_stream().wait_stream(side)
+        graph.replay()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(replays):
+            graph.replay()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / (replays * launches) * 1e3
+    except Exception as exc:  # capture refused: report no figure rather than a host-bound one
+        log(f"append graph timing unavailable: {exc}")
+        return None
 
 
 def cpu_baseline(torch, pool, q0, y0, cfg, scale, seconds):
@@ -138,21 +170,18 @@ def main():
     spec = ops.AttnSpec(q_heads=nq, window=0, scale=scale, m=B, causal=True, seq=None, args=rows)
     torch.cuda.synchronize()
 
-    # events[i][layer] = (before kv_store, after kv_store, after attention)
-    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(L)] for _ in range(args.steps)]
+    # ev[i] = (before layer 1, after layer L-1) of timed step i
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
 
     def step(i=None):
         rows.write(positions, seqs, B)
         for layer in range(L):
-            e = ev[i][layer] if i is not None else None
-            if e:
-                e[0].record()
-            ops.kv_store(k_new[layer], v_new[layer], pool, layer, B, rows)
-            if e:
-                e[1].record()
-            ops.attn(q[layer], pool, layer, y[layer], spec)
-            if e:
-                e[2].record()
+            if i is not None and layer == min(1, L - 1):
+                ev[i][0].record()
+            # kv_store + attn of the layer (transformer/forward.rs:300-336), one launch
+            ops.kv_store_attn(k_new[layer], v_new[layer], q[layer], pool, layer, y[layer], spec)
+        if i is not None:
+            ev[i][1].record()
 
     for _ in range(args.warmup):
         step()
@@ -167,20 +196,22 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = t_start.elapsed_time(t_end) / args.steps
-    timed = [ev[i][layer] for i in range(args.steps) for layer in range(1, L)]
-    append_us = sum(e[0].elapsed_time(e[1]) for e in timed) / len(timed) * 1e3
-    attn_us = sum(e[1].elapsed_time(e[2]) for e in timed) / len(timed) * 1e3
-    log(f"step {ms_step:.3f} ms (host wall {wall / args.steps * 1e3:.3f} ms); attn {attn_us:.1f} us/launch; "
-        f"append {append_us:.2f} us/launch")
+    timed = ev
+    per_run = max(L - 1, 1)
+    attn_us = sum(e[0].elapsed_time(e[1]) for e in timed) / len(timed) / per_run * 1e3
+    append_us = time_append_graph(torch, ops, pool, rows, k_new[1 % L], v_new[1 % L], 1 % L, B)
+    log(f"step {ms_step:.3f} ms (host wall {wall / args.steps * 1e3:.3f} ms); fused append+attention "
+        f"{attn_us:.1f} us/launch; standalone append {append_us} us/launch")
 
     kv_bytes = B * nkv * ctx * hd * 2 * 2
     qo_bytes = 2 * B * nq * hd * 2
     bt_bytes = B * (-(-ctx // pl)) * 4 + B * 32
     attn_bytes = kv_bytes + qo_bytes + bt_bytes
     append_bytes = B * nkv * hd * 2 * (2 + 2)
-    step_bytes = L * (attn_bytes + append_bytes)
+    fused_bytes = attn_bytes + append_bytes  # one fused launch per layer
+    step_bytes = L * fused_bytes
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    achieved = attn_bytes / (attn_us * 1e-6) / 1e9
+    achieved = fused_bytes / (attn_us * 1e-6) / 1e9
     traffic = load_traffic(f"attn_mfma_{args.config}-decode_traffic.json")
 
     out = {
@@ -203,13 +234,15 @@ def main():
         "us_per_step": round(ms_step * 1e3, 1),
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 1),
         "decode": {"us_per_layer": round(attn_us, 2), "GBps": round(achieved, 1),
-                   "bytes_per_launch": attn_bytes},
-        "append": {"us_per_layer": round(append_us, 2), "GBps": round(append_bytes / (append_us * 1e-6) / 1e9, 1),
-                   "bytes_per_launch": append_bytes},
+                   "bytes_per_launch": fused_bytes, "note": "one launch per layer: append fused into attention"},
+        "append": {"us_per_launch": round(append_us, 2) if append_us else None,
+                   "GBps": round(append_bytes / (append_us * 1e-6) / 1e9, 1) if append_us else None,
+                   "bytes_per_launch": append_bytes,
+                   "note": "standalone kv_store kernel (32 rows), graph of back-to-back launches after the steps"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
-                     "kernel": "attn_mfma<128,f16,8 waves,ring 2>", "algorithmic_bytes": attn_bytes,
-                     "launches_timed": len(timed)},
+                     "kernel": "attn_mfma<128,f16,8 waves,ring 2> with fused append",
+                     "algorithmic_bytes": fused_bytes, "launches_timed": len(timed) * per_run},
         "cpu_baseline": None,
     }
     if args.calibrate_copy_mib:

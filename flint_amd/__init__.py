@@ -12,5 +12,6 @@ the reference's pool / ops interface for that path:
 """
 
 from ._lib import ThubanError, lib  # noqa: F401
-from .ops import AttnSpec, attn, block_copy, check_head_dim, default_scale, kv_gather, kv_scatter, kv_store  # noqa: F401
+from .ops import (AttnSpec, attn, block_copy, check_head_dim, default_scale, kv_gather, kv_scatter,  # noqa: F401
+                  kv_store, kv_store_attn)
 from .pool import ArenaSpec, KvArena, KvPool, RowMeta, row_meta, write_row_meta  # noqa: F401

@@ -123,6 +123,7 @@ SIGNATURES = [
     ("thb_rows_device", _vp, [_vp]),
     ("thb_kv_store", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _u32, _u32, _vp]),
     ("thb_attn", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
+    ("thb_attn_append", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_block_copy", _int, [_vp, _pu32, _u32, _vp]),

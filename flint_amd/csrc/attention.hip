@@ -35,6 +35,7 @@
 #include <algorithm>
 #include <string>
 
+#include "codec.hpp"
 #include "pool.hpp"
 
 namespace thb {
@@ -53,7 +54,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct AttnArgs {
     const void* q;
@@ -62,8 +62,11 @@ struct AttnArgs {
     const uint32_t* items;   // work item -> group
     const uint32_t* ranges;  // [m][2]: lo, hi
     const uint32_t* table;
-    const uint16_t* k;
-    const uint16_t* v;
+    uint16_t* k;
+    uint16_t* v;
+    const void* k_src;  // fused append: new K/V rows [m, n_kvh, hd] (null: none)
+    const void* v_src;
+    uint32_t src_dtype;
     float* part_o;   // [n_items][n_kvh][16][hd_t]
     float* part_ml;  // [n_items][n_kvh][16][2]
     uint64_t plane;  // 16-bit elements per head plane
@@ -252,12 +255,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
             O::split8(x, qh[j], ql[j]);
         }
     }
-    __syncthreads();
 
-    float m = kFloor, l = 0.0f;
-    f32x4 o[MT];
-#pragma unroll
-    for (int i = 0; i < MT; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // This wave's run of 16-token tiles inside [tb, te).
     const uint32_t tb16 = tb & ~15u;
@@ -265,6 +263,64 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     const uint32_t run = ((span + W - 1) / W + 15u) & ~15u;
     const uint32_t ws = tb16 + wave * run;
     const uint32_t we = min(ws + run, te);
+
+    // Fused append (thb_attn_append).  A row's new token sits at position
+    // hi - 1 of the row, and the only wave that ever loads it is the wave
+    // whose run holds that position.  That wave encodes and stores the row's
+    // K and V of this KV head (exactly as kv_store) before its first tile
+    // load; one wave's accesses to an address are ordered, so no barrier is
+    // needed.  Work item t of the group: row t / (2 cpr), K or V, 8-element
+    // chunk.  The first item of each lane is loaded before the barrier,
+    // under the latency of the query loads.
+    const uint32_t cpr = hd >> 3;
+    const uint32_t app_items = a.k_src != nullptr ? R * 2 * cpr : 0u;
+    constexpr uint32_t KVE = F16 ? THB_KV_F16_RNE : THB_KV_BF16_TRUNC;
+    auto app_decode = [&](uint32_t t, uint32_t& pos, bool& is_v, uint32_t& d, uint64_t& e) -> bool {
+        const uint32_t ar = t / (2 * cpr), rem = t - ar * 2 * cpr;
+        is_v = rem >= cpr;
+        d = (is_v ? rem - cpr : rem) << 3;
+        pos = a.ranges[2 * (r0 + ar) + 1] - 1;
+        e = (static_cast<uint64_t>(r0 + ar) * a.n_kvh + kvh) * hd + d;
+        return pos >= ws && pos < we;
+    };
+    auto app_store = [&](uint32_t pos, bool is_v, uint32_t d, const uint4& w) {
+        const uint64_t base = ((static_cast<uint64_t>(s_page[(pos - pbeg) >> pshift]) * hd + d) << pshift) +
+                              static_cast<uint64_t>(kvh) * a.plane;
+        if (!is_v) {
+            *reinterpret_cast<uint4*>(a.k + base + ((pos & pmask) << 3)) = w;
+        } else {
+            uint16_t* dst = a.v + base + (pos & pmask);
+            const uint32_t ws4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int q2 = 0; q2 < 4; q2++) {
+                dst[static_cast<uint64_t>(2 * q2) << pshift] = static_cast<uint16_t>(ws4[q2] & 0xffffu);
+                dst[static_cast<uint64_t>(2 * q2 + 1) << pshift] = static_cast<uint16_t>(ws4[q2] >> 16);
+            }
+        }
+    };
+    uint32_t app_pos = 0, app_d = 0;
+    uint64_t app_e = 0;
+    bool app_v = false, app_own = false;
+    uint4 app_w = make_uint4(0u, 0u, 0u, 0u);
+    if (lane < app_items) {
+        app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
+        if (app_own) app_w = load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e);
+    }
+    __syncthreads();
+    if (app_items != 0) {
+        if (app_own) app_store(app_pos, app_v, app_d, app_w);
+        for (uint32_t t = lane + 64; t < app_items; t += 64) {
+            if (app_decode(t, app_pos, app_v, app_d, app_e))
+                app_store(app_pos, app_v, app_d,
+                          load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e));
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+
+    float m = kFloor, l = 0.0f;
+    f32x4 o[MT];
+#pragma unroll
+    for (int i = 0; i < MT; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
     const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
     const uint32_t last = te > 0 ? te - 1 : 0;
@@ -619,26 +675,48 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     plan.n_items = n_items;
     plan.split = any_split;
     plan.hd_t = template_hd(hd);
+
+    // The append can run inside the attention launch when no query reads a
+    // token that another workgroup appends: the call is causal, every row's
+    // new token is its last key (hi == pos + 1), positions rise within a
+    // sequence chunk, each chunk fits in one group, and no sequence appears
+    // in two chunks.
+    bool fuse = sp.causal != 0;
+    std::vector<uint32_t> seen;
+    for (auto& c : rp.chunks) {
+        if (!fuse) break;
+        const uint32_t n = c.second - c.first;
+        fuse = G <= kCols ? n <= kCols / G : n == 1;
+        for (uint32_t r = c.first; r < c.second && fuse; r++) {
+            const uint32_t pos = args[8 * r];
+            fuse = rp.hi[r] == static_cast<uint64_t>(pos) + 1 && rp.lo[r] <= pos &&
+                   (r == c.first || pos > args[8 * (r - 1)]);
+        }
+        seen.push_back(rp.seq[c.first]);
+    }
+    if (fuse) {
+        std::sort(seen.begin(), seen.end());
+        fuse = std::adjacent_find(seen.begin(), seen.end()) == seen.end();
+    }
+    plan.fusable = fuse;
     return THB_OK;
 }
 
-}  // namespace
-}  // namespace thb
+struct AppendSrc {
+    const void* k;
+    const void* v;
+    uint32_t dtype;
+};
 
-using namespace thb;
-
-extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec,
-                        const thb_rows* rows, void* stream) {
-    if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
+int check_attn_call(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec& sp,
+                    const thb_rows* rows) {
     if (layer >= pool->layers)
         return fail(THB_ERR_INVALID, "layer " + std::to_string(layer) + " out of range (" +
                                          std::to_string(pool->layers) + " layers)");
-    const thb_attn_spec& sp = *spec;
-    if (sp.m == 0) return THB_OK;
     if (!q || !y) return fail(THB_ERR_INVALID, "null q or y");
     if (sp.q_heads == 0 || sp.q_heads % pool->kv_heads != 0)
-        return fail(THB_ERR_CONFIG, "q_heads " + std::to_string(sp.q_heads) + " must be a positive multiple of kv_heads " +
-                                        std::to_string(pool->kv_heads));
+        return fail(THB_ERR_CONFIG, "q_heads " + std::to_string(sp.q_heads) +
+                                        " must be a positive multiple of kv_heads " + std::to_string(pool->kv_heads));
     if (sp.q_dtype > THB_DT_F16 || sp.y_dtype > THB_DT_F16)
         return fail(THB_ERR_INVALID, "q_dtype and y_dtype must be THB_DT_F32 or THB_DT_F16");
     if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u))
@@ -649,92 +727,164 @@ extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, 
     if (sp.seq != THB_SEQ_PER_ROW && sp.seq >= pool->arena.a.seqs())
         return fail(THB_ERR_INVALID, "sequence " + std::to_string(sp.seq) + " out of range");
     if (!(sp.softcap >= 0.0f)) return fail(THB_ERR_INVALID, "softcap must be >= 0");
-    const uint32_t hd = pool->geom[layer].head_dim;
     if (pool->part_len >> pool->page_shift > kMaxPartPages)
         return fail(THB_ERR_CONFIG, "part_len / page_len must be at most " + std::to_string(kMaxPartPages));
+    return THB_OK;
+}
 
+// Finds or builds the launch plan of this call (cached per rows write, call
+// shape and allocator state).  Runs inside guarded().
+int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint32_t hd, hipStream_t s,
+             AttnPlan** out) {
+    const uint64_t av = pool->arena.a.version();
+    for (auto& p : pool->plans)
+        if (p.rows == rows && p.rows_version == rows->version && p.arena_version == av && p.row_off == sp.row_off &&
+            p.m == sp.m && p.seq == sp.seq && p.causal == sp.causal && p.window == sp.window &&
+            p.q_heads == sp.q_heads && p.head_dim == hd) {
+            p.last_use = ++pool->plan_clock;
+            *out = &p;
+            return THB_OK;
+        }
+    AttnPlan* plan = &pool->plans[0];
+    for (auto& p : pool->plans)
+        if (p.last_use < plan->last_use) plan = &p;
+    plan->rows = nullptr;
+    if (int rc = build_plan(pool, rows, sp, hd, *plan, s)) return rc;
+    plan->rows = rows;
+    plan->rows_version = rows->version;
+    plan->arena_version = av;
+    plan->row_off = sp.row_off;
+    plan->m = sp.m;
+    plan->seq = sp.seq;
+    plan->causal = sp.causal;
+    plan->window = sp.window;
+    plan->q_heads = sp.q_heads;
+    plan->head_dim = hd;
+    plan->last_use = ++pool->plan_clock;
+    *out = plan;
+    return THB_OK;
+}
+
+// Launches attention (and, when app is set, the fused append) for a plan.
+void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec& sp, const AttnPlan& plan,
+                 const AppendSrc* app, hipStream_t s) {
+    const uint32_t hd = pool->geom[layer].head_dim;
+    const uint32_t hd_t = plan.hd_t;
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    if (plan.split) {
+        const uint64_t n_part = static_cast<uint64_t>(plan.n_items) * pool->kv_heads * kCols;
+        const uint64_t o_bytes = (n_part * hd_t * 4 + 255) & ~uint64_t(255), ml_bytes = n_part * 8;
+        uint8_t* part = static_cast<uint8_t*>(pool->partials.reserve(o_bytes + ml_bytes, false));
+        part_o = reinterpret_cast<float*>(part);
+        part_ml = reinterpret_cast<float*>(part + o_bytes);
+    }
+    const uint32_t* blob = static_cast<const uint32_t*>(plan.dev.get());
+    const LayerGeom& g = pool->geom[layer];
+    AttnArgs a;
+    a.q = q;
+    a.y = y;
+    a.groups = blob;
+    a.items = blob + static_cast<size_t>(plan.n_groups) * kGroupWords;
+    a.ranges = a.items + plan.n_items;
+    a.table = pool->table_dev;
+    a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
+    a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
+    a.k_src = app ? app->k : nullptr;
+    a.v_src = app ? app->v : nullptr;
+    a.src_dtype = app ? app->dtype : 0u;
+    a.part_o = part_o;
+    a.part_ml = part_ml;
+    a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
+    a.max_pages = pool->arena.a.max_pages();
+    a.page_shift = pool->page_shift;
+    a.q_heads = sp.q_heads;
+    a.nq_per_kv = sp.q_heads / pool->kv_heads;
+    a.head_dim = hd;
+    a.part_len = pool->part_len;
+    a.n_kvh = pool->kv_heads;
+    const float log2e = 1.4426950408889634f;
+    if (sp.softcap > 0.0f) {
+        a.qscale = sp.scale / sp.softcap;
+        a.cap2 = sp.softcap * log2e;
+    } else {
+        a.qscale = sp.scale * log2e;
+        a.cap2 = 0.0f;
+    }
+    a.q_f16 = sp.q_dtype == THB_DT_F16;
+    a.y_f16 = sp.y_dtype == THB_DT_F16;
+    const bool f16 = pool->kv_dtype == THB_KV_F16_RNE;
+    launch(hd_t, f16, dim3(plan.n_items, pool->kv_heads), a, s);
+    THB_HIP(hipGetLastError());
+    if (plan.split) {
+        launch_merge(hd_t, dim3(plan.n_groups, pool->kv_heads), a, s);
+        THB_HIP(hipGetLastError());
+    }
+}
+
+}  // namespace
+}  // namespace thb
+
+using namespace thb;
+
+extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec,
+                        const thb_rows* rows, void* stream) {
+    if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
+    if (spec->m == 0) return layer < pool->layers ? THB_OK : check_attn_call(pool, layer, q, y, *spec, rows);
+    if (int rc = check_attn_call(pool, layer, q, y, *spec, rows)) return rc;
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
-        // Plan cache: one entry per (rows write, call shape, allocator state).
-        const uint64_t av = pool->arena.a.version();
         AttnPlan* plan = nullptr;
-        for (auto& p : pool->plans)
-            if (p.rows == rows && p.rows_version == rows->version && p.arena_version == av && p.row_off == sp.row_off &&
-                p.m == sp.m && p.seq == sp.seq && p.causal == sp.causal && p.window == sp.window &&
-                p.q_heads == sp.q_heads && p.head_dim == hd) {
-                plan = &p;
-                break;
-            }
-        if (!plan) {
-            plan = &pool->plans[0];
-            for (auto& p : pool->plans)
-                if (p.last_use < plan->last_use) plan = &p;
-            plan->rows = nullptr;
-            if (int rc = build_plan(pool, rows, sp, hd, *plan, s)) return rc;
-            plan->rows = rows;
-            plan->rows_version = rows->version;
-            plan->arena_version = av;
-            plan->row_off = sp.row_off;
-            plan->m = sp.m;
-            plan->seq = sp.seq;
-            plan->causal = sp.causal;
-            plan->window = sp.window;
-            plan->q_heads = sp.q_heads;
-            plan->head_dim = hd;
-        }
-        plan->last_use = ++pool->plan_clock;
+        if (int rc = get_plan(pool, rows, *spec, pool->geom[layer].head_dim, s, &plan)) return rc;
+        launch_plan(pool, layer, q, y, *spec, *plan, nullptr, s);
+        return THB_OK;
+    });
+}
 
-        const uint32_t hd_t = plan->hd_t;
-        const bool split = plan->split;
-        float* part_o = nullptr;
-        float* part_ml = nullptr;
-        if (split) {
-            const uint64_t n_part = static_cast<uint64_t>(plan->n_items) * pool->kv_heads * kCols;
-            const uint64_t o_bytes = (n_part * hd_t * 4 + 255) & ~uint64_t(255), ml_bytes = n_part * 8;
-            uint8_t* part = static_cast<uint8_t*>(pool->partials.reserve(o_bytes + ml_bytes, false));
-            part_o = reinterpret_cast<float*>(part);
-            part_ml = reinterpret_cast<float*>(part + o_bytes);
+extern "C" int thb_attn_append(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src,
+                               uint32_t src_dtype, const void* q, void* y, const thb_attn_spec* spec,
+                               const thb_rows* rows, void* stream) {
+    if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
+    if (spec->m == 0) return layer < pool->layers ? THB_OK : check_attn_call(pool, layer, q, y, *spec, rows);
+    if (int rc = check_attn_call(pool, layer, q, y, *spec, rows)) return rc;
+    if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
+    if (src_dtype > THB_DT_BF16) return fail(THB_ERR_INVALID, "unknown src_dtype " + std::to_string(src_dtype));
+    if ((reinterpret_cast<uintptr_t>(k_src) & 15u) || (reinterpret_cast<uintptr_t>(v_src) & 15u))
+        return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
+    // Pages must cover every appended token (thb_kv_store's check; the
+    // append takes each row's sequence from the row meta, kv_store.wgsl:39).
+    const Arena& arena = pool->arena.a;
+    for (uint32_t r = spec->row_off; r < spec->row_off + spec->m; r++) {
+        const uint32_t pos = rows->host[8 * r];
+        const uint32_t seq = rows->host[8 * r + 1];
+        if (seq >= arena.seqs())
+            return fail(THB_ERR_INVALID, "sequence " + std::to_string(seq) + " out of range (" +
+                                             std::to_string(arena.seqs()) + " sequences)");
+        if (pos == 0xFFFFFFFFu || !arena.covers(seq, pos + 1))
+            return fail(THB_ERR_MODEL, "pages must cover the chunk: sequence " + std::to_string(seq) + " holds " +
+                                           std::to_string(arena.table_of(seq).size() * arena.page_len()) +
+                                           " slots, needs " + std::to_string(static_cast<uint64_t>(pos) + 1));
+    }
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        AttnPlan* plan = nullptr;
+        if (int rc = get_plan(pool, rows, *spec, pool->geom[layer].head_dim, s, &plan)) return rc;
+        // The row meta's sequence must be the one the append uses: a fixed
+        // AttnSpec.seq that differs from the rows' own seq is not fused.
+        bool fuse = plan->fusable;
+        if (fuse && spec->seq != THB_SEQ_PER_ROW)
+            for (uint32_t r = spec->row_off; r < spec->row_off + spec->m && fuse; r++)
+                fuse = rows->host[8 * r + 1] == spec->seq;
+        if (fuse) {
+            const AppendSrc app{k_src, v_src, src_dtype};
+            launch_plan(pool, layer, q, y, *spec, *plan, &app, s);
+            return THB_OK;
         }
-
-        const uint32_t* blob = static_cast<const uint32_t*>(plan->dev.get());
-        const LayerGeom& g = pool->geom[layer];
-        AttnArgs a;
-        a.q = q;
-        a.y = y;
-        a.groups = blob;
-        a.items = blob + static_cast<size_t>(plan->n_groups) * kGroupWords;
-        a.ranges = a.items + plan->n_items;
-        a.table = pool->table_dev;
-        a.k = reinterpret_cast<const uint16_t*>(pool->mem + g.k_off);
-        a.v = reinterpret_cast<const uint16_t*>(pool->mem + g.v_off);
-        a.part_o = part_o;
-        a.part_ml = part_ml;
-        a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
-        a.max_pages = pool->arena.a.max_pages();
-        a.page_shift = pool->page_shift;
-        a.q_heads = sp.q_heads;
-        a.nq_per_kv = sp.q_heads / pool->kv_heads;
-        a.head_dim = hd;
-        a.part_len = pool->part_len;
-        a.n_kvh = pool->kv_heads;
-        const float log2e = 1.4426950408889634f;
-        if (sp.softcap > 0.0f) {
-            a.qscale = sp.scale / sp.softcap;
-            a.cap2 = sp.softcap * log2e;
-        } else {
-            a.qscale = sp.scale * log2e;
-            a.cap2 = 0.0f;
-        }
-        a.q_f16 = sp.q_dtype == THB_DT_F16;
-        a.y_f16 = sp.y_dtype == THB_DT_F16;
-        const bool f16 = pool->kv_dtype == THB_KV_F16_RNE;
-        launch(hd_t, f16, dim3(plan->n_items, pool->kv_heads), a, s);
-        THB_HIP(hipGetLastError());
-        if (split) {
-            launch_merge(hd_t, dim3(plan->n_groups, pool->kv_heads), a, s);
-            THB_HIP(hipGetLastError());
-        }
+        if (int rc = thb_kv_store(pool, layer, k_src, v_src, src_dtype, rows, spec->row_off, spec->m, stream))
+            return rc;
+        launch_plan(pool, layer, q, y, *spec, *plan, nullptr, s);
         return THB_OK;
     });
 }

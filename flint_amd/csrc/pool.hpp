@@ -35,6 +35,7 @@ struct AttnPlan {
     uint32_t n_groups = 0, n_items = 0;
     uint32_t hd_t = 0;   // head_dim template of the kernel
     bool split = false;  // some group spans several partitions: merge kernel runs
+    bool fusable = false;  // an append of the call's rows can run inside the launch
     DevBuf dev;  // [groups | items | row ranges]
     uint64_t last_use = 0;
 };

@@ -56,9 +56,7 @@ def kv_store(k_src, v_src, kv: KvPool, layer: int, m: int, meta: RowMeta, row_of
                              meta.handle, row_off, m, _stream_ptr(stream)))
 
 
-def attn(q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
-    """ops/attn.rs:18-51: paged attention of spec.m rows; q and y are
-    [m, q_heads, head_dim] (f32 as the reference, or f16)."""
+def _spec_c(spec: AttnSpec, q, y) -> _lib.AttnSpecC:
     c = _lib.AttnSpecC()
     c.q_heads, c.window, c.scale, c.m = spec.q_heads, spec.window, spec.scale, spec.m
     c.causal = 1 if spec.causal else 0
@@ -66,7 +64,24 @@ def attn(q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
     c.row_off, c.softcap = spec.row_off, spec.softcap
     c.q_dtype = _dtype_code(getattr(q, "dtype", None))
     c.y_dtype = _dtype_code(getattr(y, "dtype", None))
+    return c
+
+
+def attn(q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
+    """ops/attn.rs:18-51: paged attention of spec.m rows; q and y are
+    [m, q_heads, head_dim] (f32 as the reference, or f16)."""
+    c = _spec_c(spec, q, y)
     check(lib().thb_attn(kv.handle, layer, _ptr(q), _ptr(y), ctypes.byref(c), spec.args.handle, _stream_ptr(stream)))
+
+
+def kv_store_attn(k_src, v_src, q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
+    """kv_store of the spec's rows followed by attn (the per-layer step of
+    transformer/forward.rs:300-336), in one launch where the rows allow it;
+    bit-identical to calling the two."""
+    c = _spec_c(spec, q, y)
+    check(lib().thb_attn_append(kv.handle, layer, _ptr(k_src), _ptr(v_src),
+                                _dtype_code(getattr(k_src, "dtype", None)), _ptr(q), _ptr(y), ctypes.byref(c),
+                                spec.args.handle, _stream_ptr(stream)))
 
 
 def default_scale(head_dim: int) -> float:
@@ -89,4 +104,4 @@ def block_copy(kv: KvPool, triples: Sequence[Sequence[int]], stream=None) -> Non
 
 
 __all__ = ["AttnSpec", "ThubanError", "attn", "block_copy", "check_head_dim", "default_scale", "kv_gather",
-           "kv_scatter", "kv_store"]
+           "kv_scatter", "kv_store", "kv_store_attn"]

@@ -226,6 +226,16 @@ typedef struct thb_attn_spec {
 int thb_attn(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
              const thb_rows* rows, void* stream);
 
+/* thb_kv_store of rows [spec->row_off, spec->row_off + spec->m) followed by
+ * thb_attn(spec): the step the model runs per layer (transformer/forward.rs
+ * :300-336).  Results are bit-identical to the two calls.  When the call is
+ * causal, each sequence's rows fit in one query group (decode, and verify
+ * chunks of up to 16 / (q_heads / kv_heads) rows) and every row's new token
+ * is its last key, the append runs inside the attention launch (one kernel
+ * instead of two); otherwise the two kernels run in order. */
+int thb_attn_append(thb_pool* pool, uint32_t layer, const void* k_src_dev, const void* v_src_dev, uint32_t src_dtype,
+                    const void* q_dev, void* y_dev, const thb_attn_spec* spec, const thb_rows* rows, void* stream);
+
 /* No reference counterpart.  Copies tokens [t0, t0 + n) of seq, layer
  * `layer`, into contiguous k_dst/v_dst [kv_heads, n, head_dim] in the KV type
  * (bit copy). */

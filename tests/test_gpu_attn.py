@@ -259,3 +259,63 @@ def test_attn_errors(torch_cuda):
     ops.attn(q, pool, 0, y, ops.AttnSpec(4, 0, 0.125, 1, True, None, rows))
     torch.cuda.synchronize()
     assert torch.isfinite(y).all()
+
+
+FUSE_CASES = [
+    # name, nq, nkv, hd, kv, src dtype, rows per sequence, fused in one launch
+    ("decode-llama3-f16", 32, 8, 128, "f16", "f16", 1, True),
+    ("decode-qwen2-bf16-f32src", 14, 2, 64, "bf16", "f32", 1, True),
+    ("verify4-gemma2", 16, 8, 256, "f16", "f32", 4, True),
+    ("prefill40-fallback", 8, 2, 128, "f16", "bf16", 40, False),
+]
+
+
+@pytest.mark.parametrize("case", FUSE_CASES, ids=[c[0] for c in FUSE_CASES])
+def test_fused_append_matches_separate_calls(torch_cuda, case):
+    """kv_store_attn (thb_attn_append) gives bit-identical outputs and pool
+    contents to kv_store followed by attn, whether it fuses or falls back."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    name, nq, nkv, hd, kv, src, rps, _ = case
+    say("fused append", name)
+    lens = [700, 1500, 33]  # tokens already in the cache
+    budget = [n + rps for n in lens]
+    pools = []
+    for _ in range(2):
+        P = make_pool(budget, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype=kv, extra_pages=3)
+        scattered_alloc(P, budget, random.Random(zlib.crc32(name.encode())), 16)
+        pools.append(P)
+    rows = RowMeta(256)
+    for P in pools:
+        fill(torch, P, rows, lens, seed=7)
+    dt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[src]
+    positions, seqs = [], []
+    for s, n in enumerate(lens):
+        positions += list(range(n, n + rps))
+        seqs += [s] * rps
+    m = len(seqs)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    k_new = torch.randn(m, nkv, hd, device="cuda", generator=g).to(dt)
+    v_new = torch.randn(m, nkv, hd, device="cuda", generator=g).to(dt)
+    q = torch.randn(m, nq, hd, device="cuda", generator=g)
+    rows.write(positions, seqs, m)
+    spec = ops.AttnSpec(q_heads=nq, window=0, scale=1 / math.sqrt(hd), m=m, causal=True, seq=None, args=rows)
+    ya = torch.empty_like(q)
+    yb = torch.empty_like(q)
+    ops.kv_store(k_new, v_new, pools[0], 0, m, rows)
+    ops.attn(q, pools[0], 0, ya, spec)
+    ops.kv_store_attn(k_new, v_new, q, pools[1], 0, yb, spec)
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb)
+    ka, va = pools[0].read_layer(0)
+    kb, vb = pools[1].read_layer(0)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    # and the output is right: oracle over the appended cache
+    want = oracle_layer(torch, pools[1]).attn(q.cpu().numpy(), oracle.row_meta(positions, seqs), m, nq,
+                                              1 / math.sqrt(hd))
+    err = float(np.max(np.abs(yb.cpu().numpy() - want)))
+    say("fused append", name, "max abs err", err)
+    assert err <= TOL
