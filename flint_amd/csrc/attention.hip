@@ -19,8 +19,9 @@
 //    v_mfma_f32_16x16x32_{f16,bf16}.  The A operand is 16 bytes of one key
 //    per lane; the pool keeps K pages chunk-major ([head_dim/8][page_len][8])
 //    so that one load instruction covers 1 KiB of contiguous memory.  The B
-//    operand is Q^T held in registers.  Q is split into a high and a low half-precision part and
-//    both are multiplied, which keeps the products at f32 accuracy.
+//    operand is Q^T held in registers.  Q is split into a high and a low
+//    half-precision part and both are multiplied, which keeps the products
+//    at f32 accuracy; the softmax scale is applied to the f32 scores.
 //  * S^T leaves lane (a, c) holding tokens 4a..4a+3 of column c.  That is
 //    exactly the B-operand layout of v_mfma_f32_16x16x16 for P^T, so the
 //    probabilities feed the PV product without any lane exchange.  The A
@@ -224,7 +225,9 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
         chi = min(a.ranges[2 * row + 1], te);
     }
 
-    // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8] * qscale, split.
+    // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8], split into high
+    // and low halves.  The raw query is split and the f32 scores are scaled
+    // afterwards, so the low half stays out of the f16 subnormal range.
     in8 qh[KS], ql[KS];
     {
         const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
@@ -250,8 +253,6 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; e++) x[e] = 0.0f;
             }
-#pragma unroll
-            for (int e = 0; e < 8; e++) x[e] *= a.qscale;
             O::split8(x, qh[j], ql[j]);
         }
     }
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
         float mx = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            float x = s[e];
+            float x = s[e] * a.qscale;
             if (a.cap2 != 0.0f) x = a.cap2 * tanh_approx(x);
             const uint32_t t = t0 + 4u * a4 + e;
             x = (t >= clo && t < chi) ? x : -INFINITY;

@@ -63,3 +63,59 @@ def make_pool(lens, kv_heads, head_dim, page_len=16, kv_dtype="f16", layers=1, e
     pages = sum(-(-n // page_len) for n in seq_lens) + extra_pages
     return KvPool(ArenaSpec(seq_lens, pages), kv_heads, head_dim, layers=layers, page_len=page_len,
                   kv_dtype=kv_dtype, part_len=part_len, head_dims=head_dims)
+
+
+def oracle_seq(torch, pool: KvPool, layer: int, seq: int, n: int) -> oracle.Layer:
+    """Oracle layer holding only tokens [0, n) of `seq`, gathered through the
+    product's gather kernel into contiguous pages (identity block table,
+    the sequence is oracle sequence 0).  Works at any pool size."""
+    from flint_amd import ops
+
+    info = pool.layer_info(layer)
+    P = info.page_len
+    pages = -(-n // P)
+    kd = torch.empty(info.kv_heads, n, info.head_dim, dtype=torch.int16, device="cuda")
+    vd = torch.empty_like(kd)
+    ops.kv_gather(pool, layer, seq, 0, n, kd, vd)  # contiguous [kv_heads, n, head_dim]
+    torch.cuda.synchronize()
+    k = np.zeros((info.kv_heads, pages * P, info.head_dim), np.uint16)
+    v = np.zeros_like(k)
+    k[:, :n] = kd.cpu().numpy().view(np.uint16)
+    v[:, :n] = vd.cpu().numpy().view(np.uint16)
+    return oracle.Layer(info.kv_heads, info.head_dim, pages, P, np.arange(pages, dtype=np.uint32), pages,
+                        KV_CODE[pool.kv_dtype], k=k, v=v)
+
+
+def fill_layer_random(torch, pool: KvPool, layer: int, seed: int, scale: float = 1.0) -> None:
+    """N(0, scale^2) f16/bf16 words in every slot of a layer (layout-agnostic)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    dt = torch.float16 if pool.kv_dtype == "f16" else torch.bfloat16
+    for t in pool.layer_tensors(layer):
+        w = t.view(dt)
+        w.normal_(generator=g)
+        if scale != 1.0:
+            w.mul_(scale)
+    torch.cuda.synchronize()
+
+
+def fragment(pool: KvPool, filler_seqs, occupied_frac: float, rng) -> None:
+    """Fills the free list with a random scattering: every page goes to a
+    random filler sequence one page at a time, then a random subset of the
+    filler sequences is freed so that `occupied_frac` of the pages stay
+    held.  Filler sequence budgets must cover their share of the pool."""
+    pages = pool.arena.pages()
+    owners = [filler_seqs[rng.randrange(len(filler_seqs))] for _ in range(pages)]
+    have = {s: 0 for s in filler_seqs}
+    P = pool.page_len
+    for s in owners:
+        pool.alloc(s, have[s] * P, P)
+        have[s] += 1
+    order = list(filler_seqs)
+    rng.shuffle(order)
+    freed = 0
+    for s in order:
+        if freed >= (1.0 - occupied_frac) * pages:
+            break
+        freed += have[s]
+        pool.free_seq(s)
