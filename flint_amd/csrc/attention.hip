@@ -9,12 +9,14 @@
 //  * A "group" holds up to 16 query vectors that read the same keys: R rows
 //    of one sequence x H query heads of one KV head.  Every K/V byte of a
 //    group is loaded once for all of its query vectors (GQA packing).
-//  * Keys are cut into fixed logical partitions of part_len tokens.  One
+//  * A group's key span (from its first key rounded down to the page and tile
+//    size) is cut into n = ceil(span / part_len) equal partitions.  One
 //    workgroup of W waves handles one (group, partition, KV head); the waves
 //    split the partition into W contiguous runs of 16-token tiles.  All
 //    boundaries depend only on the group's own key range, so a row's
 //    arithmetic is the same whatever else is in the batch and wherever its
 //    pages sit: batch == solo and paged == contiguous hold bit-exactly.
+//    Work items are launched longest first.
 //  * Scores come from MFMA: S^T[16 tokens x 16 columns] = K Q^T with
 //    v_mfma_f32_16x16x32_{f16,bf16}.  The A operand is 16 bytes of one key
 //    per lane; the pool keeps K pages chunk-major ([head_dim/8][page_len][8])
@@ -44,10 +46,11 @@ namespace {
 
 constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units)
 constexpr float kFloor = -1.0e30f;    // initial running max (finite on purpose)
-constexpr uint32_t kGroupWords = 10;  // r0, R, h0, H, seq, lo, hi, n_parts, part0, item0
+constexpr uint32_t kGroupWords = 11;  // r0, R, h0, H, seq, lo, hi, n_parts, base, plen, item0
 constexpr uint32_t kMaxPartPages = 1024;
 constexpr uint32_t kMaxParts = 512;   // partitions of one group the merge kernel takes
 constexpr uint32_t kCols = 16;        // query vectors per group (MFMA N)
+constexpr uint32_t kBlockWords = 9;   // g0, ng, seq, lo, hi, n_parts, base, plen, bitem0
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -62,6 +65,8 @@ struct AttnArgs {
     const uint32_t* groups;
     const uint32_t* items;   // work item -> group
     const uint32_t* ranges;  // [m][2]: lo, hi
+    const uint32_t* blocks;  // prefill blocks of consecutive groups
+    const uint32_t* bitems;  // prefill work item -> block
     const uint32_t* table;
     uint16_t* k;
     uint16_t* v;
@@ -188,14 +193,14 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     const uint32_t a4 = lane >> 4, c = lane & 15u;
-    const uint32_t item = blockIdx.x, kvh = blockIdx.y;
+    // 1-D grid, KV head fastest: consecutive workgroups share a work item,
+    // and items are ordered longest first (the host sorts them).
+    const uint32_t item = blockIdx.x / a.n_kvh, kvh = blockIdx.x - item * a.n_kvh;
 
     const uint32_t* G = a.groups + a.items[item] * kGroupWords;
     const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3], seq = G[4];
-    const uint32_t glo = G[5], ghi = G[6], n_parts = G[7], part0 = G[8], item0 = G[9];
-    const uint32_t part = part0 + (item - item0);
-    const uint32_t P = a.part_len;
-    const uint32_t pbeg = part * P;
+    const uint32_t glo = G[5], ghi = G[6], n_parts = G[7], gbase = G[8], P = G[9], item0 = G[10];
+    const uint32_t pbeg = gbase + (item - item0) * P;
     const uint32_t tb = max(glo, pbeg), te = min(ghi, pbeg + P);
     const uint32_t hd = a.head_dim;
     const uint32_t pshift = a.page_shift;
@@ -478,7 +483,7 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
     const uint32_t g = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const uint32_t* G = a.groups + g * kGroupWords;
     const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3];
-    const uint32_t n_parts = G[7], item0 = G[9];
+    const uint32_t n_parts = G[7], item0 = G[10];
     if (n_parts <= 1) return;
     const uint32_t ncols = R * H;
     const uint32_t hd = a.head_dim;
@@ -513,6 +518,267 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
     }
 }
 
+// Chunked prefill (and any sequence chunk that needs more than one group).
+// One workgroup of W waves handles a block of up to W consecutive groups of
+// one chunk (wave w: group g0 + w) for one KV head and one partition of the
+// block's key span.  K and V tiles of TT tokens are loaded once per
+// workgroup into LDS (double-buffered: the next tile's global loads are in
+// flight while the waves compute on the current one) and shared by all
+// waves; each wave skips the 16-token slices outside its group's keys (the
+// causal triangle).  The per-slice arithmetic is the decode kernel's: split
+// Q and P, MFMA, online softmax with the lazy rescale.
+//   K tile in LDS: [TT/16 slices][HD/8 chunks][16 tokens] x 16 bytes, the
+//     order of a chunk-major page, so 8 lanes of an operand read are 128
+//     contiguous bytes.
+//   V tile in LDS: [TT/16 slices][HD dims][4 groups of 4 tokens] x 8 bytes,
+//     the group index XOR-ed with (dim / 8) % 4 so that the 16 lanes of a
+//     PV operand read hit distinct banks.
+template <int HD, bool F16, int W>
+__global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
+    using O = Ops<F16>;
+    typedef typename O::in8 in8;
+    typedef typename O::in4 in4;
+    constexpr int KS = HD / 32;
+    constexpr int MT = HD / 16;
+    constexpr int TT = HD <= 128 ? 64 : (HD == 256 ? 32 : 16);
+    constexpr int ST = TT / 16;
+    constexpr int KU = TT * HD / 8;  // 16-byte K units per tile
+    constexpr int VU = TT * HD / 8;  // 16-byte V units per tile (8 tokens of one dim)
+    constexpr int NT = 64 * W;
+    constexpr int KPT = (KU + NT - 1) / NT;
+    constexpr int VPT = (VU + NT - 1) / NT;
+
+    __shared__ u32x4 s_k[2][KU];
+    __shared__ u32x2 s_v[2][ST * HD * 4];
+    __shared__ uint32_t s_page[kMaxPartPages];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t a4 = lane >> 4, c = lane & 15u;
+    const uint32_t bitem = blockIdx.x / a.n_kvh, kvh = blockIdx.x - bitem * a.n_kvh;
+
+    const uint32_t* Bk = a.blocks + a.bitems[bitem] * kBlockWords;
+    const uint32_t g0 = Bk[0], ng = Bk[1], seq = Bk[2], blo = Bk[3], bhi = Bk[4];
+    const uint32_t n_parts = Bk[5], bbase = Bk[6], P = Bk[7], bitem0 = Bk[8];
+    const uint32_t part = bitem - bitem0;
+    const uint32_t pbeg = bbase + part * P;
+    const uint32_t tb = max(blo, pbeg), te = min(bhi, pbeg + P);
+    const uint32_t hd = a.head_dim;
+    const uint32_t pshift = a.page_shift;
+    const uint32_t pmask = (1u << pshift) - 1u;
+    const uint32_t last = te > 0 ? te - 1 : 0;
+
+    {
+        const uint32_t npg = P >> pshift;
+        const uint32_t lp0 = pbeg >> pshift;
+        const uint32_t* trow = a.table + static_cast<uint64_t>(seq) * a.max_pages;
+        for (uint32_t i = tid; i < npg; i += NT) {
+            const uint32_t lp = lp0 + i;
+            const bool used = tb < te && (lp << pshift) < te && ((lp + 1) << pshift) > tb;
+            s_page[i] = used ? trow[lp] : 0u;
+        }
+    }
+
+    // This wave's group and its columns.
+    const bool gon = wave < ng;
+    const uint32_t* G = a.groups + (g0 + (gon ? wave : 0u)) * kGroupWords;
+    const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3], item0 = G[10];
+    const uint32_t wlo = max(G[5], tb), whi = min(G[6], te);
+    const uint32_t ncols = gon ? R * H : 0u;
+    const bool con = c < ncols;
+    const uint32_t rr = con ? c / H : 0u;
+    const uint32_t row = r0 + rr;
+    const uint32_t head = kvh * a.nq_per_kv + h0 + (con ? c - rr * H : 0u);
+    uint32_t clo = 0, chi = 0;
+    if (con) {
+        clo = max(a.ranges[2 * row], tb);
+        chi = min(a.ranges[2 * row + 1], te);
+    }
+    in8 qh[KS], ql[KS];
+    {
+        const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const uint32_t d0 = 32u * j + 8u * a4;
+            float x[8];
+            if (con && d0 < hd) {
+                if (a.q_f16) {
+                    const f16x8 w = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.q) + qbase + d0);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) x[e] = static_cast<float>(w[e]);
+                } else {
+                    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + qbase + d0);
+                    const f32x4 u0 = p[0], u1 = p[1];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        x[e] = u0[e];
+                        x[4 + e] = u1[e];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = 0.0f;
+            }
+            O::split8(x, qh[j], ql[j]);
+        }
+    }
+
+    const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
+    const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
+    const uint32_t cph = HD / 8;
+
+    // Global -> registers for one tile; tokens outside [tb, te) are clamped
+    // into it (their scores are masked).
+    auto load = [&](uint32_t t0, u32x4 (&kr)[KPT], u32x4 (&vr)[VPT]) {
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const uint32_t u = tid + k * NT;
+            const uint32_t st = u / (16 * cph), rem = u - st * (16 * cph);
+            const uint32_t ch = rem >> 4, tok = rem & 15u;
+            const uint32_t t = min(max(t0 + 16u * st + tok, tb), last);
+            const uint32_t page = s_page[(t - pbeg) >> pshift];
+            const bool ok = u < static_cast<uint32_t>(KU) && 8u * ch < hd;
+            kr[k] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                             kplane + ((static_cast<uint64_t>(page) * hd + 8u * ch) << pshift) + ((t & pmask) << 3)))
+                       : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const uint32_t u = tid + k * NT;
+            const uint32_t st = u / (2 * HD), rem = u - st * (2 * HD);
+            const uint32_t d = rem >> 1, h8 = rem & 1u;
+            const uint32_t t = min(max(t0 + 16u * st + 8u * h8, tb & ~7u), last & ~7u);
+            const uint32_t page = s_page[(t - pbeg) >> pshift];
+            const bool ok = u < static_cast<uint32_t>(VU) && d < hd;
+            vr[k] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                             vplane + ((static_cast<uint64_t>(page) * hd + d) << pshift) + (t & pmask)))
+                       : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto store = [&](int buf, const u32x4 (&kr)[KPT], const u32x4 (&vr)[VPT]) {
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const uint32_t u = tid + k * NT;
+            if (u < static_cast<uint32_t>(KU)) s_k[buf][u] = kr[k];
+        }
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const uint32_t u = tid + k * NT;
+            if (u >= static_cast<uint32_t>(VU)) continue;
+            const uint32_t st = u / (2 * HD), rem = u - st * (2 * HD);
+            const uint32_t d = rem >> 1, h8 = rem & 1u;
+            const uint32_t sw = (d >> 3) & 3u;
+            u32x2* row4 = &s_v[buf][(st * HD + d) * 4];
+            row4[(2u * h8) ^ sw] = u32x2{vr[k].x, vr[k].y};
+            row4[(2u * h8 + 1u) ^ sw] = u32x2{vr[k].z, vr[k].w};
+        }
+    };
+
+    float m = kFloor, l = 0.0f;
+    f32x4 o[MT];
+#pragma unroll
+    for (int i = 0; i < MT; i++) o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](int buf, uint32_t t0) {
+#pragma unroll
+        for (int st = 0; st < ST; st++) {
+            const uint32_t ts = t0 + 16u * st;
+            if (ts >= whi || ts + 16u <= wlo) continue;  // outside this wave's keys
+            f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < KS; j++) {
+                const u32x4 kv = s_k[buf][(st * cph + 4u * j + a4) * 16u + c];
+                s = O::qk(kv, qh[j], s);
+                s = O::qk(kv, ql[j], s);
+            }
+            float sv[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float x = s[e] * a.qscale;
+                if (a.cap2 != 0.0f) x = a.cap2 * tanh_approx(x);
+                const uint32_t t = ts + 4u * a4 + e;
+                x = (t >= clo && t < chi) ? x : -INFINITY;
+                sv[e] = x;
+                mx = fmaxf(mx, x);
+            }
+            mx = col_max(mx);
+            if (mx > m + kTau) {
+                const float alpha = fast_exp2(m - mx);
+                l *= alpha;
+#pragma unroll
+                for (int i = 0; i < MT; i++) o[i] *= alpha;
+                m = mx;
+            }
+            float p[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                p[e] = fast_exp2(sv[e] - m);
+                l += p[e];
+            }
+            in4 ph, pl;
+            O::split4(p, ph, pl);
+#pragma unroll
+            for (int i = 0; i < MT; i++) {
+                const uint32_t d = 16u * i + c;
+                const u32x2 vv = s_v[buf][(st * HD + d) * 4 + (a4 ^ ((d >> 3) & 3u))];
+                o[i] = O::pv(vv, ph, o[i]);
+                o[i] = O::pv(vv, pl, o[i]);
+            }
+        }
+    };
+
+    const uint32_t t_first = tb & ~15u;
+    const uint32_t n_tiles = te > t_first ? (te - t_first + TT - 1) / TT : 0u;
+    __syncthreads();  // s_page complete
+    {
+        u32x4 kr[KPT], vr[VPT];
+        if (n_tiles) {
+            load(t_first, kr, vr);
+            store(0, kr, vr);
+        }
+        __syncthreads();
+        for (uint32_t i = 0; i < n_tiles; i++) {
+            const uint32_t t0 = t_first + i * TT;
+            const bool more = i + 1 < n_tiles;
+            if (more) load(t0 + TT, kr, vr);
+            if (gon) compute(static_cast<int>(i & 1u), t0);
+            if (more) store(static_cast<int>((i + 1) & 1u), kr, vr);
+            __syncthreads();
+        }
+    }
+    l = col_sum(l);
+    if (!con) return;
+
+    if (n_parts == 1) {
+        const float inv = 1.0f / l;
+        const uint64_t ybase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            const uint32_t d = 16u * i + 4u * a4;
+            if (d >= hd) continue;
+            const f32x4 yv = o[i] * inv;
+            if (a.y_f16) {
+                f16x4 h;
+#pragma unroll
+                for (int e = 0; e < 4; e++) h[e] = static_cast<_Float16>(yv[e]);
+                *reinterpret_cast<f16x4*>(static_cast<_Float16*>(a.y) + ybase + d) = h;
+            } else {
+                *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + ybase + d) = yv;
+            }
+        }
+        return;
+    }
+    const uint64_t pb = (static_cast<uint64_t>(item0 + part) * a.n_kvh + kvh) * kCols + c;
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+        *reinterpret_cast<f32x4*>(a.part_o + pb * HD + 16u * i + 4u * a4) = o[i];
+    if (a4 == 0) {
+        a.part_ml[2 * pb] = m;
+        a.part_ml[2 * pb + 1] = l;
+    }
+}
+
 // ------------------------------------------------------------ host side
 uint32_t template_hd(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : hd <= 256 ? 256 : 512; }
 
@@ -541,6 +807,21 @@ void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s
         case 128: f16 ? launch_hd<128, true>(grid, a, s) : launch_hd<128, false>(grid, a, s); break;
         case 256: f16 ? launch_hd<256, true>(grid, a, s) : launch_hd<256, false>(grid, a, s); break;
         default: f16 ? launch_hd<512, true>(grid, a, s) : launch_hd<512, false>(grid, a, s); break;
+    }
+}
+
+template <int HD, bool F16>
+void launch_prefill_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
+    constexpr int W = waves_for(HD);
+    hipLaunchKernelGGL((attn_prefill<HD, F16, W>), grid, dim3(64 * W), 0, s, a);
+}
+
+void launch_prefill(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
+    switch (hd_t) {
+        case 64: f16 ? launch_prefill_hd<64, true>(grid, a, s) : launch_prefill_hd<64, false>(grid, a, s); break;
+        case 128: f16 ? launch_prefill_hd<128, true>(grid, a, s) : launch_prefill_hd<128, false>(grid, a, s); break;
+        case 256: f16 ? launch_prefill_hd<256, true>(grid, a, s) : launch_prefill_hd<256, false>(grid, a, s); break;
+        default: f16 ? launch_prefill_hd<512, true>(grid, a, s) : launch_prefill_hd<512, false>(grid, a, s); break;
     }
 }
 
@@ -617,10 +898,32 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
                                            std::to_string(rp.hi[r]));
     }
 
-    std::vector<uint32_t> groups, items;
-    const uint32_t P = pool->part_len;
+    // Partitions of a group (or of a prefill block) start at its first key
+    // (rounded down to the page and tile size) and split its span into
+    // n = ceil(span / part_len) equal parts: a function of its own key range
+    // only.
+    std::vector<uint32_t> groups, items, blocks, bitems;
+    const uint32_t PL = pool->part_len;
+    const uint32_t align = std::max<uint32_t>(pool->page_len, 16);
+    const uint32_t hd_t = template_hd(hd);
+    const uint32_t WB = static_cast<uint32_t>(hd_t >= 256 ? 4 : 8);  // waves of attn_prefill
     uint32_t max_parts = 0;
     bool any_split = false;
+    auto partition = [&](uint32_t& lo, uint32_t& hi, uint32_t& base, uint32_t& n_parts, uint32_t& plen) {
+        base = 0;
+        n_parts = 1;
+        plen = align;
+        if (hi <= lo || lo == 0xFFFFFFFFu) {
+            lo = hi = 0;  // no keys: one empty partition, output 0/0 = NaN
+        } else {
+            base = lo & ~(align - 1);
+            const uint64_t span = uint64_t(hi) - base;
+            n_parts = static_cast<uint32_t>((span + PL - 1) / PL);
+            plen = static_cast<uint32_t>(((span + n_parts - 1) / n_parts + align - 1) / align * align);
+        }
+        max_parts = std::max(max_parts, n_parts);
+        any_split = any_split || n_parts > 1;
+    };
     auto add_group = [&](uint32_t r0, uint32_t R, uint32_t h0, uint32_t H, uint32_t seq) {
         uint32_t lo = 0xFFFFFFFFu, hi = 0;
         for (uint32_t r = r0; r < r0 + R; r++) {
@@ -628,24 +931,17 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
             lo = std::min(lo, rp.lo[r]);
             hi = std::max(hi, rp.hi[r]);
         }
-        uint32_t part0, n_parts;
-        if (hi <= lo || lo == 0xFFFFFFFFu) {
-            lo = hi = 0;  // no keys: one empty partition, output 0/0 = NaN
-            part0 = 0;
-            n_parts = 1;
-        } else {
-            part0 = lo / P;
-            n_parts = (hi - 1) / P - part0 + 1;
-        }
-        max_parts = std::max(max_parts, n_parts);
-        any_split = any_split || n_parts > 1;
-        const uint32_t gidx = static_cast<uint32_t>(groups.size() / kGroupWords);
-        const uint32_t item0 = static_cast<uint32_t>(items.size());
-        groups.insert(groups.end(), {r0, R, h0, H, seq, lo, hi, n_parts, part0, item0});
-        for (uint32_t i = 0; i < n_parts; i++) items.push_back(gidx);
+        uint32_t base, n_parts, plen;
+        partition(lo, hi, base, n_parts, plen);
+        groups.insert(groups.end(), {r0, R, h0, H, seq, lo, hi, n_parts, base, plen, 0u});
     };
+    // A chunk that needs at least 4 groups (a prefill chunk) is cut into
+    // blocks of WB consecutive groups for attn_prefill; the others go to the
+    // decode kernel.
+    std::vector<uint8_t> in_block;
     for (auto& c : rp.chunks) {
         const uint32_t seq = rp.seq[c.first];
+        const uint32_t first = static_cast<uint32_t>(groups.size() / kGroupWords);
         if (G <= kCols) {
             const uint32_t rg = kCols / G;
             for (uint32_t r = c.first; r < c.second; r += rg) add_group(r, std::min(rg, c.second - r), 0, G, seq);
@@ -653,29 +949,92 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
             for (uint32_t r = c.first; r < c.second; r++)
                 for (uint32_t h0 = 0; h0 < G; h0 += kCols) add_group(r, 1, h0, std::min(kCols, G - h0), seq);
         }
+        const uint32_t ncg = static_cast<uint32_t>(groups.size() / kGroupWords) - first;
+        in_block.resize(first + ncg, 0);
+        if (G > kCols || ncg < 4) continue;
+        for (uint32_t b = 0; b < ncg; b += WB) {
+            const uint32_t g0 = first + b, ng = std::min(WB, ncg - b);
+            uint32_t lo = 0xFFFFFFFFu, hi = 0;
+            for (uint32_t g = g0; g < g0 + ng; g++) {
+                const uint32_t* gr = &groups[static_cast<size_t>(g) * kGroupWords];
+                in_block[g] = 1;
+                if (gr[6] <= gr[5]) continue;
+                lo = std::min(lo, gr[5]);
+                hi = std::max(hi, gr[6]);
+            }
+            uint32_t base, n_parts, plen;
+            partition(lo, hi, base, n_parts, plen);
+            for (uint32_t g = g0; g < g0 + ng; g++) {  // members share the block's partitions
+                uint32_t* gr = &groups[static_cast<size_t>(g) * kGroupWords];
+                gr[7] = n_parts;
+                gr[8] = base;
+                gr[9] = plen;
+            }
+            blocks.insert(blocks.end(), {g0, ng, seq, lo, hi, n_parts, base, plen, 0u});
+        }
     }
     if (max_parts > kMaxParts)
-        return fail(THB_ERR_CONFIG, "context of " + std::to_string(static_cast<uint64_t>(max_parts) * P) +
+        return fail(THB_ERR_CONFIG, "context of " + std::to_string(static_cast<uint64_t>(max_parts) * PL) +
                                         " tokens exceeds " + std::to_string(kMaxParts) + " partitions of " +
-                                        std::to_string(P) + " tokens");
+                                        std::to_string(PL) + " tokens");
     const uint32_t n_groups = static_cast<uint32_t>(groups.size() / kGroupWords);
+    const uint32_t n_blocks = static_cast<uint32_t>(blocks.size() / kBlockWords);
+    // Work items, longest partitions first, so that the short ones fill in
+    // behind them (the order does not change any row's arithmetic).  Decode
+    // items come first in the partial-result slots, then block members.
+    auto work = [](const uint32_t* r, uint32_t lo_i, uint32_t hi_i, uint32_t base_i, uint32_t plen_i) {
+        return std::min(r[plen_i], r[hi_i] - r[base_i]);
+    };
+    std::vector<uint32_t> order;
+    for (uint32_t g = 0; g < n_groups; g++)
+        if (!in_block[g]) order.push_back(g);
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
+        return work(&groups[static_cast<size_t>(x) * kGroupWords], 5, 6, 8, 9) >
+               work(&groups[static_cast<size_t>(y) * kGroupWords], 5, 6, 8, 9);
+    });
+    for (uint32_t g : order) {
+        groups[static_cast<size_t>(g) * kGroupWords + 10] = static_cast<uint32_t>(items.size());
+        for (uint32_t i = 0; i < groups[static_cast<size_t>(g) * kGroupWords + 7]; i++) items.push_back(g);
+    }
     const uint32_t n_items = static_cast<uint32_t>(items.size());
+    uint32_t n_slots = n_items;
+    for (uint32_t g = 0; g < n_groups; g++)
+        if (in_block[g]) {
+            groups[static_cast<size_t>(g) * kGroupWords + 10] = n_slots;
+            n_slots += groups[static_cast<size_t>(g) * kGroupWords + 7];
+        }
+    std::vector<uint32_t> border(n_blocks);
+    for (uint32_t b = 0; b < n_blocks; b++) border[b] = b;
+    std::stable_sort(border.begin(), border.end(), [&](uint32_t x, uint32_t y) {
+        return work(&blocks[static_cast<size_t>(x) * kBlockWords], 3, 4, 6, 7) >
+               work(&blocks[static_cast<size_t>(y) * kBlockWords], 3, 4, 6, 7);
+    });
+    for (uint32_t b : border) {
+        blocks[static_cast<size_t>(b) * kBlockWords + 8] = static_cast<uint32_t>(bitems.size());
+        for (uint32_t i = 0; i < blocks[static_cast<size_t>(b) * kBlockWords + 5]; i++) bitems.push_back(b);
+    }
+    const uint32_t n_bitems = static_cast<uint32_t>(bitems.size());
     if (n_items > 0x7FFFFFFFu || n_groups > 0x7FFFFFFFu) return fail(THB_ERR_CONFIG, "attention call too large");
 
     std::vector<uint32_t> blob;
-    blob.reserve(groups.size() + items.size() + 2 * m);
+    blob.reserve(groups.size() + items.size() + 2 * m + blocks.size() + bitems.size());
     blob.insert(blob.end(), groups.begin(), groups.end());
     blob.insert(blob.end(), items.begin(), items.end());
     for (uint32_t r = 0; r < m; r++) {
         blob.push_back(rp.lo[r]);
         blob.push_back(rp.hi[r]);
     }
+    blob.insert(blob.end(), blocks.begin(), blocks.end());
+    blob.insert(blob.end(), bitems.begin(), bitems.end());
     void* dev = plan.dev.reserve(blob.size() * 4, false);
     pool->stager.upload(dev, blob.data(), blob.size() * 4, stream);
     plan.n_groups = n_groups;
     plan.n_items = n_items;
+    plan.n_blocks = n_blocks;
+    plan.n_bitems = n_bitems;
+    plan.n_slots = n_slots;
     plan.split = any_split;
-    plan.hd_t = template_hd(hd);
+    plan.hd_t = hd_t;
 
     // The append can run inside the attention launch when no query reads a
     // token that another workgroup appends: the call is causal, every row's
@@ -774,7 +1133,7 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
     float* part_o = nullptr;
     float* part_ml = nullptr;
     if (plan.split) {
-        const uint64_t n_part = static_cast<uint64_t>(plan.n_items) * pool->kv_heads * kCols;
+        const uint64_t n_part = static_cast<uint64_t>(plan.n_slots) * pool->kv_heads * kCols;
         const uint64_t o_bytes = (n_part * hd_t * 4 + 255) & ~uint64_t(255), ml_bytes = n_part * 8;
         uint8_t* part = static_cast<uint8_t*>(pool->partials.reserve(o_bytes + ml_bytes, false));
         part_o = reinterpret_cast<float*>(part);
@@ -788,6 +1147,8 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
     a.groups = blob;
     a.items = blob + static_cast<size_t>(plan.n_groups) * kGroupWords;
     a.ranges = a.items + plan.n_items;
+    a.blocks = a.ranges + 2 * static_cast<size_t>(sp.m);
+    a.bitems = a.blocks + static_cast<size_t>(plan.n_blocks) * kBlockWords;
     a.table = pool->table_dev;
     a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
     a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
@@ -815,8 +1176,18 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
     a.q_f16 = sp.q_dtype == THB_DT_F16;
     a.y_f16 = sp.y_dtype == THB_DT_F16;
     const bool f16 = pool->kv_dtype == THB_KV_F16_RNE;
-    launch(hd_t, f16, dim3(plan.n_items, pool->kv_heads), a, s);
-    THB_HIP(hipGetLastError());
+    const uint64_t n_wg = static_cast<uint64_t>(plan.n_items) * pool->kv_heads;
+    const uint64_t n_pwg = static_cast<uint64_t>(plan.n_bitems) * pool->kv_heads;
+    if (n_wg > 0x7FFFFFFFull || n_pwg > 0x7FFFFFFFull)
+        throw HipError{hipErrorInvalidConfiguration, "attention grid too large"};
+    if (n_wg) {
+        launch(hd_t, f16, dim3(static_cast<uint32_t>(n_wg)), a, s);
+        THB_HIP(hipGetLastError());
+    }
+    if (n_pwg) {
+        launch_prefill(hd_t, f16, dim3(static_cast<uint32_t>(n_pwg)), a, s);
+        THB_HIP(hipGetLastError());
+    }
     if (plan.split) {
         launch_merge(hd_t, dim3(plan.n_groups, pool->kv_heads), a, s);
         THB_HIP(hipGetLastError());

@@ -32,7 +32,9 @@ struct AttnPlan {
     uint64_t arena_version = ~0ull;
     uint32_t row_off = 0, m = 0, seq = 0, causal = 0, window = 0, q_heads = 0, head_dim = 0;
     // value
-    uint32_t n_groups = 0, n_items = 0;
+    uint32_t n_groups = 0, n_items = 0;     // decode work items
+    uint32_t n_blocks = 0, n_bitems = 0;    // prefill blocks and their work items
+    uint32_t n_slots = 0;                   // partial-result slots (all groups' partitions)
     uint32_t hd_t = 0;   // head_dim template of the kernel
     bool split = false;  // some group spans several partitions: merge kernel runs
     bool fusable = false;  // an append of the call's rows can run inside the launch
