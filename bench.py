@@ -19,6 +19,11 @@ back-to-back launches (Python cannot enqueue 5-us kernels fast enough to
 keep the GPU busy).  traffic = HBM bytes per launch from the committed rocprofv3
 counter summary.  cpu_baseline = the CPU oracle (restatement of the
 reference's f32 online-softmax algorithm) on layer 0 of the same step.
+
+--config selects one of the other BASELINE configurations instead (C1
+qwen2-0.5b, C3 qwen3-8b, C4 gemma2-9b, C5 qwen2.5-32b).  Those are parity-
+test shapes; their lines are secondary measurements of the same kernels and
+carry no cpu_baseline.
 """
 
 from __future__ import annotations
@@ -39,6 +44,7 @@ PEAK_HBM_GBPS = 8000.0
 CONFIGS = {
     "llama3-8b": dict(layers=32, batch=32, ctx=4096, q_heads=32, kv_heads=8, head_dim=128, page_len=16),
 }
+SECONDARY = ("qwen2-0.5b", "qwen3-8b", "gemma2-9b", "qwen2.5-32b")
 
 
 def log(*a):
@@ -119,12 +125,201 @@ def cpu_baseline(torch, pool, q0, y0, cfg, scale, seconds):
     return el / runs, runs, err
 
 
+def _time_steps(torch, step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        step()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps * 1e3  # us per step
+
+
+def run_secondary(args):
+    """The other BASELINE configurations, each as one JSON line (see the
+    module docstring).  Synthetic N(0,1) data, block tables scattered."""
+    import numpy as np
+    import torch
+
+    from flint_amd import ops
+    from flint_amd.pool import ArenaSpec, KvPool, RowMeta
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    name = args.config
+    out = {"metric": "paged attention us/step + achieved HBM GB/s (% peak) [secondary config]", "unit": "GB/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f16", "data": "synthetic N(0,1), block tables randomly scattered",
+           "cpu_baseline": None}
+
+    def make(seq_lens, pages, nkv, hd, layers, pl=16):
+        return KvPool(ArenaSpec(list(seq_lens), pages), nkv, hd, layers=layers, page_len=pl, kv_dtype="f16",
+                      part_len=args.part_len)
+
+    def randomize(pool, layers, seed):
+        g.manual_seed(seed)
+        for layer in layers:
+            for t in pool.layer_tensors(layer):
+                t.view(torch.float16).normal_(generator=g)
+
+    def spec(rows, nq, hd, m, window=0, softcap=0.0):
+        return ops.AttnSpec(q_heads=nq, window=window, scale=1.0 / math.sqrt(hd), m=m, causal=True, seq=None,
+                            args=rows, softcap=softcap)
+
+    if name == "qwen2-0.5b":  # C1: one layer, B=4, ctx U[128, 512], 256-page pool
+        rng = random.Random(1001)
+        nq, nkv, hd, L, B = 14, 2, 64, 1, 4
+        ctx = [rng.randint(128, 512) for _ in range(B)]
+        budget = [c + 1 for c in ctx]
+        pool = make(budget, 256, nkv, hd, L)
+        scattered_alloc(pool, budget, rng, 16)
+        randomize(pool, range(L), 1001)
+        rows = RowMeta(B)
+        rows.write(ctx, list(range(B)), B)
+        k = torch.randn(B, nkv, hd, device=dev, generator=g)
+        v = torch.randn(B, nkv, hd, device=dev, generator=g)
+        q = torch.randn(B, nq, hd, device=dev, generator=g)
+        y = torch.empty_like(q)
+        sp = spec(rows, nq, hd, B)
+        us = _time_steps(torch, lambda: ops.kv_store_attn(k, v, q, pool, 0, y, sp), args.steps, args.warmup)
+        byts = sum(c + 1 for c in ctx) * nkv * hd * 2 * 2
+        out["config"] = {"workload": f"qwen2-0.5b C1: 1 layer, B=4, ctx {ctx}, 14q/2kv/hd64, page 16, f16 KV, "
+                                     "step = append 1 token + decode (fused), f32 sources"}
+    elif name == "qwen3-8b":  # C3: 64 ragged decode rows + 8 x 512 prefill rows in one call per layer
+        rng = random.Random(1003)
+        nprng = np.random.default_rng(1003)
+        nq, nkv, hd, L, pre = 32, 8, 128, 4, 512
+        ctx = np.clip(np.round(nprng.lognormal(math.log(2048), 1.0, 64)), 256, 32768).astype(int).tolist()
+        budget = [c + 1 for c in ctx] + [pre] * 8
+        need = sum(-(-b // 16) for b in budget)
+        n_fill = 256
+        pages = int(need / 0.4) + 64
+        fill_cap = -(-pages // n_fill) * 4 * 16
+        pool = make([fill_cap] * n_fill + budget, pages, nkv, hd, L)
+        owners = [rng.randrange(n_fill) for _ in range(pages)]  # 60% pre-occupied, fragmented free list
+        have = [0] * n_fill
+        for s in owners:
+            pool.alloc(s, have[s] * 16, 16)
+            have[s] += 1
+        order = list(range(n_fill))
+        rng.shuffle(order)
+        freed = 0
+        for s in order:
+            if freed >= 0.4 * pages:
+                break
+            freed += have[s]
+            pool.free_seq(s)
+        for i, b in enumerate(budget):
+            pool.alloc(n_fill + i, 0, b)
+        randomize(pool, range(L), 1003)
+        positions = list(ctx) + [p for _ in range(8) for p in range(pre)]
+        seqs = [n_fill + i for i in range(64)] + [n_fill + 64 + i for i in range(8) for _ in range(pre)]
+        m = len(seqs)
+        rows = RowMeta(m)
+        rows.write(positions, seqs, m)
+        k = torch.randn(m, nkv, hd, device=dev, generator=g).half()
+        v = torch.randn(m, nkv, hd, device=dev, generator=g).half()
+        q = torch.randn(m, nq, hd, device=dev, generator=g).half()
+        y = torch.empty_like(q)
+        sp = spec(rows, nq, hd, m)
+
+        def step():
+            for layer in range(L):
+                ops.kv_store_attn(k, v, q, pool, layer, y, sp)
+        us = _time_steps(torch, step, args.steps, args.warmup) / L
+        byts = sum(c + 1 for c in ctx) * nkv * hd * 2 * 2 + 8 * pre * nkv * hd * 2 * 2
+        flops = 8 * (pre * (pre + 1) // 2) * nq * hd * 4
+        # the prefill rows alone (their K/V already appended), for the matrix-core roofline
+        rp = RowMeta(8 * pre)
+        rp.write(positions[64:], seqs[64:], 8 * pre)
+        qp, yp = q[64:].contiguous(), torch.empty_like(q[64:])
+        spp = spec(rp, nq, hd, 8 * pre)
+        pus = _time_steps(torch, lambda: [ops.attn(qp, pool, layer, yp, spp) for layer in range(L)],
+                          args.steps, args.warmup) / L
+        out["prefill"] = {"us_per_layer": round(pus, 1), "TFLOPs": round(flops / (pus * 1e-6) / 1e12, 1),
+                          "mfma_frac_of_2.5PF": round(flops / (pus * 1e-6) / 2.5e15, 4),
+                          "flops": flops, "note": "8 x 512 causal rows; unmasked (q,k) pairs x 4 x nq x hd"}
+        out["config"] = {"workload": "qwen3-8b C3: 64 decode rows (log-normal ctx in [256, 32768], median 2048) "
+                                     "+ 8 x 512-token causal prefill chunks in one call per layer, 32q/8kv/hd128, "
+                                     f"page 16, f16 KV, pool {pages} pages 60% pre-occupied, {L} layers cycled"}
+    elif name == "gemma2-9b":  # C4: verify 4 drafts per sequence, window / global layers alternating
+        rng = random.Random(1004)
+        nq, nkv, hd, L, B, ctx = 16, 8, 256, 4, 16, 8192
+        pool = make([ctx + 4] * B, None, nkv, hd, L)
+        scattered_alloc(pool, [ctx + 4] * B, rng, 16)
+        randomize(pool, range(L), 1004)
+        m = 4 * B
+        rows = RowMeta(m)
+        rows.write([ctx + i for _ in range(B) for i in range(4)], [s for s in range(B) for _ in range(4)], m)
+        k = torch.randn(m, nkv, hd, device=dev, generator=g).half()
+        v = torch.randn(m, nkv, hd, device=dev, generator=g).half()
+        q = torch.randn(m, nq, hd, device=dev, generator=g).half()
+        y = torch.empty_like(q)
+        specs = [spec(rows, nq, hd, m, window=4096 if layer % 2 == 0 else 0, softcap=50.0) for layer in range(L)]
+
+        def step():
+            for layer in range(L):
+                ops.kv_store_attn(k, v, q, pool, layer, y, specs[layer])
+        us = _time_steps(torch, step, args.steps, args.warmup) / L
+        byts = B * (4096 + ctx + 8) // 2 * nkv * hd * 2 * 2 + m * nkv * hd * 2 * 2
+        out["config"] = {"workload": "gemma2-9b C4: B=16 at ctx 8192, 16q/8kv/hd256, soft-cap 50, layers alternate "
+                                     "window 4096 / global; step = append 4 drafts + 4-row causal verify (fused), "
+                                     f"{L} layers"}
+    else:  # qwen2.5-32b, C5: 64 layers, 4 x 131072 forked to 8, 25% evicted and reallocated, decode
+        rng = random.Random(1005)
+        nq, nkv, hd, L = 40, 8, 128, 64
+        ctx, new_ctx = 131072 - 5, 20000
+        pages = 4 * (131072 // 16) + 4 + 2 * (-(-(new_ctx + 1) // 16)) + 64
+        pool = make([131072 + 8] * 8 + [new_ctx + 8] * 2, pages, nkv, hd, L)
+        scattered_alloc(pool, [ctx] * 4, rng, 16)
+        for s in range(4):
+            pool.fork(s, 4 + s, ctx)
+        evict = rng.sample(range(8), 2)
+        for s in evict:
+            pool.free_seq(s)
+        live = [s for s in range(8) if s not in evict] + [8, 9]
+        for s in (8, 9):
+            pool.alloc(s, 0, new_ctx)
+        pos = [ctx if s < 8 else new_ctx for s in live]
+        for s, p in zip(live, pos):
+            pool.alloc(s, p, 1)
+        randomize(pool, (0, L - 1), 1005)
+        m = len(live)
+        rows = RowMeta(m)
+        rows.write(pos, live, m)
+        k = torch.randn(m, nkv, hd, device=dev, generator=g).half()
+        v = torch.randn(m, nkv, hd, device=dev, generator=g).half()
+        q = torch.randn(m, nq, hd, device=dev, generator=g).half()
+        y = torch.empty_like(q)
+        sp = spec(rows, nq, hd, m)
+
+        def step():
+            for layer in range(L):
+                ops.kv_store_attn(k, v, q, pool, layer, y, sp)
+        us = _time_steps(torch, step, max(1, args.steps // 5), max(1, args.warmup // 2)) / L
+        byts = sum(p + 1 for p in pos) * nkv * hd * 2 * 2
+        out["arena_bytes"] = pool.memory()[1]
+        out["config"] = {"workload": f"qwen2.5-32b C5: 64 layers, 4 x 131072 forked to 8, evicted {evict} and "
+                                     "reallocated to 2 new sequences of 20000, decode step (fused append), "
+                                     "40q/8kv/hd128, page 16, f16 KV"}
+    gbps = byts / (us * 1e-6) / 1e9
+    out.update({"value": round(gbps, 1), "us_per_layer_step": round(us, 1),
+                "pct_of_peak": round(100 * gbps / PEAK_HBM_GBPS, 1), "ms_per_step": round(us * 1e-3, 4),
+                "bytes_per_layer_step": byts})
+    out["config"]["config_name"] = name
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="llama3-8b", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="llama3-8b", choices=sorted(CONFIGS) + list(SECONDARY))
     ap.add_argument("--part-len", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -137,6 +332,10 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for {max(args.gpus, world)}); "
               "the paged KV path has no multi-GPU code.", file=sys.stderr)
         sys.exit(2)
+
+    if args.config in SECONDARY:
+        run_secondary(args)
+        return
 
     import torch
 
