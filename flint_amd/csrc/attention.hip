@@ -1180,11 +1180,22 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
     const uint64_t n_pwg = static_cast<uint64_t>(plan.n_bitems) * pool->kv_heads;
     if (n_wg > 0x7FFFFFFFull || n_pwg > 0x7FFFFFFFull)
         throw HipError{hipErrorInvalidConfiguration, "attention grid too large"};
-    if (n_wg) {
+    if (n_wg && n_pwg) {
+        // A mixed call: the HBM-bound decode items and the matrix-core-bound
+        // prefill blocks are independent, so the prefill kernel runs on the
+        // pool's second stream, forked from and joined back into s.
+        THB_HIP(hipEventRecord(pool->fork_ev, s));
+        THB_HIP(hipStreamWaitEvent(pool->aux, pool->fork_ev, 0));
+        launch_prefill(hd_t, f16, dim3(static_cast<uint32_t>(n_pwg)), a, pool->aux);
+        THB_HIP(hipGetLastError());
         launch(hd_t, f16, dim3(static_cast<uint32_t>(n_wg)), a, s);
         THB_HIP(hipGetLastError());
-    }
-    if (n_pwg) {
+        THB_HIP(hipEventRecord(pool->join_ev, pool->aux));
+        THB_HIP(hipStreamWaitEvent(s, pool->join_ev, 0));
+    } else if (n_wg) {
+        launch(hd_t, f16, dim3(static_cast<uint32_t>(n_wg)), a, s);
+        THB_HIP(hipGetLastError());
+    } else if (n_pwg) {
         launch_prefill(hd_t, f16, dim3(static_cast<uint32_t>(n_pwg)), a, s);
         THB_HIP(hipGetLastError());
     }

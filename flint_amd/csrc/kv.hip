@@ -61,6 +61,64 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
     }
 }
 
+struct RunArgs {
+    const void* k_src;  // [m, kv_heads, head_dim] from the call's first row
+    const void* v_src;
+    uint16_t* k;
+    uint16_t* v;
+    const uint32_t* runs;   // [n_runs][4]: first row (call-relative), length, seq, first position
+    const uint32_t* table;  // [seqs * max_pages]
+    uint64_t plane;
+    uint32_t max_pages, page_shift, head_dim, kv_heads;
+};
+
+constexpr uint32_t kMaxRun = 64;  // tokens of one run (LDS: kMaxRun * head_dim * 2 bytes)
+
+// Append of runs: consecutive rows of one sequence whose positions are
+// consecutive and inside one page (a prefill chunk).  One workgroup per
+// (run, KV head).  K: the run's tokens of each chunk row are contiguous
+// 16-byte units.  V: the encoded rows are staged in LDS as [token][dim] and
+// written as the page's [dim][token] rows, 8 tokens (16 bytes) per store
+// where a whole aligned group of 8 lies inside the run, 2 bytes at its ends.
+template <uint32_t SRC, uint32_t KV>
+__global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
+    __shared__ uint4 s_v[kMaxRun * 512 / 8];
+    const uint32_t run = blockIdx.x / a.kv_heads, h = blockIdx.x - run * a.kv_heads;
+    const uint32_t* R = a.runs + 4 * run;
+    const uint32_t row0 = R[0], len = R[1], seq = R[2], pos0 = R[3];
+    const uint32_t shift = a.page_shift, hd = a.head_dim, cph = hd >> 3;
+    const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (pos0 >> shift)];
+    const uint32_t j0 = pos0 & ((1u << shift) - 1u);
+    const uint64_t pbase = static_cast<uint64_t>(h) * a.plane + ((static_cast<uint64_t>(page) * hd) << shift);
+    for (uint32_t u = threadIdx.x; u < len * cph; u += 256) {
+        const uint32_t ch = u / len, t = u - ch * len;
+        const uint64_t e = ((static_cast<uint64_t>(row0 + t)) * a.kv_heads + h) * hd + 8u * ch;
+        *reinterpret_cast<uint4*>(a.k + pbase + (static_cast<uint64_t>(8u * ch) << shift) + ((j0 + t) << 3)) =
+            load_encode8<SRC, KV>(a.k_src, e);
+        s_v[t * cph + ch] = load_encode8<SRC, KV>(a.v_src, e);
+    }
+    __syncthreads();
+    const uint16_t* sv = reinterpret_cast<const uint16_t*>(s_v);
+    const uint32_t g0 = j0 >> 3, ng = ((j0 + len - 1) >> 3) - g0 + 1;
+    for (uint32_t u = threadIdx.x; u < hd * ng; u += 256) {
+        const uint32_t d = u / ng, jg = (g0 + (u - d * ng)) << 3;
+        uint16_t* dst = a.v + pbase + (static_cast<uint64_t>(d) << shift) + jg;
+        if (jg >= j0 && jg + 8 <= j0 + len) {
+            uint32_t w[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                w[q] = static_cast<uint32_t>(sv[(jg - j0 + 2 * q) * hd + d]) |
+                       (static_cast<uint32_t>(sv[(jg - j0 + 2 * q + 1) * hd + d]) << 16);
+            *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            for (uint32_t e = 0; e < 8; e++) {
+                const uint32_t j = jg + e;
+                if (j >= j0 && j < j0 + len) dst[e] = sv[(j - j0) * hd + d];
+            }
+        }
+    }
+}
+
 struct GatherArgs {
     uint16_t* k;
     uint16_t* v;
@@ -168,6 +226,33 @@ void launch_store(uint32_t kv, dim3 grid, const StoreArgs& a, hipStream_t s) {
         hipLaunchKernelGGL((kv_store_kernel<SRC, THB_KV_BF16_TRUNC>), grid, dim3(256), 0, s, a);
 }
 
+template <uint32_t SRC>
+void launch_runs(uint32_t kv, dim3 grid, const RunArgs& a, hipStream_t s) {
+    if (kv == THB_KV_F16_RNE)
+        hipLaunchKernelGGL((kv_store_runs_kernel<SRC, THB_KV_F16_RNE>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((kv_store_runs_kernel<SRC, THB_KV_BF16_TRUNC>), grid, dim3(256), 0, s, a);
+}
+
+// Cuts rows [0, m) of the call into runs (consecutive rows of one sequence,
+// consecutive positions, one page, at most kMaxRun tokens).  Returns the
+// number of rows in runs of 8 or more tokens.
+uint32_t make_runs(const uint32_t* meta, uint32_t m, uint32_t page_shift, std::vector<uint32_t>& runs) {
+    uint32_t long_rows = 0;
+    uint32_t r = 0;
+    while (r < m) {
+        const uint32_t seq = meta[8 * r + 1], pos0 = meta[8 * r];
+        uint32_t len = 1;
+        while (r + len < m && len < kMaxRun && meta[8 * (r + len) + 1] == seq &&
+               meta[8 * (r + len)] == pos0 + len && ((pos0 + len) >> page_shift) == (pos0 >> page_shift))
+            len++;
+        runs.insert(runs.end(), {r, len, seq, pos0});
+        if (len >= 8) long_rows += len;
+        r += len;
+    }
+    return long_rows;
+}
+
 int check_layer(const thb_pool* p, uint32_t layer) {
     if (layer >= p->layers)
         return fail(THB_ERR_INVALID, "layer " + std::to_string(layer) + " out of range (" +
@@ -249,6 +334,38 @@ int thb_kv_store(thb_pool* pool, uint32_t layer, const void* k_src, const void* 
         a.head_dim = g.head_dim;
         a.chunks = pool->kv_heads * g.head_dim / 8;
         const size_t esize = src_dtype == THB_DT_F32 ? 4 : 2;
+        // Mostly long runs (prefill chunks): the run kernel writes whole V
+        // page rows; otherwise (decode) one lane per 8 elements of a row.
+        std::vector<uint32_t> runs;
+        const uint32_t long_rows = make_runs(rows->host.data() + 8 * static_cast<size_t>(row_off), m,
+                                             pool->page_shift, runs);
+        if (2 * static_cast<uint64_t>(long_rows) >= m) {
+            const uint32_t n_runs = static_cast<uint32_t>(runs.size() / 4);
+            void* dev = pool->run_buf.reserve(runs.size() * 4, false);
+            pool->stager.upload(dev, runs.data(), runs.size() * 4, s);
+            RunArgs ra;
+            ra.k_src = k_src;
+            ra.v_src = v_src;
+            ra.k = a.k;
+            ra.v = a.v;
+            ra.runs = static_cast<const uint32_t*>(dev);
+            ra.table = a.table;
+            ra.plane = a.plane;
+            ra.max_pages = a.max_pages;
+            ra.page_shift = a.page_shift;
+            ra.head_dim = a.head_dim;
+            ra.kv_heads = pool->kv_heads;
+            const uint64_t n_wg = static_cast<uint64_t>(n_runs) * pool->kv_heads;
+            if (n_wg > 0x7FFFFFFFull) throw HipError{hipErrorInvalidConfiguration, "append grid too large"};
+            const dim3 grid(static_cast<uint32_t>(n_wg));
+            switch (src_dtype) {
+                case THB_DT_F32: launch_runs<THB_DT_F32>(pool->kv_dtype, grid, ra, s); break;
+                case THB_DT_F16: launch_runs<THB_DT_F16>(pool->kv_dtype, grid, ra, s); break;
+                default: launch_runs<THB_DT_BF16>(pool->kv_dtype, grid, ra, s); break;
+            }
+            THB_HIP(hipGetLastError());
+            return THB_OK;
+        }
         for (uint32_t r0 = 0; r0 < m; r0 += kMaxGridY) {  // grid.y limit
             const uint32_t n = std::min(kMaxGridY, m - r0);
             StoreArgs b = a;

@@ -70,9 +70,14 @@ struct thb_pool {
     thb::DevBuf copy_buf;            // copy triples
     thb::DevBuf geom_buf;            // per-layer DevLayer records
     thb::DevBuf partials;            // split-K partial results
+    thb::DevBuf run_buf;             // append runs of the last run-kernel call
     std::array<thb::AttnPlan, 4> plans;
     uint64_t plan_clock = 0;
     int device = 0;
+    // Second stream for the prefill kernel of a mixed call, forked from and
+    // joined back into the caller's stream with these events.
+    hipStream_t aux = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
 };
 
 namespace thb {

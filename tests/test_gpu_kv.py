@@ -231,3 +231,42 @@ def test_page_layout_matches_header(torch_cuda, page_len, hd):
         rk, rv = ref.gather(s, 0, n)
         assert np.array_equal(kd.cpu().numpy().view(np.uint16), rk)
         assert np.array_equal(vd.cpu().numpy().view(np.uint16), rv)
+
+
+@pytest.mark.parametrize("page_len,hd,src", [(16, 128, "f16"), (8, 64, "f32"), (32, 256, "bf16"),
+                                             (64, 512, "f32"), (16, 80, "f16")])
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_kv_store_prefill_runs_bit_exact(torch_cuda, page_len, hd, src, kv):
+    """Prefill-like appends (consecutive positions of one sequence, starting
+    mid-page, several sequences interleaved in one call, plus a few decode
+    rows) take the run kernel; the pool must equal the oracle's appends."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    say("kv_store runs", page_len, hd, src, kv)
+    lens = [300, 137, 90]
+    pool = make_pool(lens, kv_heads=3, head_dim=hd, page_len=page_len, kv_dtype=kv, extra_pages=2)
+    scattered_alloc(pool, lens, random.Random(page_len + hd), page_len)
+    ref = oracle_layer(torch, pool)
+    rows = RowMeta(512)
+    dt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[src]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(hd)
+    # call 1: seq 0 tokens [5, 205) + seq 1 tokens [3, 100) + decode rows of seq 2
+    # call 2: the rest of every sequence
+    calls = [[(0, p) for p in range(5, 205)] + [(1, p) for p in range(3, 100)] + [(2, 7), (2, 8)],
+             [(0, p) for p in list(range(0, 5)) + list(range(205, 300))] + [(1, p) for p in list(range(0, 3)) +
+                                                                             list(range(100, 137))] +
+             [(2, p) for p in range(90) if p not in (7, 8)]]
+    for chunk in calls:
+        m = len(chunk)
+        pos, seqs = [p for _, p in chunk], [s for s, _ in chunk]
+        rows.write(pos, seqs, m)
+        k = (torch.randn(m, 3, hd, device="cuda", generator=g) * 3).to(dt)
+        v = (torch.randn(m, 3, hd, device="cuda", generator=g) * 100).to(dt)
+        ops.kv_store(k, v, pool, 0, m, rows)
+        ref.kv_store(_src_words(torch, k), _src_words(torch, v), oracle.row_meta(pos, seqs), m, SRC[src])
+    got = oracle_layer(torch, pool)
+    assert np.array_equal(got.k, ref.k)
+    assert np.array_equal(got.v, ref.v)
