@@ -19,6 +19,8 @@ back-to-back launches (Python cannot enqueue 5-us kernels fast enough to
 keep the GPU busy).  traffic = HBM bytes per launch from the committed rocprofv3
 counter summary.  cpu_baseline = the CPU oracle (restatement of the
 reference's f32 online-softmax algorithm) on layer 0 of the same step.
+gather / scatter / block_copy = the page-move kernels at the same shape
+(secondary fields of the same line).
 
 --config selects one of the other BASELINE configurations instead (C1
 qwen2-0.5b, C3 qwen3-8b, C4 gemma2-9b, C5 qwen2.5-32b).  Those are parity-
@@ -97,6 +99,88 @@ def time_append_graph(torch, ops, pool, rows, k, v, layer, m, launches=50, repla
     except Exception as exc:  # capture refused: report no figure rather than a host-bound one
         log(f"append graph timing unavailable: {exc}")
         return None
+
+
+def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
+    """Gather of every sequence of one layer into contiguous buffers, the
+    scatter of those buffers back (the pool is left bit-identical), and a
+    block copy of 512 whole pages (every layer) in a second pool of the same
+    geometry whose sequences leave 512 pages free (the decode pool holds
+    exactly its sequences' pages).  HIP events around `reps` replays of a
+    captured graph of the B gather (scatter) calls, and around `reps`
+    block-copy calls; algorithmic bytes = 2 x bytes moved."""
+    from flint_amd.pool import ArenaSpec, KvPool
+
+    kb = torch.empty(B, nkv, ctx, hd, dtype=torch.int16, device=dev)
+    vb = torch.empty_like(kb)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    def sweep(fn):
+        for s in range(B):
+            fn(pool, layer, s, 0, ctx, kb[s], vb[s])
+
+    def graph_of(fn):
+        # one graph of the B calls: Python issues a call in ~10 us, longer than the kernel
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            sweep(fn)  # warm
+            side.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                sweep(fn)
+        torch.cuda.current_stream().wait_stream(side)
+        return graph
+
+    gg, gs = graph_of(ops.kv_gather), graph_of(ops.kv_scatter)
+    gg.replay()
+    gs.replay()
+    torch.cuda.synchronize()
+    ev[0].record()
+    for _ in range(reps):
+        gg.replay()
+    ev[1].record()
+    for _ in range(reps):
+        gs.replay()
+    ev[2].record()
+    torch.cuda.synchronize()
+    del gg, gs
+    moved = B * nkv * ctx * hd * 2 * 2
+    g_us = ev[0].elapsed_time(ev[1]) / reps * 1e3
+    s_us = ev[1].elapsed_time(ev[2]) / reps * 1e3
+    del kb, vb
+    spare, held = 512, 3584  # pages: copy destinations / held by the second pool's sequences
+    cpool = KvPool(ArenaSpec([ctx] * (-(-held * pl // ctx)), held + spare), nkv, hd, layers=pool.layers,
+                   page_len=pl, kv_dtype="f16")
+    scattered_alloc(cpool, [ctx] * (held * pl // ctx), random.Random(7), pl)
+    used = [p for s in range(held * pl // ctx) for p in cpool.arena.table_of(s)]
+    free = sorted(set(range(cpool.arena.pages())) - set(used))[:spare]
+    triples = [[used[i * 7 % len(used)], free[i], pl] for i in range(len(free))]
+    ops.block_copy(cpool, triples)
+    torch.cuda.synchronize()
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # a spin kernel ahead of the first event keeps the GPU busy while Python
+    # prepares the calls (the triple list costs more host time than the copy)
+    torch.cuda._sleep(20_000_000)
+    c0.record()
+    for _ in range(reps):
+        ops.block_copy(cpool, triples)
+    c1.record()
+    torch.cuda.synchronize()
+    c_us = c0.elapsed_time(c1) / reps * 1e3
+    c_moved = len(triples) * pool.layers * 2 * nkv * pl * hd * 2
+    cpool.close()
+
+    def rec(us, nbytes, note):
+        gbps = 2 * nbytes / (us * 1e-6) / 1e9
+        return {"us_per_call": round(us, 1), "GBps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                "bytes_moved": nbytes, "note": note}
+
+    return {"gather": rec(g_us, moved, f"kv_gather of all {B} sequences x {ctx} tokens of one layer "
+                                       f"({B} calls, one graph) into [kv_heads, ctx, head_dim]"),
+            "scatter": rec(s_us, moved, f"kv_scatter of the same {B} buffers back ({B} calls, one graph)"),
+            "block_copy": rec(c_us, c_moved, f"one block_copy call of {len(triples)} whole pages x "
+                                             f"{pool.layers} layers x K,V x {nkv} heads")}
 
 
 def cpu_baseline(torch, pool, q0, y0, cfg, scale, seconds):
@@ -444,6 +528,9 @@ def main():
                      "algorithmic_bytes": fused_bytes, "launches_timed": len(timed) * per_run},
         "cpu_baseline": None,
     }
+    moves = time_gather_copy(torch, ops, pool, 1 % L, B, ctx, nkv, hd, pl, dev)
+    log("gather/scatter/copy: " + ", ".join(f"{k} {v['us_per_call']} us {v['GBps']} GB/s" for k, v in moves.items()))
+    out.update(moves)
     if args.calibrate_copy_mib:
         src = torch.empty(args.calibrate_copy_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

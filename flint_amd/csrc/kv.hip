@@ -7,6 +7,7 @@
 // product), so the lane's 8 V elements are 8 16-bit accesses page_len
 // elements apart.  In both, element (slot s, dim d) of page p starts from
 // the offset (p * head_dim + d) * page_len.
+#include <algorithm>
 #include <string>
 
 #include "codec.hpp"
@@ -39,7 +40,6 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
     if (is_v) c -= a.chunks;
     const uint32_t pos = a.meta[8 * row], seq = a.meta[8 * row + 1];
     const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (pos >> a.page_shift)];
-    const uint64_t slot = (static_cast<uint64_t>(page) << a.page_shift) | (pos & ((1u << a.page_shift) - 1u));
     const uint32_t cph = a.head_dim >> 3;
     const uint32_t h = c / cph, d = (c - h * cph) << 3;
     const uint64_t src_e = (static_cast<uint64_t>(row) * a.chunks + c) << 3;
@@ -126,96 +126,247 @@ struct GatherArgs {
     uint16_t* v_flat;
     const uint32_t* table_row;  // the sequence's block-table row
     uint64_t plane;
-    uint32_t page_shift, head_dim, n, t0, cpt;  // cpt = chunks per token = kv_heads * head_dim / 8
+    uint32_t page_shift, head_dim, n, t0;
+    uint32_t tile;   // tokens per LDS tile of V (min(page_len, 64))
+    uint32_t heads;  // KV heads per workgroup
+};
+
+// Byte offset in the V tile of dimension d, tile slot jj: rows of `tile`
+// 16-bit slots, and 16 bytes of padding after every 8 rows so that the lanes
+// of one token (consecutive 8-dimension chunks, 8 rows apart) hit distinct
+// LDS banks.
+__device__ inline uint32_t vtile_off(uint32_t d, uint32_t jj, uint32_t tile) {
+    return (d >> 3) * (16u * tile + 16u) + (d & 7u) * 2u * tile + 2u * jj;
+}
+
+// Copies 16 bytes from `src` to `dst` keeping the 16-bit slots of `dst`
+// outside [e0, e1) (a V page group of 8 tokens that the range cuts).
+__device__ inline void merge8(uint16_t* dst, const uint16_t* src, uint32_t e0, uint32_t e1) {
+    if (e0 == 0 && e1 == 8) {
+        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+        return;
+    }
+    uint4 o = *reinterpret_cast<const uint4*>(dst);
+    const uint4 n = *reinterpret_cast<const uint4*>(src);
+    uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
+    const uint32_t* nw = reinterpret_cast<const uint32_t*>(&n);
+#pragma unroll
+    for (uint32_t e = 0; e < 8; e++) {
+        if (e < e0 || e >= e1) continue;
+        const uint32_t sh = 16u * (e & 1u), mask = 0xffffu << sh;
+        ow[e >> 1] = (ow[e >> 1] & ~mask) | (nw[e >> 1] & mask);
+    }
+    *reinterpret_cast<uint4*>(dst) = o;
+}
+
+// 16-byte store with the non-temporal hint (the destination is not read
+// again by this kernel or soon after).
+__device__ inline void st_stream16(void* p, const uint4& v) {
+    __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, static_cast<u32x4*>(p));
+}
+
+// u / d without a division instruction: exact for u, d < 2^16 (the error
+// term u * (m * d - 2^32) stays below 2^32).
+struct DivSmall {
+    uint64_t m;
+    __device__ explicit DivSmall(uint32_t d) : m(0xFFFFFFFFull / d + 1u) {}
+    __device__ uint32_t operator()(uint32_t u) const { return static_cast<uint32_t>((u * m) >> 32); }
 };
 
 // Gather (TO_FLAT) or scatter (!TO_FLAT) of tokens [t0, t0 + n) of one
-// sequence.  Grid: (ceil(n * cpt / 256), 2); y selects K or V.
+// sequence.  One workgroup per (page of the range, group of `heads` KV
+// heads).  K: a token's 8-dimension chunk is 16 contiguous bytes on both
+// sides.  V: the page's [head_dim][page_len] rows go through an LDS tile of
+// up to 64 tokens per head and are read and written as 16-byte vectors on
+// both sides; a page group of 8 tokens that the range cuts is merged into
+// its 16 bytes by one lane.  A tile's K and V loads are issued together, two
+// of each per lane at a time.
 template <bool TO_FLAT>
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
-    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (c >= static_cast<uint64_t>(a.n) * a.cpt) return;
-    const uint32_t t = static_cast<uint32_t>(c / a.cpt);
-    const uint32_t r = static_cast<uint32_t>(c - static_cast<uint64_t>(t) * a.cpt);
-    const uint32_t cph = a.head_dim >> 3;
-    const uint32_t h = r / cph, d = (r - h * cph) << 3;
-    const uint32_t pos = a.t0 + t;
-    const uint32_t page = a.table_row[pos >> a.page_shift];
-    const uint32_t j = pos & ((1u << a.page_shift) - 1u);
-    if (blockIdx.y == 0) {
-        uint16_t* paged = a.k + h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + d) << a.page_shift) + (j << 3);
-        uint16_t* flat = a.k_flat + (static_cast<uint64_t>(h) * a.n + t) * a.head_dim + d;
-        if constexpr (TO_FLAT)
-            *reinterpret_cast<uint4*>(flat) = *reinterpret_cast<const uint4*>(paged);
-        else
-            *reinterpret_cast<uint4*>(paged) = *reinterpret_cast<const uint4*>(flat);
-        return;
-    }
-    uint16_t* paged = a.v + h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + d) << a.page_shift) + j;
-    uint16_t* flat = a.v_flat + (static_cast<uint64_t>(h) * a.n + t) * a.head_dim + d;
-    if constexpr (TO_FLAT) {
-        uint32_t w[4];
+    extern __shared__ uint4 s_tile[];
+    uint8_t* tile_b = reinterpret_cast<uint8_t*>(s_tile);
+    const uint32_t shift = a.page_shift, hd = a.head_dim, cph = hd >> 3, T = a.tile;
+    const uint32_t tile_bytes = cph * (16u * T + 16u);
+    const uint32_t pi = (a.t0 >> shift) + blockIdx.x, h0 = blockIdx.y * a.heads;
+    const uint32_t p0 = pi << shift;
+    const uint32_t ja = max(a.t0, p0) - p0;
+    const uint32_t jb = static_cast<uint32_t>(
+        min(static_cast<uint64_t>(a.t0) + a.n, static_cast<uint64_t>(p0) + (1u << shift)) - p0);
+    const uint64_t pbase0 = (static_cast<uint64_t>(a.table_row[pi]) * hd) << shift;
+    auto pbase = [&](uint32_t hh) { return static_cast<uint64_t>(h0 + hh) * a.plane + pbase0; };
+    // flat row of page slot j of head h: h * n + p0 + j - t0 (j >= ja keeps it >= h * n)
+    auto flat_off = [&](uint32_t hh, uint32_t j, uint32_t c) {
+        return (static_cast<uint64_t>(h0 + hh) * a.n + p0 - a.t0 + j) * hd + 8u * c;
+    };
+    auto k_paged = [&](uint32_t hh, uint32_t j, uint32_t c) {
+        return a.k + pbase(hh) + (static_cast<uint64_t>(8u * c) << shift) + (j << 3);
+    };
+    auto v_paged = [&](uint32_t hh, uint32_t d, uint32_t j) {
+        return a.v + pbase(hh) + (static_cast<uint64_t>(d) << shift) + j;
+    };
+    const DivSmall by_cph(cph);
+    for (uint32_t tb = ja & ~(T - 1u); tb < jb; tb += T) {
+        const uint32_t lo = max(ja, tb), hi = min(jb, tb + T);
+        const uint32_t g_lo = (lo - tb) >> 3, g_hi = (hi - tb + 7u) >> 3;  // groups the range touches
+        const uint32_t ng = g_hi - g_lo;
+        const uint32_t n_tok = (hi - lo) * cph;  // K (and flat V) vectors of the tile, per head
+        const uint32_t n_grp = hd * ng;          // V page vectors of the tile, per head
+        const DivSmall by_ng(ng), by_tok(n_tok), by_grp(n_grp);
+        // vector u of the K (flat) side: head hh, token lo + t, chunk c
+        auto split_tok = [&](uint32_t u, uint32_t& hh, uint32_t& t, uint32_t& c) {
+            hh = by_tok(u);
+            const uint32_t r = u - hh * n_tok;
+            t = by_cph(r);
+            c = r - t * cph;
+        };
+        // vector u of the V page side: head hh, dimension d, group g
+        auto split_grp = [&](uint32_t u, uint32_t& hh, uint32_t& d, uint32_t& g) {
+            hh = by_grp(u);
+            const uint32_t r = u - hh * n_grp;
+            d = by_ng(r);
+            g = g_lo + r - d * ng;
+        };
+        const uint32_t NT = a.heads * n_tok, NG = a.heads * n_grp;
+        if constexpr (TO_FLAT) {
+            for (uint32_t u0 = threadIdx.x; u0 < max(NT, NG); u0 += 512) {
+                uint4 kr[2], vr[2];
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            w[e] = static_cast<uint32_t>(paged[static_cast<uint64_t>(2 * e) << a.page_shift]) |
-                   (static_cast<uint32_t>(paged[static_cast<uint64_t>(2 * e + 1) << a.page_shift]) << 16);
-        *reinterpret_cast<uint4*>(flat) = make_uint4(w[0], w[1], w[2], w[3]);
-    } else {
-        const uint4 v = *reinterpret_cast<const uint4*>(flat);
+                for (uint32_t i = 0; i < 2; i++) {
+                    const uint32_t u = u0 + 256 * i;
+                    uint32_t hh, t, c, d, g;
+                    split_tok(u, hh, t, c);
+                    if (u < NT) kr[i] = ld_stream16(k_paged(hh, lo + t, c));
+                    split_grp(u, hh, d, g);
+                    if (u < NG) vr[i] = ld_stream16(v_paged(hh, d, tb + 8u * g));
+                }
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const uint32_t x = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
-            paged[static_cast<uint64_t>(2 * e) << a.page_shift] = static_cast<uint16_t>(x & 0xffffu);
-            paged[static_cast<uint64_t>(2 * e + 1) << a.page_shift] = static_cast<uint16_t>(x >> 16);
+                for (uint32_t i = 0; i < 2; i++) {
+                    const uint32_t u = u0 + 256 * i;
+                    uint32_t hh, t, c, d, g;
+                    split_tok(u, hh, t, c);
+                    if (u < NT) st_stream16(a.k_flat + flat_off(hh, lo + t, c), kr[i]);
+                    split_grp(u, hh, d, g);
+                    if (u < NG) *reinterpret_cast<uint4*>(tile_b + hh * tile_bytes + vtile_off(d, 8u * g, T)) = vr[i];
+                }
+            }
+            __syncthreads();
+            for (uint32_t u = threadIdx.x; u < NT; u += 256) {
+                uint32_t hh, t, c;
+                split_tok(u, hh, t, c);
+                const uint32_t jj = lo - tb + t;
+                const uint8_t* tl = tile_b + hh * tile_bytes;
+                uint32_t w[4];
+#pragma unroll
+                for (uint32_t q = 0; q < 4; q++)
+                    w[q] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tl + vtile_off(8u * c + 2u * q, jj, T))) |
+                           (static_cast<uint32_t>(
+                                *reinterpret_cast<const uint16_t*>(tl + vtile_off(8u * c + 2u * q + 1u, jj, T)))
+                            << 16);
+                st_stream16(a.v_flat + flat_off(hh, tb + jj, c), make_uint4(w[0], w[1], w[2], w[3]));
+            }
+        } else {
+            for (uint32_t u0 = threadIdx.x; u0 < NT; u0 += 512) {
+                uint4 kr[2], vr[2];
+#pragma unroll
+                for (uint32_t i = 0; i < 2; i++) {
+                    const uint32_t u = u0 + 256 * i;
+                    uint32_t hh, t, c;
+                    split_tok(u, hh, t, c);
+                    if (u < NT) {
+                        kr[i] = ld_stream16(a.k_flat + flat_off(hh, lo + t, c));
+                        vr[i] = ld_stream16(a.v_flat + flat_off(hh, lo + t, c));
+                    }
+                }
+#pragma unroll
+                for (uint32_t i = 0; i < 2; i++) {
+                    const uint32_t u = u0 + 256 * i;
+                    if (u >= NT) continue;
+                    uint32_t hh, t, c;
+                    split_tok(u, hh, t, c);
+                    st_stream16(k_paged(hh, lo + t, c), kr[i]);
+                    uint8_t* tl = tile_b + hh * tile_bytes;
+                    const uint32_t jj = lo - tb + t;
+                    const uint32_t xw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+                    for (uint32_t e = 0; e < 8; e++)
+                        *reinterpret_cast<uint16_t*>(tl + vtile_off(8u * c + e, jj, T)) =
+                            static_cast<uint16_t>(xw[e >> 1] >> (16u * (e & 1u)));
+                }
+            }
+            __syncthreads();
+            for (uint32_t u = threadIdx.x; u < NG; u += 256) {
+                uint32_t hh, d, g;
+                split_grp(u, hh, d, g);
+                const uint32_t j8 = tb + 8u * g;
+                merge8(v_paged(hh, d, j8),
+                       reinterpret_cast<const uint16_t*>(tile_b + hh * tile_bytes + vtile_off(d, 8u * g, T)),
+                       max(lo, j8) - j8, min(hi, j8 + 8u) - j8);
+            }
         }
+        __syncthreads();
     }
 }
+
+constexpr uint32_t kInlineCopies = 32;  // page copies passed in the kernel arguments
 
 struct CopyArgs {
     uint8_t* mem;
     const DevLayer* layers;
-    const uint32_t* triples;  // (src_page, dst_page, tokens)
+    const uint32_t* triples;  // device (src_page, dst_page, tokens) list, or null: the inline list
     uint64_t pool_len;
-    uint32_t kv_heads, page_len;
+    uint32_t kv_heads, page_shift;
+    uint32_t inl[3 * kInlineCopies];
 };
 
-// Copy of slots [0, ntok) of a page for every layer, K and V, every head.
-// Grid: (ceil(page_len * max_head_dim / 256), n_triples, layers * 2 *
-// kv_heads).  A whole page moves as contiguous 16-byte vectors; a partial K
-// page as 16-byte chunks of its chunk rows; a partial V page element by
-// element ([head_dim][page_len]).
+// Copy of slots [0, ntok) of one (page, head, K or V) plane of one layer.
+// Grid: (n_triples, layers * 2 * kv_heads), plane fastest.  Every access is
+// a 16-byte vector: a whole page is one contiguous run (4 vectors in flight
+// per lane); of a partial page, a K chunk row moves its first ntok chunks
+// and a V dimension row its first ntok 16-bit slots, the group of 8 that
+// ntok cuts merged by one lane.
 __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
-    const uint32_t z = blockIdx.z;
-    const uint32_t h = z % a.kv_heads;
-    const uint32_t which = (z / a.kv_heads) & 1u;
-    const uint32_t layer = z / (2 * a.kv_heads);
+    const uint32_t planes = 2 * a.kv_heads;
+    const uint32_t layer = blockIdx.y / planes, plane = blockIdx.y - layer * planes;
+    const uint32_t which = plane >= a.kv_heads, h = plane - which * a.kv_heads;
     const DevLayer L = a.layers[layer];
-    const uint32_t src = a.triples[3 * blockIdx.y], dst = a.triples[3 * blockIdx.y + 1];
-    const uint32_t ntok = a.triples[3 * blockIdx.y + 2];
-    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
-    uint16_t* base = reinterpret_cast<uint16_t*>(a.mem + (which ? L.v_off : L.k_off)) +
-                     static_cast<uint64_t>(h) * a.pool_len * L.head_dim;
-    const uint64_t page_elems = static_cast<uint64_t>(a.page_len) * L.head_dim;
-    const uint16_t* sp = base + static_cast<uint64_t>(src) * page_elems;
-    uint16_t* dp = base + static_cast<uint64_t>(dst) * page_elems;
-    if (ntok == a.page_len) {  // whole page, K or V: contiguous
-        if (static_cast<uint64_t>(c) * 8 >= page_elems) return;
-        const uint64_t off = static_cast<uint64_t>(c) * 8;
-        *reinterpret_cast<uint4*>(dp + off) = *reinterpret_cast<const uint4*>(sp + off);
+    uint32_t src, dst, ntok;
+    if (a.triples) {
+        src = a.triples[3 * blockIdx.x];
+        dst = a.triples[3 * blockIdx.x + 1];
+        ntok = a.triples[3 * blockIdx.x + 2];
+    } else {
+        src = a.inl[3 * blockIdx.x];
+        dst = a.inl[3 * blockIdx.x + 1];
+        ntok = a.inl[3 * blockIdx.x + 2];
+    }
+    const uint32_t shift = a.page_shift, P = 1u << shift, gpr = P >> 3;  // V groups per dim row
+    const uint32_t vecs = (L.head_dim << shift) >> 3;                      // 16-byte vectors per page plane
+    const uint64_t page_elems = static_cast<uint64_t>(L.head_dim) << shift;
+    const uint16_t* base = reinterpret_cast<const uint16_t*>(a.mem + (which ? L.v_off : L.k_off)) +
+                           static_cast<uint64_t>(h) * a.pool_len * L.head_dim;
+    const uint16_t* sp = base + src * page_elems;
+    uint16_t* dp = const_cast<uint16_t*>(base) + dst * page_elems;
+    if (ntok == P) {
+        for (uint32_t b = threadIdx.x; b < vecs; b += 4 * 256) {
+            uint4 r[4];
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++)
+                if (b + 256 * i < vecs) r[i] = ld_stream16(sp + 8u * (b + 256 * i));
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++)
+                if (b + 256 * i < vecs) st_stream16(dp + 8u * (b + 256 * i), r[i]);
+        }
         return;
     }
-    if (which == 0) {  // K: the first ntok 16-byte chunks of every chunk row
-        const uint32_t rows = L.head_dim >> 3;
-        if (c >= rows * ntok) return;
-        const uint32_t r = c / ntok, j = c - r * ntok;
-        const uint64_t off = (static_cast<uint64_t>(r) * a.page_len + j) * 8;
-        *reinterpret_cast<uint4*>(dp + off) = *reinterpret_cast<const uint4*>(sp + off);
-        return;
+    for (uint32_t u = threadIdx.x; u < vecs; u += 256) {
+        if (which == 0) {  // K: vector u = chunk row u / P, token u % P
+            if ((u & (P - 1u)) < ntok)
+                *reinterpret_cast<uint4*>(dp + 8u * u) = *reinterpret_cast<const uint4*>(sp + 8u * u);
+        } else {  // V: vector u = dim u / gpr, tokens 8 * (u % gpr) + [0, 8)
+            const uint32_t j8 = 8u * (u & (gpr - 1u));
+            if (j8 < ntok) merge8(dp + 8u * u, sp + 8u * u, 0, min(ntok - j8, 8u));
+        }
     }
-    if (c >= ntok * L.head_dim) return;
-    const uint32_t d = c / ntok, j = c - d * ntok;
-    const uint64_t off = static_cast<uint64_t>(d) * a.page_len + j;
-    dp[off] = sp[off];
 }
 
 template <uint32_t SRC>
@@ -277,21 +428,30 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
-void launch_block_copy(thb_pool* p, const uint32_t* triples_dev, uint32_t n, uint32_t max_tokens,
-                       hipStream_t stream) {
+void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_t max_tokens, hipStream_t stream) {
     if (n == 0 || max_tokens == 0) return;
-    uint32_t max_hd = 0;
-    for (const auto& g : p->geom) max_hd = std::max(max_hd, g.head_dim);
-    CopyArgs a{p->mem, static_cast<const DevLayer*>(p->geom_buf.get()), triples_dev,
-               static_cast<uint64_t>(p->arena.a.pages()) * p->page_len, p->kv_heads, p->page_len};
-    const uint32_t chunks = (max_tokens * max_hd + 255) / 256;
-    const uint32_t planes = p->layers * 2 * p->kv_heads;
+    CopyArgs a{};
+    a.mem = p->mem;
+    a.layers = static_cast<const DevLayer*>(p->geom_buf.get());
+    a.pool_len = static_cast<uint64_t>(p->arena.a.pages()) * p->page_len;
+    a.kv_heads = p->kv_heads;
+    a.page_shift = p->page_shift;
+    const uint64_t planes = static_cast<uint64_t>(p->layers) * 2 * p->kv_heads;
     if (planes > kMaxGridY) throw HipError{hipErrorInvalidConfiguration, "block copy: layers*2*kv_heads > 65535"};
-    for (uint32_t i0 = 0; i0 < n; i0 += kMaxGridY) {
+    if (n <= kInlineCopies) {  // a fork's or rollback's few copies: no upload
+        std::copy(triples, triples + 3 * static_cast<size_t>(n), a.inl);
+        a.triples = nullptr;
+    } else {
+        void* dev = p->copy_buf.reserve(static_cast<size_t>(n) * 12, false);
+        p->stager.upload(dev, triples, static_cast<size_t>(n) * 12, stream);
+        a.triples = static_cast<const uint32_t*>(dev);
+    }
+    constexpr uint32_t kMaxGridX = 1u << 30;
+    for (uint32_t i0 = 0; i0 < n; i0 += kMaxGridX) {
         CopyArgs b = a;
-        b.triples = triples_dev + 3 * static_cast<size_t>(i0);
-        hipLaunchKernelGGL(block_copy_kernel, dim3(chunks, std::min(kMaxGridY, n - i0), planes), dim3(256), 0, stream,
-                           b);
+        if (a.triples) b.triples = a.triples + 3 * static_cast<size_t>(i0);
+        hipLaunchKernelGGL(block_copy_kernel, dim3(std::min(kMaxGridX, n - i0), static_cast<uint32_t>(planes)),
+                           dim3(256), 0, stream, b);
         THB_HIP(hipGetLastError());
     }
 }
@@ -407,13 +567,30 @@ static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t 
         a.head_dim = g.head_dim;
         a.n = n;
         a.t0 = t0;
-        a.cpt = pool->kv_heads * g.head_dim / 8;
-        const uint64_t total = static_cast<uint64_t>(n) * a.cpt;
-        dim3 grid(static_cast<uint32_t>((total + 255) / 256), 2);
+        // V tile: up to 64 tokens of every dimension, at most 32 KiB of LDS
+        // per head.  Heads per workgroup: enough for 4 KiB of K per page
+        // (small pages), at most 4, within 64 KiB of LDS.  More heads per
+        // workgroup serialise load rounds and measured slower at 4 KiB pages.
+        uint32_t tile = std::min(pool->page_len, 64u);
+        while (tile > 8 && (g.head_dim / 8) * (16 * tile + 16) > 32768) tile >>= 1;
+        a.tile = tile;
+        const size_t tile_bytes = static_cast<size_t>(g.head_dim / 8) * (16 * tile + 16);
+        const uint32_t want = std::min<uint32_t>(4, std::max<uint32_t>(1, 2048 / (pool->page_len * g.head_dim)));
+        uint32_t heads = 1;
+        for (uint32_t hpw = want; hpw > 1; hpw--)
+            if (pool->kv_heads % hpw == 0 && hpw * tile_bytes <= 65536) {
+                heads = hpw;
+                break;
+            }
+        a.heads = heads;
+        const size_t lds = heads * tile_bytes;
+        const uint32_t pages = static_cast<uint32_t>(((static_cast<uint64_t>(t0) + n - 1) >> pool->page_shift) -
+                                                     (t0 >> pool->page_shift) + 1);
+        dim3 grid(pages, pool->kv_heads / heads);
         if (to_flat)
-            hipLaunchKernelGGL(gather_kernel<true>, grid, dim3(256), 0, s, a);
+            hipLaunchKernelGGL(gather_kernel<true>, grid, dim3(256), lds, s, a);
         else
-            hipLaunchKernelGGL(gather_kernel<false>, grid, dim3(256), 0, s, a);
+            hipLaunchKernelGGL(gather_kernel<false>, grid, dim3(256), lds, s, a);
         THB_HIP(hipGetLastError());
         return THB_OK;
     });
@@ -456,9 +633,7 @@ int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* st
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
-        void* dev = pool->copy_buf.reserve(static_cast<size_t>(n) * 12, false);
-        pool->stager.upload(dev, triples, static_cast<size_t>(n) * 12, s);
-        launch_block_copy(pool, static_cast<const uint32_t*>(dev), n, max_tok, s);
+        launch_block_copy(pool, triples, n, max_tok, s);
         return THB_OK;
     });
 }

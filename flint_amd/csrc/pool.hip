@@ -107,9 +107,7 @@ static void run_copies(thb_pool* p, hipStream_t stream) {
             max_tok = std::max(max_tok, c.tokens);
         }
         uint32_t n = static_cast<uint32_t>(batch.size() / 3);
-        void* dev = p->copy_buf.reserve(batch.size() * 4, false);
-        p->stager.upload(dev, batch.data(), batch.size() * 4, stream);
-        launch_block_copy(p, static_cast<const uint32_t*>(dev), n, max_tok, stream);
+        launch_block_copy(p, batch.data(), n, max_tok, stream);
     }
     copies.clear();
 }

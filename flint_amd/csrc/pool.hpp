@@ -83,7 +83,7 @@ struct thb_pool {
 namespace thb {
 // Uploads dirty block-table rows and executes pending page copies.
 void pool_flush(thb_pool* p, hipStream_t stream);
-// Launches the block-copy kernel for non-chaining triples already on device.
-void launch_block_copy(thb_pool* p, const uint32_t* triples_dev, uint32_t n, uint32_t max_tokens,
-                       hipStream_t stream);
+// Launches the block-copy kernel for n non-chaining host triples (passed in
+// the kernel arguments when few, else uploaded through the stager).
+void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_t max_tokens, hipStream_t stream);
 }  // namespace thb

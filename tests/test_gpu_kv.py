@@ -270,3 +270,82 @@ def test_kv_store_prefill_runs_bit_exact(torch_cuda, page_len, hd, src, kv):
     got = oracle_layer(torch, pool)
     assert np.array_equal(got.k, ref.k)
     assert np.array_equal(got.v, ref.v)
+
+
+@pytest.mark.parametrize("page_len,hd", [(8, 64), (16, 128), (32, 80), (64, 512), (256, 128)])
+def test_gather_scatter_unaligned_ranges_bit_exact(torch_cuda, page_len, hd):
+    """Gather and scatter over ranges that start and end inside pages and
+    inside 8-token groups of the transposed V page.  Gather matches the
+    oracle; after a scatter the whole layer equals the closed form (the
+    range replaced, every other slot, including the rest of a cut group,
+    unchanged)."""
+    torch = torch_cuda
+    from flint_amd import ops
+
+    say("gather/scatter unaligned", page_len, hd)
+    P = page_len
+    lens = [4 * P + 3, 2 * P + 1]
+    pool = make_pool(lens, kv_heads=2, head_dim=hd, page_len=P, kv_dtype="f16", extra_pages=3)
+    scattered_alloc(pool, lens, random.Random(P + hd), P)
+    info = pool.layer_info(0)
+    rng = np.random.default_rng(P * hd)
+    k = rng.integers(0, 1 << 16, size=(2, info.pool_len, hd), dtype=np.uint16)
+    v = rng.integers(0, 1 << 16, size=(2, info.pool_len, hd), dtype=np.uint16)
+    pool.write_layer(0, k, v)
+    ranges = [(0, 0, lens[0]), (0, 3, P), (0, P - 1, 2), (0, 5, 2 * P + 3), (1, P + 1, P), (1, 2 * P, 1),
+              (0, 1, 6), (1, 0, lens[1])]
+    for seq, t0, n in ranges:
+        table = pool.arena.table_of(seq)
+        ref = oracle.Layer(2, hd, pool.arena.pages(), P, np.array(pool.arena.table(), np.uint32),
+                           pool.arena.max_pages(), oracle.KV_F16, k=k, v=v)
+        kd = torch.empty(2, n, hd, dtype=torch.int16, device="cuda")
+        vd = torch.empty_like(kd)
+        ops.kv_gather(pool, 0, seq, t0, n, kd, vd)
+        torch.cuda.synchronize()
+        rk, rv = ref.gather(seq, t0, n)
+        assert np.array_equal(kd.cpu().numpy().view(np.uint16), rk), (seq, t0, n)
+        assert np.array_equal(vd.cpu().numpy().view(np.uint16), rv), (seq, t0, n)
+        nk = rng.integers(0, 1 << 16, size=(2, n, hd), dtype=np.uint16)
+        nv = rng.integers(0, 1 << 16, size=(2, n, hd), dtype=np.uint16)
+        ops.kv_scatter(pool, 0, seq, t0, n, torch.from_numpy(nk.view(np.int16)).cuda(),
+                       torch.from_numpy(nv.view(np.int16)).cuda())
+        torch.cuda.synchronize()
+        slots = [table[t // P] * P + t % P for t in range(t0, t0 + n)]
+        k[:, slots] = nk
+        v[:, slots] = nv
+        k2, v2 = pool.read_layer(0)
+        assert np.array_equal(k2, k) and np.array_equal(v2, v), (seq, t0, n)
+
+
+@pytest.mark.parametrize("page_len", [8, 16, 64])
+def test_block_copy_partial_pages_bit_exact(torch_cuda, page_len):
+    """Block copies of 1 .. page_len tokens (cutting 8-token V groups) in a
+    pool whose layers have different head dims; every layer matches the
+    oracle's copy of slots [0, tokens)."""
+    torch = torch_cuda
+    from flint_amd import ops
+
+    say("block copy partial", page_len)
+    P = page_len
+    hds = [64, 80, 128]
+    pool = make_pool([P * 8], kv_heads=3, head_dim=128, page_len=P, kv_dtype="bf16", layers=3, extra_pages=8,
+                     head_dims=hds)
+    rng = np.random.default_rng(P)
+    want = []
+    for layer, hd in enumerate(hds):
+        info = pool.layer_info(layer)
+        k = rng.integers(0, 1 << 16, size=(3, info.pool_len, hd), dtype=np.uint16)
+        v = rng.integers(0, 1 << 16, size=(3, info.pool_len, hd), dtype=np.uint16)
+        pool.write_layer(layer, k, v)
+        want.append(oracle.Layer(3, hd, pool.arena.pages(), P, np.array(pool.arena.table(), np.uint32),
+                                 pool.arena.max_pages(), oracle.KV_BF16, k=k, v=v))
+    counts = sorted({1, 7, 8, 9, P - 1, P} & set(range(1, P + 1)))
+    pages = list(range(pool.arena.pages()))
+    random.Random(P).shuffle(pages)
+    triples = [[pages[2 * i], pages[2 * i + 1], c] for i, c in enumerate(counts)]
+    ops.block_copy(pool, triples)
+    torch.cuda.synchronize()
+    for layer in range(3):
+        want[layer].block_copy(triples)
+        k2, v2 = pool.read_layer(layer)
+        assert np.array_equal(k2, want[layer].k) and np.array_equal(v2, want[layer].v), layer
