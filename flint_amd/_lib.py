@@ -12,7 +12,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libthuban_hip.so")
 
-ABI_VERSION = 2  # THB_ABI_VERSION of include/thuban_hip.h
+ABI_VERSION = 3  # THB_ABI_VERSION of include/thuban_hip.h
 
 THB_OK = 0
 THB_ERR_MODEL = -1
@@ -86,6 +86,18 @@ class AttnSpecC(ctypes.Structure):
     ]
 
 
+class RopeC(ctypes.Structure):
+    _fields_ = [
+        ("cos_dev", ctypes.c_void_p),
+        ("sin_dev", ctypes.c_void_p),
+        ("rot", ctypes.c_uint32),
+        ("max_pos", ctypes.c_uint32),
+        ("q_norm_dev", ctypes.c_void_p),
+        ("k_norm_dev", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+    ]
+
+
 # (name, restype, argtypes) for every symbol declared in include/thuban_hip.h.
 _vp, _u32, _u64, _i64, _sz, _int = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int64,
                                     ctypes.c_size_t, ctypes.c_int)
@@ -124,6 +136,11 @@ SIGNATURES = [
     ("thb_kv_store", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _u32, _u32, _vp]),
     ("thb_attn", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_attn_append", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
+    ("thb_rope_rows", _int, [_vp, _u32, _u32, _u32, _u32, _vp, ctypes.POINTER(RopeC), _vp, _u32, _vp]),
+    ("thb_kv_store_rope", _int, [_vp, _u32, _vp, _vp, _u32, ctypes.POINTER(RopeC), _vp, _u32, _u32, _vp]),
+    ("thb_attn_rope", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), ctypes.POINTER(RopeC), _vp, _vp]),
+    ("thb_attn_append_rope", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC),
+                                    ctypes.POINTER(RopeC), _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_block_copy", _int, [_vp, _pu32, _u32, _vp]),

@@ -40,6 +40,7 @@
 
 #include "codec.hpp"
 #include "pool.hpp"
+#include "rope.hpp"
 
 namespace thb {
 namespace {
@@ -56,7 +57,6 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct AttnArgs {
@@ -80,7 +80,30 @@ struct AttnArgs {
     float qscale;  // scale * log2(e), or scale / softcap
     float cap2;    // softcap * log2(e), 0 = no soft-cap
     uint32_t q_f16, y_f16;
+    // Rotary position embedding (thb_attn_rope / thb_attn_append_rope): the
+    // query is normalised and rotated as it is loaded, the fused append
+    // rotates the key.  rope_on = 0: none.
+    uint32_t rope_on;
+    const uint32_t* meta;  // row meta of the call's rows (positions)
+    RopeDev qrope, krope;
 };
+
+// Loads 8 query elements (f16 or f32) of dims [d0, d0 + 8) as f32.
+__device__ inline void load_q8(const AttnArgs& a, uint64_t qbase, uint32_t d0, float (&x)[8]) {
+    if (a.q_f16) {
+        const f16x8 w = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.q) + qbase + d0);
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = static_cast<float>(w[e]);
+    } else {
+        const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + qbase + d0);
+        const f32x4 u0 = p[0], u1 = p[1];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[e] = u0[e];
+            x[4 + e] = u1[e];
+        }
+    }
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -173,6 +196,59 @@ struct Ops<false> {
     }
 };
 
+// Q^T operand of a lane: column (row, head), dims 32j + 8 a4 .. + 8 of k-step
+// j, split into high and low halves.  The raw query is split and the f32
+// scores are scaled afterwards, so the low half stays out of the f16
+// subnormal range.  With rope on, the query head is first normalised
+// (q_norm; the four lanes of the column add their sums of squares) and
+// rotated at the row's position.  Every lane must call it (column sums).
+template <int KS, class O>
+__device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_t head, uint32_t a4,
+                              typename O::in8 (&qh)[KS], typename O::in8 (&ql)[KS]) {
+    const uint32_t hd = a.head_dim;
+    const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
+    uint32_t pos = 0;
+    float inv = 1.0f;
+    if (a.rope_on) {
+        pos = con ? a.meta[8 * row] : 0u;
+        if (a.qrope.w) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KS; j++) {
+                const uint32_t d0 = 32u * j + 8u * a4;
+                if (con && d0 < hd) {
+                    float x[8];
+                    load_q8(a, qbase, d0, x);
+                    ss += sumsq8(x);
+                }
+            }
+            inv = rms_inv(col_sum(ss), hd, a.qrope.eps);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < KS; j++) {
+        const uint32_t d0 = 32u * j + 8u * a4;
+        float x[8];
+        if (con && d0 < hd) {
+            load_q8(a, qbase, d0, x);
+            if (a.rope_on) {
+                if (a.qrope.w) norm8(x, inv, a.qrope.w + d0);
+                if (d0 < a.qrope.rot) {
+                    const uint32_t dp = d0 < a.qrope.half ? d0 + a.qrope.half : d0 - a.qrope.half;
+                    float y[8];
+                    load_q8(a, qbase, dp, y);
+                    if (a.qrope.w) norm8(y, inv, a.qrope.w + dp);
+                    rotate8(x, y, d0, pos, a.qrope);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = 0.0f;
+        }
+        O::split8(x, qh[j], ql[j]);
+    }
+}
+
 // One (group, partition, KV head) per workgroup of W waves.  NB tiles of
 // loads are kept in flight per wave: tile i + NB is requested as soon as
 // tile i has been consumed.
@@ -230,37 +306,9 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
         chi = min(a.ranges[2 * row + 1], te);
     }
 
-    // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8], split into high
-    // and low halves.  The raw query is split and the f32 scores are scaled
-    // afterwards, so the low half stays out of the f16 subnormal range.
+    // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8], split hi/lo.
     in8 qh[KS], ql[KS];
-    {
-        const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
-#pragma unroll
-        for (int j = 0; j < KS; j++) {
-            const uint32_t d0 = 32u * j + 8u * a4;
-            float x[8];
-            if (con && d0 < hd) {
-                if (a.q_f16) {
-                    const f16x8 w = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.q) + qbase + d0);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) x[e] = static_cast<float>(w[e]);
-                } else {
-                    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + qbase + d0);
-                    const f32x4 u0 = p[0], u1 = p[1];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        x[e] = u0[e];
-                        x[4 + e] = u1[e];
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) x[e] = 0.0f;
-            }
-            O::split8(x, qh[j], ql[j]);
-        }
-    }
+    load_q<KS, O>(a, con, row, head, a4, qh, ql);
 
 
     // This wave's run of 16-token tiles inside [tb, te).
@@ -308,12 +356,39 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     uint64_t app_e = 0;
     bool app_v = false, app_own = false;
     uint4 app_w = make_uint4(0u, 0u, 0u, 0u);
-    if (lane < app_items) {
+    if (lane < app_items && !a.rope_on) {
         app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
         if (app_own) app_w = load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e);
     }
     __syncthreads();
-    if (app_items != 0) {
+    if (app_items != 0 && a.rope_on) {
+        // Rotary append: the key head of each row this wave owns, one chunk
+        // of 8 dims per lane (the norm and the rotation need the whole head),
+        // exactly as kv_store_rope_kernel.
+        for (uint32_t ar = 0; ar < R; ar++) {
+            const uint32_t pos = a.ranges[2 * (r0 + ar) + 1] - 1;
+            if (pos < ws || pos >= we) continue;  // wave-uniform
+            const uint64_t e = (static_cast<uint64_t>(r0 + ar) * a.n_kvh + kvh) * hd + 8u * lane;
+            float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            if (lane < cpr) load8_f32(a.src_dtype, a.k_src, e, x);
+            rope_head_wave(x, lane, cpr, pos, a.krope);
+            if (lane < cpr) {
+                uint32_t w[4];
+#pragma unroll
+                for (int q2 = 0; q2 < 4; q2++) {
+                    if (a.src_dtype == THB_DT_F16)
+                        w[q2] = conv16<THB_DT_F16, KVE>(f32_to_f16_rne(x[2 * q2])) |
+                                (conv16<THB_DT_F16, KVE>(f32_to_f16_rne(x[2 * q2 + 1])) << 16);
+                    else
+                        w[q2] = conv32<KVE>(__float_as_uint(x[2 * q2])) |
+                                (conv32<KVE>(__float_as_uint(x[2 * q2 + 1])) << 16);
+                }
+                app_store(pos, false, 8u * lane, make_uint4(w[0], w[1], w[2], w[3]));
+                app_store(pos, true, 8u * lane, load_encode8_rt<KVE>(a.src_dtype, a.v_src, e));
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    } else if (app_items != 0) {
         if (app_own) app_store(app_pos, app_v, app_d, app_w);
         for (uint32_t t = lane + 64; t < app_items; t += 64) {
             if (app_decode(t, app_pos, app_v, app_d, app_e))
@@ -595,33 +670,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
         chi = min(a.ranges[2 * row + 1], te);
     }
     in8 qh[KS], ql[KS];
-    {
-        const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
-#pragma unroll
-        for (int j = 0; j < KS; j++) {
-            const uint32_t d0 = 32u * j + 8u * a4;
-            float x[8];
-            if (con && d0 < hd) {
-                if (a.q_f16) {
-                    const f16x8 w = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.q) + qbase + d0);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) x[e] = static_cast<float>(w[e]);
-                } else {
-                    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + qbase + d0);
-                    const f32x4 u0 = p[0], u1 = p[1];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        x[e] = u0[e];
-                        x[4 + e] = u1[e];
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) x[e] = 0.0f;
-            }
-            O::split8(x, qh[j], ql[j]);
-        }
-    }
+    load_q<KS, O>(a, con, row, head, a4, qh, ql);
 
     const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
     const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
@@ -1126,8 +1175,10 @@ int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint
 }
 
 // Launches attention (and, when app is set, the fused append) for a plan.
+// With rope set, the query is rotated as it is loaded (and the fused append
+// rotates the key); meta is the row meta of the call's first row.
 void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec& sp, const AttnPlan& plan,
-                 const AppendSrc* app, hipStream_t s) {
+                 const AppendSrc* app, const thb_rope* rope, const uint32_t* meta, hipStream_t s) {
     const uint32_t hd = pool->geom[layer].head_dim;
     const uint32_t hd_t = plan.hd_t;
     float* part_o = nullptr;
@@ -1175,6 +1226,10 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
     }
     a.q_f16 = sp.q_dtype == THB_DT_F16;
     a.y_f16 = sp.y_dtype == THB_DT_F16;
+    a.rope_on = rope != nullptr;
+    a.meta = meta;
+    a.qrope = rope ? rope_dev(*rope, true) : RopeDev{};
+    a.krope = rope ? rope_dev(*rope, false) : RopeDev{};
     const bool f16 = pool->kv_dtype == THB_KV_F16_RNE;
     const uint64_t n_wg = static_cast<uint64_t>(plan.n_items) * pool->kv_heads;
     const uint64_t n_pwg = static_cast<uint64_t>(plan.n_bitems) * pool->kv_heads;
@@ -1210,31 +1265,40 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
 
 using namespace thb;
 
-extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec,
-                        const thb_rows* rows, void* stream) {
+namespace {
+
+int attn_impl(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec, const thb_rope* rope,
+              const thb_rows* rows, void* stream) {
     if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
     if (spec->m == 0) return layer < pool->layers ? THB_OK : check_attn_call(pool, layer, q, y, *spec, rows);
     if (int rc = check_attn_call(pool, layer, q, y, *spec, rows)) return rc;
+    if (rope)
+        if (int rc = check_rope(rope, pool->geom[layer].head_dim, rows, spec->row_off, spec->m)) return rc;
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
         AttnPlan* plan = nullptr;
         if (int rc = get_plan(pool, rows, *spec, pool->geom[layer].head_dim, s, &plan)) return rc;
-        launch_plan(pool, layer, q, y, *spec, *plan, nullptr, s);
+        launch_plan(pool, layer, q, y, *spec, *plan, nullptr, rope, rows->dev + 8 * static_cast<size_t>(spec->row_off),
+                    s);
         return THB_OK;
     });
 }
 
-extern "C" int thb_attn_append(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src,
-                               uint32_t src_dtype, const void* q, void* y, const thb_attn_spec* spec,
-                               const thb_rows* rows, void* stream) {
+int attn_append_impl(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src, uint32_t src_dtype,
+                     const void* q, void* y, const thb_attn_spec* spec, const thb_rope* rope, const thb_rows* rows,
+                     void* stream) {
     if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
     if (spec->m == 0) return layer < pool->layers ? THB_OK : check_attn_call(pool, layer, q, y, *spec, rows);
     if (int rc = check_attn_call(pool, layer, q, y, *spec, rows)) return rc;
     if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
     if (src_dtype > THB_DT_BF16) return fail(THB_ERR_INVALID, "unknown src_dtype " + std::to_string(src_dtype));
+    if (rope && src_dtype == THB_DT_BF16)
+        return fail(THB_ERR_INVALID, "rotary append takes f32 or f16 sources (src_dtype 2)");
     if ((reinterpret_cast<uintptr_t>(k_src) & 15u) || (reinterpret_cast<uintptr_t>(v_src) & 15u))
         return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
+    if (rope)
+        if (int rc = check_rope(rope, pool->geom[layer].head_dim, rows, spec->row_off, spec->m)) return rc;
     // Pages must cover every appended token (thb_kv_store's check; the
     // append takes each row's sequence from the row meta, kv_store.wgsl:39).
     const Arena& arena = pool->arena.a;
@@ -1254,6 +1318,7 @@ extern "C" int thb_attn_append(thb_pool* pool, uint32_t layer, const void* k_src
         pool_flush(pool, s);
         AttnPlan* plan = nullptr;
         if (int rc = get_plan(pool, rows, *spec, pool->geom[layer].head_dim, s, &plan)) return rc;
+        const uint32_t* meta = rows->dev + 8 * static_cast<size_t>(spec->row_off);
         // The row meta's sequence must be the one the append uses: a fixed
         // AttnSpec.seq that differs from the rows' own seq is not fused.
         bool fuse = plan->fusable;
@@ -1262,12 +1327,40 @@ extern "C" int thb_attn_append(thb_pool* pool, uint32_t layer, const void* k_src
                 fuse = rows->host[8 * r + 1] == spec->seq;
         if (fuse) {
             const AppendSrc app{k_src, v_src, src_dtype};
-            launch_plan(pool, layer, q, y, *spec, *plan, &app, s);
+            launch_plan(pool, layer, q, y, *spec, *plan, &app, rope, meta, s);
             return THB_OK;
         }
-        if (int rc = thb_kv_store(pool, layer, k_src, v_src, src_dtype, rows, spec->row_off, spec->m, stream))
-            return rc;
-        launch_plan(pool, layer, q, y, *spec, *plan, nullptr, s);
+        const int rc = rope ? thb_kv_store_rope(pool, layer, k_src, v_src, src_dtype, rope, rows, spec->row_off,
+                                                spec->m, stream)
+                            : thb_kv_store(pool, layer, k_src, v_src, src_dtype, rows, spec->row_off, spec->m, stream);
+        if (rc) return rc;
+        launch_plan(pool, layer, q, y, *spec, *plan, nullptr, rope, meta, s);
         return THB_OK;
     });
+}
+
+}  // namespace
+
+extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec,
+                        const thb_rows* rows, void* stream) {
+    return attn_impl(pool, layer, q, y, spec, nullptr, rows, stream);
+}
+
+extern "C" int thb_attn_rope(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec,
+                             const thb_rope* rope, const thb_rows* rows, void* stream) {
+    if (!rope) return fail(THB_ERR_INVALID, "null rope");
+    return attn_impl(pool, layer, q, y, spec, rope, rows, stream);
+}
+
+extern "C" int thb_attn_append(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src,
+                               uint32_t src_dtype, const void* q, void* y, const thb_attn_spec* spec,
+                               const thb_rows* rows, void* stream) {
+    return attn_append_impl(pool, layer, k_src, v_src, src_dtype, q, y, spec, nullptr, rows, stream);
+}
+
+extern "C" int thb_attn_append_rope(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src,
+                                    uint32_t src_dtype, const void* q, void* y, const thb_attn_spec* spec,
+                                    const thb_rope* rope, const thb_rows* rows, void* stream) {
+    if (!rope) return fail(THB_ERR_INVALID, "null rope");
+    return attn_append_impl(pool, layer, k_src, v_src, src_dtype, q, y, spec, rope, rows, stream);
 }

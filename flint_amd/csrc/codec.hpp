@@ -73,6 +73,7 @@ __device__ inline uint32_t conv32(uint32_t bits) {
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load (the source rows are read exactly once).
 __device__ inline uint4 ld_stream16(const void* p) {

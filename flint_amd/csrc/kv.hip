@@ -12,6 +12,7 @@
 
 #include "codec.hpp"
 #include "pool.hpp"
+#include "rope.hpp"
 
 namespace thb {
 namespace {
@@ -70,6 +71,7 @@ struct RunArgs {
     const uint32_t* table;  // [seqs * max_pages]
     uint64_t plane;
     uint32_t max_pages, page_shift, head_dim, kv_heads;
+    uint32_t do_k;  // 0: V only (K is written by the rotary append kernel)
 };
 
 constexpr uint32_t kMaxRun = 64;  // tokens of one run (LDS: kMaxRun * head_dim * 2 bytes)
@@ -93,8 +95,9 @@ __global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
     for (uint32_t u = threadIdx.x; u < len * cph; u += 256) {
         const uint32_t ch = u / len, t = u - ch * len;
         const uint64_t e = ((static_cast<uint64_t>(row0 + t)) * a.kv_heads + h) * hd + 8u * ch;
-        *reinterpret_cast<uint4*>(a.k + pbase + (static_cast<uint64_t>(8u * ch) << shift) + ((j0 + t) << 3)) =
-            load_encode8<SRC, KV>(a.k_src, e);
+        if (a.do_k)
+            *reinterpret_cast<uint4*>(a.k + pbase + (static_cast<uint64_t>(8u * ch) << shift) + ((j0 + t) << 3)) =
+                load_encode8<SRC, KV>(a.k_src, e);
         s_v[t * cph + ch] = load_encode8<SRC, KV>(a.v_src, e);
     }
     __syncthreads();
@@ -116,6 +119,93 @@ __global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
                 if (j >= j0 && j < j0 + len) dst[e] = sv[(j - j0) * hd + d];
             }
         }
+    }
+}
+
+struct RopeStoreArgs {
+    const void* k_src;  // [m, kv_heads, head_dim], f32 or f16
+    const void* v_src;
+    uint16_t* k;
+    uint16_t* v;
+    const uint32_t* meta;
+    const uint32_t* table;
+    uint64_t plane;
+    uint32_t max_pages, page_shift, head_dim, kv_heads, m;
+    uint32_t do_v;  // 0: K only (V is written by the run kernel)
+    RopeDev rope;
+};
+
+// Rotary append: one wavefront per (row, KV head), lane u holding dims
+// [8u, 8u + 8).  K is normalised (with a weight), rotated at the row's
+// position, rounded to the source type and encoded into its page chunk; V
+// is stored as by kv_store_kernel.  Grid: ceil(m * kv_heads / 4) x 256.
+template <uint32_t SRC, uint32_t KV>
+__global__ __launch_bounds__(256) void kv_store_rope_kernel(RopeStoreArgs a) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wi >= a.m * a.kv_heads) return;  // whole wavefront
+    const uint32_t row = wi / a.kv_heads, h = wi - row * a.kv_heads;
+    const uint32_t cph = a.head_dim >> 3;
+    const uint32_t pos = a.meta[8 * row], seq = a.meta[8 * row + 1];
+    const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (pos >> a.page_shift)];
+    const uint32_t j = pos & ((1u << a.page_shift) - 1u);
+    const uint64_t e = (static_cast<uint64_t>(row) * a.kv_heads + h) * a.head_dim + 8u * lane;
+    const uint64_t pbase = h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + 8u * lane) << a.page_shift);
+    float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (lane < cph) load8_f32(SRC, a.k_src, e, x);
+    rope_head_wave(x, lane, cph, pos, a.rope);
+    if (lane >= cph) return;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if constexpr (SRC == THB_DT_F16)
+            w[q] = conv16<THB_DT_F16, KV>(f32_to_f16_rne(x[2 * q])) |
+                   (conv16<THB_DT_F16, KV>(f32_to_f16_rne(x[2 * q + 1])) << 16);
+        else
+            w[q] = conv32<KV>(__float_as_uint(x[2 * q])) | (conv32<KV>(__float_as_uint(x[2 * q + 1])) << 16);
+    }
+    *reinterpret_cast<uint4*>(a.k + pbase + (j << 3)) = make_uint4(w[0], w[1], w[2], w[3]);
+    if (!a.do_v) return;
+    const uint4 vw = load_encode8<SRC, KV>(a.v_src, e);
+    uint16_t* dst = a.v + pbase + j;
+    const uint32_t vs[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        dst[static_cast<uint64_t>(2 * q) << a.page_shift] = static_cast<uint16_t>(vs[q] & 0xffffu);
+        dst[static_cast<uint64_t>(2 * q + 1) << a.page_shift] = static_cast<uint16_t>(vs[q] >> 16);
+    }
+}
+
+struct RopeRowsArgs {
+    void* x;  // [m, heads, head_dim], f32 or f16, in place
+    const uint32_t* meta;
+    uint32_t m, heads, head_dim;
+    RopeDev rope;
+};
+
+// ops::rope / ops::norm_rope in place: one wavefront per (row, head).
+template <uint32_t DT>
+__global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wi >= a.m * a.heads) return;  // whole wavefront
+    const uint32_t row = wi / a.heads;
+    const uint32_t cph = a.head_dim >> 3;
+    const uint32_t pos = a.meta[8 * row];
+    const uint64_t e = static_cast<uint64_t>(wi) * a.head_dim + 8u * lane;
+    float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (lane < cph) load8_f32(DT, a.x, e, x);
+    rope_head_wave(x, lane, cph, pos, a.rope);
+    if (lane >= cph) return;
+    if constexpr (DT == THB_DT_F16) {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) w[q] = f32_to_f16_rne(x[2 * q]) | (f32_to_f16_rne(x[2 * q + 1]) << 16);
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.x) + e) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        f32x4* p = reinterpret_cast<f32x4*>(static_cast<float*>(a.x) + e);
+        p[0] = f32x4{x[0], x[1], x[2], x[3]};
+        p[1] = f32x4{x[4], x[5], x[6], x[7]};
     }
 }
 
@@ -426,7 +516,33 @@ int check_cover(const thb_pool* p, uint32_t seq, uint64_t end) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+template <uint32_t SRC>
+void launch_store_rope(uint32_t kv, dim3 grid, const RopeStoreArgs& a, hipStream_t s) {
+    if (kv == THB_KV_F16_RNE)
+        hipLaunchKernelGGL((kv_store_rope_kernel<SRC, THB_KV_F16_RNE>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((kv_store_rope_kernel<SRC, THB_KV_BF16_TRUNC>), grid, dim3(256), 0, s, a);
+}
+
 }  // namespace
+
+int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint32_t row_off, uint32_t m) {
+    if (!r || !r->cos_dev || !r->sin_dev) return fail(THB_ERR_INVALID, "null rope tables");
+    if (r->rot == 0 || r->rot % 16 != 0 || r->rot > head_dim)
+        return fail(THB_ERR_CONFIG, "rope rot " + std::to_string(r->rot) +
+                                        " must be a positive multiple of 16 not above head_dim " +
+                                        std::to_string(head_dim));
+    if (!aligned16(r->cos_dev) || !aligned16(r->sin_dev) || !aligned16(r->q_norm_dev) || !aligned16(r->k_norm_dev))
+        return fail(THB_ERR_INVALID, "rope tables and norm weights must be 16-byte aligned");
+    if (static_cast<uint64_t>(row_off) + m > rows->m)
+        return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(rows->m) + " rows, call needs " +
+                                         std::to_string(static_cast<uint64_t>(row_off) + m));
+    for (uint32_t i = row_off; i < row_off + m; i++)
+        if (rows->host[8 * i] >= r->max_pos)
+            return fail(THB_ERR_MODEL, "row position " + std::to_string(rows->host[8 * i]) +
+                                           " outside the rope tables (" + std::to_string(r->max_pos) + " positions)");
+    return THB_OK;
+}
 
 void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_t max_tokens, hipStream_t stream) {
     if (n == 0 || max_tokens == 0) return;
@@ -515,6 +631,7 @@ int thb_kv_store(thb_pool* pool, uint32_t layer, const void* k_src, const void* 
             ra.page_shift = a.page_shift;
             ra.head_dim = a.head_dim;
             ra.kv_heads = pool->kv_heads;
+            ra.do_k = 1;
             const uint64_t n_wg = static_cast<uint64_t>(n_runs) * pool->kv_heads;
             if (n_wg > 0x7FFFFFFFull) throw HipError{hipErrorInvalidConfiguration, "append grid too large"};
             const dim3 grid(static_cast<uint32_t>(n_wg));
@@ -634,6 +751,114 @@ int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* st
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
         launch_block_copy(pool, triples, n, max_tok, s);
+        return THB_OK;
+    });
+}
+
+int thb_rope_rows(void* x, uint32_t dtype, uint32_t m, uint32_t heads, uint32_t head_dim, const float* norm_w,
+                  const thb_rope* rope, const thb_rows* rows, uint32_t row_off, void* stream) {
+    if (!rows) return fail(THB_ERR_INVALID, "null rows");
+    if (m == 0 || heads == 0) return THB_OK;
+    if (!x || !aligned16(x)) return fail(THB_ERR_INVALID, "x must be a 16-byte aligned device buffer");
+    if (dtype != THB_DT_F32 && dtype != THB_DT_F16)
+        return fail(THB_ERR_INVALID, "rope rows take f32 or f16 (dtype " + std::to_string(dtype) + ")");
+    if (int rc = thb_check_head_dim(head_dim)) return rc;
+    if (int rc = check_rope(rope, head_dim, rows, row_off, m)) return rc;
+    if (!aligned16(norm_w)) return fail(THB_ERR_INVALID, "norm weight must be 16-byte aligned");
+    const uint64_t waves = static_cast<uint64_t>(m) * heads;
+    if (waves > 0x7FFFFFFFull) return fail(THB_ERR_INVALID, "rope rows: m * heads too large");
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        RopeRowsArgs a;
+        a.x = x;
+        a.meta = rows->dev + 8 * static_cast<size_t>(row_off);
+        a.m = m;
+        a.heads = heads;
+        a.head_dim = head_dim;
+        a.rope = rope_dev(*rope, true);
+        a.rope.w = norm_w;
+        const dim3 grid(static_cast<uint32_t>((waves + 3) / 4));
+        if (dtype == THB_DT_F16)
+            hipLaunchKernelGGL(rope_rows_kernel<THB_DT_F16>, grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(rope_rows_kernel<THB_DT_F32>, grid, dim3(256), 0, s, a);
+        THB_HIP(hipGetLastError());
+        return THB_OK;
+    });
+}
+
+int thb_kv_store_rope(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src, uint32_t src_dtype,
+                      const thb_rope* rope, const thb_rows* rows, uint32_t row_off, uint32_t m, void* stream) {
+    if (!pool || !rows) return fail(THB_ERR_INVALID, "null pool or rows");
+    if (int rc = check_layer(pool, layer)) return rc;
+    if (m == 0) return THB_OK;
+    if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
+    if (src_dtype != THB_DT_F32 && src_dtype != THB_DT_F16)
+        return fail(THB_ERR_INVALID, "rotary append takes f32 or f16 sources (src_dtype " +
+                                         std::to_string(src_dtype) + ")");
+    if (!aligned16(k_src) || !aligned16(v_src)) return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
+    if (int rc = check_rope(rope, pool->geom[layer].head_dim, rows, row_off, m)) return rc;
+    for (uint32_t r = row_off; r < row_off + m; r++) {
+        uint32_t pos = rows->host[8 * r], seq = rows->host[8 * r + 1];
+        if (int rc = check_cover(pool, seq, static_cast<uint64_t>(pos) + 1)) return rc;
+    }
+    const uint64_t waves = static_cast<uint64_t>(m) * pool->kv_heads;
+    if (waves > 0x7FFFFFFFull) return fail(THB_ERR_INVALID, "rotary append: m * kv_heads too large");
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        const LayerGeom& g = pool->geom[layer];
+        RopeStoreArgs a;
+        a.k_src = k_src;
+        a.v_src = v_src;
+        a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
+        a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
+        a.meta = rows->dev + 8 * static_cast<size_t>(row_off);
+        a.table = pool->table_dev;
+        a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * g.head_dim;
+        a.max_pages = pool->arena.a.max_pages();
+        a.page_shift = pool->page_shift;
+        a.head_dim = g.head_dim;
+        a.kv_heads = pool->kv_heads;
+        a.m = m;
+        a.rope = rope_dev(*rope, false);
+        // Prefill chunks: V goes through the run kernel (whole page rows).
+        std::vector<uint32_t> runs;
+        const uint32_t long_rows = make_runs(rows->host.data() + 8 * static_cast<size_t>(row_off), m,
+                                             pool->page_shift, runs);
+        const bool by_runs = 2 * static_cast<uint64_t>(long_rows) >= m;
+        a.do_v = by_runs ? 0u : 1u;
+        const dim3 grid(static_cast<uint32_t>((waves + 3) / 4));
+        if (src_dtype == THB_DT_F16)
+            launch_store_rope<THB_DT_F16>(pool->kv_dtype, grid, a, s);
+        else
+            launch_store_rope<THB_DT_F32>(pool->kv_dtype, grid, a, s);
+        THB_HIP(hipGetLastError());
+        if (by_runs) {
+            const uint32_t n_runs = static_cast<uint32_t>(runs.size() / 4);
+            void* dev = pool->run_buf.reserve(runs.size() * 4, false);
+            pool->stager.upload(dev, runs.data(), runs.size() * 4, s);
+            RunArgs ra;
+            ra.k_src = k_src;
+            ra.v_src = v_src;
+            ra.k = a.k;
+            ra.v = a.v;
+            ra.runs = static_cast<const uint32_t*>(dev);
+            ra.table = a.table;
+            ra.plane = a.plane;
+            ra.max_pages = a.max_pages;
+            ra.page_shift = a.page_shift;
+            ra.head_dim = a.head_dim;
+            ra.kv_heads = pool->kv_heads;
+            ra.do_k = 0;
+            const uint64_t n_wg = static_cast<uint64_t>(n_runs) * pool->kv_heads;
+            if (n_wg > 0x7FFFFFFFull) throw HipError{hipErrorInvalidConfiguration, "append grid too large"};
+            if (src_dtype == THB_DT_F16)
+                launch_runs<THB_DT_F16>(pool->kv_dtype, dim3(static_cast<uint32_t>(n_wg)), ra, s);
+            else
+                launch_runs<THB_DT_F32>(pool->kv_dtype, dim3(static_cast<uint32_t>(n_wg)), ra, s);
+            THB_HIP(hipGetLastError());
+        }
         return THB_OK;
     });
 }

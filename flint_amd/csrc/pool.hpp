@@ -83,6 +83,8 @@ struct thb_pool {
 namespace thb {
 // Uploads dirty block-table rows and executes pending page copies.
 void pool_flush(thb_pool* p, hipStream_t stream);
+// Validates a thb_rope for rows [row_off, row_off + m) of head_dim vectors.
+int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint32_t row_off, uint32_t m);
 // Launches the block-copy kernel for n non-chaining host triples (passed in
 // the kernel arguments when few, else uploaded through the stager).
 void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_t max_tokens, hipStream_t stream);

@@ -54,7 +54,7 @@ extern "C" {
 const char* thb_last_error(void);
 /* ABI revision of this header. */
 uint32_t thb_abi_version(void);
-#define THB_ABI_VERSION 2u
+#define THB_ABI_VERSION 3u
 
 /* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90):
  * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]".  This backend also needs
@@ -235,6 +235,59 @@ int thb_attn(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, con
  * instead of two); otherwise the two kernels run in order. */
 int thb_attn_append(thb_pool* pool, uint32_t layer, const void* k_src_dev, const void* v_src_dev, uint32_t src_dtype,
                     const void* q_dev, void* y_dev, const thb_attn_spec* spec, const thb_rows* rows, void* stream);
+
+/* ----------------------------------------------------------------- RoPE */
+
+/* Rotary position embedding as rope.wgsl:16-40 / ops::rope (ops/rope.rs:22-48)
+ * and, with a weight, the RMSNorm + rotation of norm.wgsl MODE 4 /
+ * ops::norm_rope (ops/norm.rs:73-109), keyed off each row's row-meta pos.
+ * With half = rot / 2 and c = cos[pos][d % half], s = sin[pos][d % half]:
+ *   y[d] = x[d] c - x[d + half] s   (d < half)
+ *   y[d] = x[d] c + x[d - half] s   (half <= d < rot)
+ *   y[d] = x[d]                     (d >= rot)
+ * where x is the head vector, first scaled by w[d] / sqrt(mean(x^2) + eps)
+ * when a norm weight is given.  The tables are the reference's rope_tables
+ * (ops/rope.rs:50-80): f32 [max_pos][rot / 2], on the device.  Arithmetic is
+ * f32 without fused multiply-adds; the sum of squares runs over 8-element
+ * chunks in order, then over the chunks in order. */
+typedef struct thb_rope {
+    const float* cos_dev;    /* [max_pos][rot / 2] */
+    const float* sin_dev;
+    uint32_t rot;            /* rotated leading dims: a multiple of 16, <= head_dim */
+    uint32_t max_pos;        /* table rows; every row's pos must be below it */
+    const float* q_norm_dev; /* [head_dim] RMSNorm weight of query heads, or NULL (rope only) */
+    const float* k_norm_dev; /* [head_dim] RMSNorm weight of key heads, or NULL */
+    float eps;               /* RMSNorm epsilon */
+} thb_rope;
+
+/* ops::rope / ops::norm_rope on rows [row_off, row_off + m) of x [m, heads,
+ * head_dim] (dtype THB_DT_F32 or THB_DT_F16, 16-byte aligned), in place.
+ * norm_w_dev: [head_dim] weight (norm_rope) or NULL (rope only). */
+int thb_rope_rows(void* x_dev, uint32_t dtype, uint32_t m, uint32_t heads, uint32_t head_dim,
+                  const float* norm_w_dev, const thb_rope* rope, const thb_rows* rows, uint32_t row_off,
+                  void* stream);
+
+/* No reference counterpart: the model's ops::rope(k) (or norm_rope with
+ * rope->k_norm_dev) followed by ops::kv_store (transformer/forward.rs
+ * :186-313) in one pass: the rotated K is encoded straight into the pages,
+ * never written back.  V is stored as by thb_kv_store.  The pool contents
+ * are bit-identical to thb_rope_rows on K followed by thb_kv_store. */
+int thb_kv_store_rope(thb_pool* pool, uint32_t layer, const void* k_src_dev, const void* v_src_dev,
+                      uint32_t src_dtype, const thb_rope* rope, const thb_rows* rows, uint32_t row_off, uint32_t m,
+                      void* stream);
+
+/* thb_attn with the query rotated (and normalised with rope->q_norm_dev) as
+ * it is loaded: ops::rope(q) / norm_rope(q) + ops::attn in one launch. */
+int thb_attn_rope(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
+                  const thb_rope* rope, const thb_rows* rows, void* stream);
+
+/* The whole per-layer step (transformer/forward.rs:186-336): rope of q and
+ * k, kv_store, attention.  When thb_attn_append would fuse, one launch does
+ * all of it; otherwise thb_kv_store_rope then thb_attn_rope.  Results are
+ * bit-identical either way. */
+int thb_attn_append_rope(thb_pool* pool, uint32_t layer, const void* k_src_dev, const void* v_src_dev,
+                         uint32_t src_dtype, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
+                         const thb_rope* rope, const thb_rows* rows, void* stream);
 
 /* No reference counterpart.  Copies tokens [t0, t0 + n) of seq, layer
  * `layer`, into contiguous k_dst/v_dst [kv_heads, n, head_dim] in the KV type

@@ -97,6 +97,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_kv_gather.restype = ctypes.c_int
     L.orc_block_copy.argtypes = [ctypes.POINTER(OrcLayer), vp, u32]
     L.orc_block_copy.restype = None
+    L.orc_rope_rows.argtypes = [vp, u32, u32, u32, u32, vp, vp, u32, vp, vp, ctypes.c_float]
+    L.orc_rope_rows.restype = ctypes.c_int
     L.orc_num_threads.argtypes = []
     L.orc_num_threads.restype = ctypes.c_int
 
@@ -196,6 +198,27 @@ class Layer:
         t = np.ascontiguousarray(triples, dtype=np.uint32).reshape(-1)
         s = self._struct()
         lib().orc_block_copy(ctypes.byref(s), _ptr(t), len(t) // 3)
+
+
+def rope_rows(x, pos, rot, cos, sin, w=None, eps=1e-6) -> np.ndarray:
+    """rope.wgsl:16-40 / norm.wgsl MODE 4 on x [m, heads, hd] (float32;
+    float16 input is widened and the result rounded back to float16 with
+    f32_to_f16).  pos: the m row positions; cos/sin [max_pos, rot/2]."""
+    x = np.asarray(x)
+    half_out = x.dtype == np.float16
+    v = np.ascontiguousarray(x.astype(np.float32))
+    m, heads, hd = v.shape
+    p = np.ascontiguousarray(np.asarray(pos, np.uint32))
+    c = np.ascontiguousarray(cos, np.float32)
+    s = np.ascontiguousarray(sin, np.float32)
+    wv = None if w is None else np.ascontiguousarray(w, np.float32)
+    rc = lib().orc_rope_rows(_ptr(v), m, heads, hd, rot, _ptr(c), _ptr(s), c.shape[0], _ptr(p),
+                             _ptr(wv) if wv is not None else None, eps)
+    if rc != 0:
+        raise ValueError(f"oracle rope: bad input (code {rc})")
+    if half_out:
+        return f32_to_f16(v).view(np.float16)
+    return v
 
 
 def attn_ranges(args, m, seq=None, causal=True, window=0):

@@ -12,6 +12,8 @@
  *   crates/thuban_kernel/wgsl/kv_store.wgsl:20-46 append/scatter
  *   crates/thuban_kernel/wgsl/attn.wgsl:42-365    paged attention masks/kv_len
  *   crates/thuban_backend/tests/support/cpu_ref.rs:172-228 exact softmax
+ *   crates/thuban_kernel/wgsl/rope.wgsl:16-40     rotary embedding
+ *   crates/thuban_kernel/wgsl/norm.wgsl:122-160   RMSNorm + rotation (MODE 4)
  *
  * How each function is pinned (checked by tests/test_oracle.py):
  *   codecs        thuban_num known-answer tests (lib.rs:78-139) + exhaustive
@@ -26,6 +28,14 @@
  *                 round trips against kv_store)
  *   softcap       closed form cap*tanh(s/cap); parity vs the reference is
  *                 unpinned because the reference has no attention soft-cap.
+ *   rope_rows     reference anchor kernels.rs:1410-1436, the rope_case vectors
+ *                 of kernels.rs:1200-1263 (LCG inputs) against a double-
+ *                 precision rotation, position 0 = identity, dims >= rot
+ *                 untouched, pair norms kept; the RMSNorm against a double-
+ *                 precision RMS.  Sums of squares run over 8-element chunks in
+ *                 order, then over the chunks in order (the WGSL kernel sums
+ *                 4-element vectors per thread and reduces by a tree; float
+ *                 association differs, within the reference tests' 1e-5).
  */
 #include <math.h>
 #include <stdint.h>
@@ -387,6 +397,47 @@ int orc_attn(const orc_layer* L, const float* q, void* y, const uint32_t* args, 
     }
     free(lo);
     return status;
+}
+
+/* ------------------------------------------------------------------ rope */
+
+/* rope.wgsl:16-40 (cpu_ref.rs:132-152) and, with a weight w, norm.wgsl
+ * MODE 4 (:122-160): x [m][heads][hd] in place; row r is at position
+ * pos[r] (its row meta).  Products and sums are separate roundings (this
+ * file is compiled with -ffp-contract=off).  Returns -1 when a position is
+ * outside the tables, -2 for a shape it does not take. */
+int orc_rope_rows(float* x, uint32_t m, uint32_t heads, uint32_t hd, uint32_t rot, const float* cos_t,
+                  const float* sin_t, uint32_t max_pos, const uint32_t* pos, const float* w, float eps) {
+    const uint32_t half = rot / 2;
+    float t[512];
+    if (hd > 512 || rot > hd || rot % 2) return -2;
+    for (uint32_t r = 0; r < m; r++) {
+        if (pos[r] >= max_pos) return -1;
+        for (uint32_t h = 0; h < heads; h++) {
+            float* v = x + ((size_t)r * heads + h) * hd;
+            float inv = 1.0f;
+            if (w) {
+                float ss = 0.0f;
+                for (uint32_t c = 0; c < hd / 8; c++) {
+                    float sc = 0.0f;
+                    for (uint32_t e = 0; e < 8; e++) sc = sc + v[8 * c + e] * v[8 * c + e];
+                    ss = ss + sc;
+                }
+                inv = 1.0f / sqrtf(ss / (float)hd + eps);
+            }
+            for (uint32_t d = 0; d < hd; d++) t[d] = w ? (v[d] * inv) * w[d] : v[d];
+            for (uint32_t d = 0; d < hd; d++) {
+                if (d >= rot) {
+                    v[d] = t[d];
+                    continue;
+                }
+                const size_t ti = (size_t)pos[r] * half + d % half;
+                const float c = cos_t[ti], s = sin_t[ti];
+                v[d] = d < half ? t[d] * c - t[d + half] * s : t[d] * c + t[d - half] * s;
+            }
+        }
+    }
+    return 0;
 }
 
 /* ------------------------------------------------- gather / block copy */

@@ -164,8 +164,52 @@ def attn_cases():
             dict(base, name="window_1", window=1, expect=[3.0, 4.0])]
 
 
+# -------------------------------------------------------------------- rope
+def rope_cases():
+    """rope_case (kernels.rs:1200-1253) at the two shapes the reference runs
+    (kernels.rs:1255-1263): x from Rng(seed), theta 1e7 tables built in
+    double and rounded to f32 as the test does, rows at positions pos + r.
+    The expectation is the rotation evaluated in double precision on those
+    f32 inputs (cpu_ref.rs:132-152 is the same formula in f32); the
+    reference accepts |gpu - cpu| <= 1e-5 |cpu| + 1e-6.  Plus anchor_rope
+    (kernels.rs:1410-1436), whose expectation is spelled out in the test."""
+    cases = []
+    for m, heads, hd, rot, pos, seed in [(2, 2, 32, 16, 2, 51), (1, 1, 32, 32, 0, 53)]:
+        half = rot // 2
+        max_seq = pos + m + 2
+        x = np.array(Rng(seed).fill(m * heads * hd), np.float32)
+        cos = np.empty((max_seq, half), np.float32)
+        sin = np.empty((max_seq, half), np.float32)
+        for p in range(max_seq):
+            for i in range(half):
+                a = p * (1.0 / 1e7 ** ((2 * i) / rot))
+                cos[p, i], sin[p, i] = np.float32(np.cos(a)), np.float32(np.sin(a))
+        xv = x.astype(np.float64).reshape(m, heads, hd)
+        want = xv.copy()
+        for r in range(m):
+            c, s_ = cos[pos + r].astype(np.float64), sin[pos + r].astype(np.float64)
+            lo, hi = xv[r, :, :half], xv[r, :, half:rot]
+            want[r, :, :half] = lo * c - hi * s_
+            want[r, :, half:rot] = hi * c + lo * s_
+        cases.append({"cite": "crates/thuban_backend/tests/kernels.rs:1200-1263", "m": m, "heads": heads,
+                      "head_dim": hd, "rot": rot, "pos": [pos + r for r in range(m)], "seed": seed,
+                      "x": x.tolist(), "cos": cos.reshape(-1).tolist(), "sin": sin.reshape(-1).tolist(),
+                      "expect": want.reshape(-1).tolist(), "rel": 1e-5, "abs": 1e-6})
+    inv1 = 1.0 / 10000.0 ** (2.0 / 4.0)
+    c0, s0 = np.float32(np.cos(1.0)), np.float32(np.sin(1.0))
+    c1, s1 = np.float32(np.cos(inv1)), np.float32(np.sin(inv1))
+    f = np.float32
+    want = [f(1) * c0 - f(3) * s0, f(2) * c1 - f(4) * s1, f(3) * c0 + f(1) * s0, f(4) * c1 + f(2) * s1]
+    cases.append({"cite": "crates/thuban_backend/tests/kernels.rs:1410-1436", "m": 1, "heads": 1, "head_dim": 4,
+                  "rot": 4, "pos": [1], "x": [1.0, 2.0, 3.0, 4.0], "cos": [0.0, 0.0, float(c0), float(c1)],
+                  "sin": [0.0, 0.0, float(s0), float(s1)], "expect": [float(w) for w in want], "rel": 0.0,
+                  "abs": 1e-6})
+    return cases
+
+
 def main():
     out = {
+        "rope_cases.json": rope_cases(),
         "codec_cases.json": codec_cases(),
         "arena_cases.json": arena_cases(),
         "kv_store_cases.json": kv_store_cases(),

@@ -229,3 +229,79 @@ def test_gather_and_block_copy_closed_form(orc):
     L.block_copy([[2, 5, 3]])
     assert np.array_equal(L.k[:, 20:23], before[:, 8:11])
     assert np.array_equal(L.k[:, 23], before[:, 23])
+
+
+# ------------------------------------------------------------------ rope
+def _tables(max_pos, rot, theta=10000.0):
+    half = rot // 2
+    inv = 1.0 / theta ** (2.0 * np.arange(half) / rot)
+    a = np.arange(max_pos)[:, None] * inv[None, :]
+    return np.cos(a).astype(np.float32), np.sin(a).astype(np.float32)
+
+
+def test_rope_reference_cases(orc, golden):
+    """rope_case and anchor_rope of the reference's kernel tests, with the
+    reference's tolerance (kernels.rs:132-147: |got - want| <= rel |want| + abs)."""
+    for case in golden("rope_cases.json"):
+        m, heads, hd, rot = case["m"], case["heads"], case["head_dim"], case["rot"]
+        half = rot // 2
+        x = np.array(case["x"], np.float32).reshape(m, heads, hd)
+        cos = np.array(case["cos"], np.float32).reshape(-1, half)
+        sin = np.array(case["sin"], np.float32).reshape(-1, half)
+        got = orc.rope_rows(x, case["pos"], rot, cos, sin).reshape(-1).astype(np.float64)
+        want = np.array(case["expect"], np.float64)
+        assert np.all(np.abs(got - want) <= case["rel"] * np.abs(want) + case["abs"]), case["cite"]
+
+
+def test_rope_closed_forms(orc):
+    """Position 0 is the identity; dims >= rot pass through bit for bit; each
+    rotated pair keeps its norm; dot products of rotated vectors depend only
+    on the position difference (the defining property of RoPE)."""
+    rng = np.random.default_rng(3)
+    hd, rot, heads = 64, 32, 3
+    cos, sin = _tables(40, rot)
+    x = rng.standard_normal((4, heads, hd)).astype(np.float32)
+    same = orc.rope_rows(x, [0, 0, 0, 0], rot, cos, sin)
+    assert np.array_equal(same, x)
+    y = orc.rope_rows(x, [5, 9, 17, 33], rot, cos, sin)
+    assert np.array_equal(y[..., rot:], x[..., rot:])
+    half = rot // 2
+    n_in = x[..., :half].astype(np.float64) ** 2 + x[..., half:rot].astype(np.float64) ** 2
+    n_out = y[..., :half].astype(np.float64) ** 2 + y[..., half:rot].astype(np.float64) ** 2
+    assert np.allclose(n_out, n_in, rtol=1e-5, atol=1e-6)
+    q = rng.standard_normal((1, 1, hd)).astype(np.float32)
+    k = rng.standard_normal((1, 1, hd)).astype(np.float32)
+    dots = []
+    for a, b in [(7, 3), (11, 7), (30, 26)]:
+        qa = orc.rope_rows(q, [a], rot, cos, sin).astype(np.float64)
+        kb = orc.rope_rows(k, [b], rot, cos, sin).astype(np.float64)
+        dots.append(float(np.sum(qa * kb)))
+    assert max(dots) - min(dots) < 1e-4 * (1 + abs(dots[0]))
+    # a plausible slip (partner from the wrong half) breaks the property
+    assert not np.allclose(y[..., :half], x[..., :half] * cos[[5, 9, 17, 33]][:, None, :]
+                           + x[..., half:rot] * sin[[5, 9, 17, 33]][:, None, :], atol=1e-3)
+
+
+def test_rope_rmsnorm_matches_double(orc):
+    """norm.wgsl MODE 4: y = x / sqrt(mean(x^2) + eps) * w, then the rotation;
+    against a double-precision evaluation."""
+    rng = np.random.default_rng(4)
+    hd, rot, eps = 128, 64, 1e-6
+    cos, sin = _tables(16, rot)
+    x = (rng.standard_normal((2, 4, hd)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    got = orc.rope_rows(x, [3, 12], rot, cos, sin, w=w, eps=eps).astype(np.float64)
+    xd = x.astype(np.float64)
+    t = xd / np.sqrt(np.mean(xd * xd, axis=-1, keepdims=True) + eps) * w.astype(np.float64)
+    half = rot // 2
+    want = t.copy()
+    for r, p in enumerate([3, 12]):
+        c, s = cos[p].astype(np.float64), sin[p].astype(np.float64)
+        want[r, :, :half] = t[r, :, :half] * c - t[r, :, half:rot] * s
+        want[r, :, half:rot] = t[r, :, half:rot] * c + t[r, :, :half] * s
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+    # no rotation (rot 0) leaves only the norm
+    only = orc.rope_rows(x, [3, 12], 0, cos, sin, w=w, eps=eps).astype(np.float64)
+    assert np.allclose(only, t, rtol=1e-6, atol=1e-7)
+    with pytest.raises(ValueError):
+        orc.rope_rows(x, [3, 16], rot, cos, sin)  # position outside the tables
