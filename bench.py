@@ -183,6 +183,47 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
                                              f"{pool.layers} layers x K,V x {nkv} heads")}
 
 
+def time_rope_step(torch, ops, pool, rows, positions, seqs, q, k_new, v_new, L, B, nq, hd, scale, steps=5):
+    """The per-layer step with rotary embedding (Llama-3: theta 500000,
+    rot = head_dim) two ways: the reference's four launches (rope q, rope k,
+    kv_store, attn; transformer/forward.rs:265-336) and thb_attn_append_rope
+    (one launch).  Copies of q and k are rotated, so the main workload's
+    buffers stay as they were.  Events around `steps` passes over the
+    layers; returns us per layer for each."""
+    from flint_amd.rope import Rope, kv_store_attn_rope, rope_rows
+
+    ctx = max(positions) + 1
+    rope = Rope.from_theta(ctx, hd, 500000.0)
+    qr, kr = q.clone(), k_new.clone()
+    y = torch.empty_like(q[0])
+    spec = ops.AttnSpec(q_heads=nq, window=0, scale=scale, m=B, causal=True, seq=None, args=rows)
+    nkv = k_new.shape[2]
+
+    def unfused():
+        for layer in range(L):
+            rope_rows(qr[layer], nq, rope, rows, B)
+            rope_rows(kr[layer], nkv, rope, rows, B)
+            ops.kv_store(kr[layer], v_new[layer], pool, layer, B, rows)
+            ops.attn(qr[layer], pool, layer, y, spec)
+
+    def fused():
+        for layer in range(L):
+            kv_store_attn_rope(k_new[layer], v_new[layer], q[layer], pool, layer, y, spec, rope)
+
+    out = {}
+    for name, fn in (("unfused", unfused), ("fused", fused)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) / (steps * L) * 1e3
+    return out
+
+
 def cpu_baseline(torch, pool, q0, y0, cfg, scale, seconds):
     """Times the oracle on layer 0 of the workload (bounded sample)."""
     import numpy as np
@@ -485,6 +526,11 @@ def main():
     append_us = time_append_graph(torch, ops, pool, rows, k_new[1 % L], v_new[1 % L], 1 % L, B)
     log(f"step {ms_step:.3f} ms (host wall {wall / args.steps * 1e3:.3f} ms); fused append+attention "
         f"{attn_us:.1f} us/launch; standalone append {append_us} us/launch")
+    rope_us = time_rope_step(torch, ops, pool, rows, positions, seqs, q, k_new, v_new, L, B, nq, hd, scale)
+    step()  # re-append the unrotated keys: the pool and y agree again for the CPU baseline
+    torch.cuda.synchronize()
+    log(f"rope step: reference-shaped 4 launches {rope_us['unfused']:.1f} us/layer, "
+        f"fused {rope_us['fused']:.1f} us/layer")
 
     kv_bytes = B * nkv * ctx * hd * 2 * 2
     qo_bytes = 2 * B * nq * hd * 2
@@ -528,6 +574,11 @@ def main():
                      "algorithmic_bytes": fused_bytes, "launches_timed": len(timed) * per_run},
         "cpu_baseline": None,
     }
+    out["rope"] = {"fused_us_per_layer": round(rope_us["fused"], 2),
+                   "unfused_us_per_layer": round(rope_us["unfused"], 2),
+                   "fused_GBps": round(fused_bytes / (rope_us["fused"] * 1e-6) / 1e9, 1),
+                   "note": "step with rotary embedding (theta 5e5, rot = head_dim): rope(q), rope(k), kv_store, "
+                           "attn as four launches vs thb_attn_append_rope as one"}
     moves = time_gather_copy(torch, ops, pool, 1 % L, B, ctx, nkv, hd, pl, dev)
     log("gather/scatter/copy: " + ", ".join(f"{k} {v['us_per_call']} us {v['GBps']} GB/s" for k, v in moves.items()))
     out.update(moves)
