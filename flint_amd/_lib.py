@@ -12,7 +12,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libthuban_hip.so")
 
-ABI_VERSION = 3  # THB_ABI_VERSION of include/thuban_hip.h
+ABI_VERSION = 4  # THB_ABI_VERSION of include/thuban_hip.h
 
 THB_OK = 0
 THB_ERR_MODEL = -1
@@ -98,6 +98,20 @@ class RopeC(ctypes.Structure):
     ]
 
 
+class AttnIoC(ctypes.Structure):
+    _fields_ = [
+        ("q_dev", ctypes.c_void_p),
+        ("q_stride", ctypes.c_uint32),
+        ("y_dev", ctypes.c_void_p),
+        ("gate_dev", ctypes.c_void_p),
+        ("gate_stride", ctypes.c_uint32),
+        ("k_src_dev", ctypes.c_void_p),
+        ("v_src_dev", ctypes.c_void_p),
+        ("src_dtype", ctypes.c_uint32),
+        ("rope", ctypes.POINTER(RopeC)),
+    ]
+
+
 # (name, restype, argtypes) for every symbol declared in include/thuban_hip.h.
 _vp, _u32, _u64, _i64, _sz, _int = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int64,
                                     ctypes.c_size_t, ctypes.c_int)
@@ -141,6 +155,7 @@ SIGNATURES = [
     ("thb_attn_rope", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), ctypes.POINTER(RopeC), _vp, _vp]),
     ("thb_attn_append_rope", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC),
                                     ctypes.POINTER(RopeC), _vp, _vp]),
+    ("thb_attn_step", _int, [_vp, _u32, ctypes.POINTER(AttnIoC), ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_block_copy", _int, [_vp, _pu32, _u32, _vp]),

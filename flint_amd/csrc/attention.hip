@@ -79,7 +79,10 @@ struct AttnArgs {
     uint32_t max_pages, page_shift, q_heads, nq_per_kv, head_dim, part_len, n_kvh;
     float qscale;  // scale * log2(e), or scale / softcap
     float cap2;    // softcap * log2(e), 0 = no soft-cap
-    uint32_t q_f16, y_f16;
+    uint32_t q_dt, y_dt;       // THB_DT_* of the query (and gate) and of the output
+    uint32_t q_stride;         // elements from one query head to the next
+    const void* gate;          // sigmoid gate of the output (q_dt), or null
+    uint32_t gate_stride;      // elements from one gate head to the next
     // Rotary position embedding (thb_attn_rope / thb_attn_append_rope): the
     // query is normalised and rotated as it is loaded, the fused append
     // rotates the key.  rope_on = 0: none.
@@ -88,12 +91,20 @@ struct AttnArgs {
     RopeDev qrope, krope;
 };
 
-// Loads 8 query elements (f16 or f32) of dims [d0, d0 + 8) as f32.
+// Loads 8 query elements (f32, f16 or bf16) of dims [d0, d0 + 8) as f32.
 __device__ inline void load_q8(const AttnArgs& a, uint64_t qbase, uint32_t d0, float (&x)[8]) {
-    if (a.q_f16) {
+    if (a.q_dt == THB_DT_F16) {
         const f16x8 w = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.q) + qbase + d0);
 #pragma unroll
         for (int e = 0; e < 8; e++) x[e] = static_cast<float>(w[e]);
+    } else if (a.q_dt == THB_DT_BF16) {
+        const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qbase + d0);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[2 * e] = __uint_as_float(ws[e] << 16);
+            x[2 * e + 1] = __uint_as_float(ws[e] & 0xffff0000u);
+        }
     } else {
         const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + qbase + d0);
         const f32x4 u0 = p[0], u1 = p[1];
@@ -196,6 +207,57 @@ struct Ops<false> {
     }
 };
 
+// One scalar of the sigmoid gate (same type as the query).
+__device__ inline float gate_at(const AttnArgs& a, uint64_t i) {
+    if (a.q_dt == THB_DT_F16) return static_cast<float>(static_cast<const _Float16*>(a.gate)[i]);
+    if (a.q_dt == THB_DT_BF16) return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(a.gate)[i]) << 16);
+    return static_cast<const float*>(a.gate)[i];
+}
+
+// f32 -> bf16 bits, round to nearest even (NaN stays NaN).
+__device__ inline uint16_t f32_to_bf16_rne(float x) {
+    const uint32_t b = __float_as_uint(x);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((b >> 16) | 0x40u);
+    return static_cast<uint16_t>((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+// Writes n (1 or 4) output values of (row, head) at dims [d, d + n): y =
+// o / l, times the sigmoid gate 1 / (1 + exp(-g)) when there is one
+// (sigmoid_mul.wgsl), in the output type.
+template <int N>
+__device__ inline void store_y(const AttnArgs& a, uint32_t row, uint32_t head, uint32_t d, const float (&v)[N]) {
+    float yv[N];
+#pragma unroll
+    for (int e = 0; e < N; e++) yv[e] = v[e];
+    if (a.gate) {
+        const uint64_t gi = (static_cast<uint64_t>(row) * a.q_heads + head) * a.gate_stride + d;
+#pragma unroll
+        for (int e = 0; e < N; e++) yv[e] = yv[e] / (1.0f + __expf(-gate_at(a, gi + e)));
+    }
+    const uint64_t yi = (static_cast<uint64_t>(row) * a.q_heads + head) * a.head_dim + d;
+    if constexpr (N == 4) {
+        if (a.y_dt == THB_DT_F32) {
+            *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + yi) = f32x4{yv[0], yv[1], yv[2], yv[3]};
+        } else if (a.y_dt == THB_DT_F16) {
+            f16x4 h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) h[e] = static_cast<_Float16>(yv[e]);
+            *reinterpret_cast<f16x4*>(static_cast<_Float16*>(a.y) + yi) = h;
+        } else {
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.y) + yi) =
+                u32x2{f32_to_bf16_rne(yv[0]) | (static_cast<uint32_t>(f32_to_bf16_rne(yv[1])) << 16),
+                      f32_to_bf16_rne(yv[2]) | (static_cast<uint32_t>(f32_to_bf16_rne(yv[3])) << 16)};
+        }
+    } else {
+        if (a.y_dt == THB_DT_F32)
+            static_cast<float*>(a.y)[yi] = yv[0];
+        else if (a.y_dt == THB_DT_F16)
+            static_cast<_Float16*>(a.y)[yi] = static_cast<_Float16>(yv[0]);
+        else
+            static_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_rne(yv[0]);
+    }
+}
+
 // Q^T operand of a lane: column (row, head), dims 32j + 8 a4 .. + 8 of k-step
 // j, split into high and low halves.  The raw query is split and the f32
 // scores are scaled afterwards, so the low half stays out of the f16
@@ -206,7 +268,7 @@ template <int KS, class O>
 __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_t head, uint32_t a4,
                               typename O::in8 (&qh)[KS], typename O::in8 (&ql)[KS]) {
     const uint32_t hd = a.head_dim;
-    const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
+    const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * a.q_stride;
     uint32_t pos = 0;
     float inv = 1.0f;
     if (a.rope_on) {
@@ -520,20 +582,13 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 
     if (n_parts == 1) {
         const float inv = 1.0f / l;
-        const uint64_t ybase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
 #pragma unroll
         for (int i = 0; i < MT; i++) {
             const uint32_t d = 16u * i + 4u * a4;
             if (d >= hd) continue;
             const f32x4 yv = o[i] * inv;
-            if (a.y_f16) {
-                f16x4 h;
-#pragma unroll
-                for (int e = 0; e < 4; e++) h[e] = static_cast<_Float16>(yv[e]);
-                *reinterpret_cast<f16x4*>(static_cast<_Float16*>(a.y) + ybase + d) = h;
-            } else {
-                *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + ybase + d) = yv;
-            }
+            const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
+            store_y<4>(a, row, head, d, v4);
         }
         return;
     }
@@ -583,13 +638,9 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
         const float* src = a.part_o + (base * kCols + c) * HD + d;
         float acc = 0.0f;
         for (uint32_t pi = 0; pi < n_parts; pi++) acc += s_w[pi * kCols + c] * src[pi * step];
-        const float yv = acc * s_inv[c];
+        const float yv[1] = {acc * s_inv[c]};
         const uint32_t rr = c / H, hh = c - rr * H;
-        const uint64_t yi = (static_cast<uint64_t>(r0 + rr) * a.q_heads + kvh * a.nq_per_kv + h0 + hh) * hd + d;
-        if (a.y_f16)
-            static_cast<_Float16*>(a.y)[yi] = static_cast<_Float16>(yv);
-        else
-            static_cast<float*>(a.y)[yi] = yv;
+        store_y<1>(a, r0 + rr, kvh * a.nq_per_kv + h0 + hh, d, yv);
     }
 }
 
@@ -801,20 +852,13 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
 
     if (n_parts == 1) {
         const float inv = 1.0f / l;
-        const uint64_t ybase = (static_cast<uint64_t>(row) * a.q_heads + head) * hd;
 #pragma unroll
         for (int i = 0; i < MT; i++) {
             const uint32_t d = 16u * i + 4u * a4;
             if (d >= hd) continue;
             const f32x4 yv = o[i] * inv;
-            if (a.y_f16) {
-                f16x4 h;
-#pragma unroll
-                for (int e = 0; e < 4; e++) h[e] = static_cast<_Float16>(yv[e]);
-                *reinterpret_cast<f16x4*>(static_cast<_Float16*>(a.y) + ybase + d) = h;
-            } else {
-                *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + ybase + d) = yv;
-            }
+            const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
+            store_y<4>(a, row, head, d, v4);
         }
         return;
     }
@@ -1111,12 +1155,6 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     return THB_OK;
 }
 
-struct AppendSrc {
-    const void* k;
-    const void* v;
-    uint32_t dtype;
-};
-
 int check_attn_call(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec& sp,
                     const thb_rows* rows) {
     if (layer >= pool->layers)
@@ -1126,8 +1164,8 @@ int check_attn_call(thb_pool* pool, uint32_t layer, const void* q, void* y, cons
     if (sp.q_heads == 0 || sp.q_heads % pool->kv_heads != 0)
         return fail(THB_ERR_CONFIG, "q_heads " + std::to_string(sp.q_heads) +
                                         " must be a positive multiple of kv_heads " + std::to_string(pool->kv_heads));
-    if (sp.q_dtype > THB_DT_F16 || sp.y_dtype > THB_DT_F16)
-        return fail(THB_ERR_INVALID, "q_dtype and y_dtype must be THB_DT_F32 or THB_DT_F16");
+    if (sp.q_dtype > THB_DT_BF16 || sp.y_dtype > THB_DT_BF16)
+        return fail(THB_ERR_INVALID, "q_dtype and y_dtype must be THB_DT_F32, THB_DT_F16 or THB_DT_BF16");
     if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u))
         return fail(THB_ERR_INVALID, "q and y must be 16-byte aligned");
     if (static_cast<uint64_t>(sp.row_off) + sp.m > rows->m)
@@ -1177,8 +1215,9 @@ int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint
 // Launches attention (and, when app is set, the fused append) for a plan.
 // With rope set, the query is rotated as it is loaded (and the fused append
 // rotates the key); meta is the row meta of the call's first row.
-void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec& sp, const AttnPlan& plan,
-                 const AppendSrc* app, const thb_rope* rope, const uint32_t* meta, hipStream_t s) {
+void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const thb_attn_spec& sp, const AttnPlan& plan,
+                 bool fused_append, const uint32_t* meta, hipStream_t s) {
+    const thb_rope* rope = io.rope;
     const uint32_t hd = pool->geom[layer].head_dim;
     const uint32_t hd_t = plan.hd_t;
     float* part_o = nullptr;
@@ -1193,8 +1232,8 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
     const uint32_t* blob = static_cast<const uint32_t*>(plan.dev.get());
     const LayerGeom& g = pool->geom[layer];
     AttnArgs a;
-    a.q = q;
-    a.y = y;
+    a.q = io.q_dev;
+    a.y = io.y_dev;
     a.groups = blob;
     a.items = blob + static_cast<size_t>(plan.n_groups) * kGroupWords;
     a.ranges = a.items + plan.n_items;
@@ -1203,9 +1242,9 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
     a.table = pool->table_dev;
     a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
     a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
-    a.k_src = app ? app->k : nullptr;
-    a.v_src = app ? app->v : nullptr;
-    a.src_dtype = app ? app->dtype : 0u;
+    a.k_src = fused_append ? io.k_src_dev : nullptr;
+    a.v_src = fused_append ? io.v_src_dev : nullptr;
+    a.src_dtype = fused_append ? io.src_dtype : 0u;
     a.part_o = part_o;
     a.part_ml = part_ml;
     a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
@@ -1224,8 +1263,11 @@ void launch_plan(thb_pool* pool, uint32_t layer, const void* q, void* y, const t
         a.qscale = sp.scale * log2e;
         a.cap2 = 0.0f;
     }
-    a.q_f16 = sp.q_dtype == THB_DT_F16;
-    a.y_f16 = sp.y_dtype == THB_DT_F16;
+    a.q_dt = sp.q_dtype;
+    a.y_dt = sp.y_dtype;
+    a.q_stride = io.q_stride ? io.q_stride : hd;
+    a.gate = io.gate_dev;
+    a.gate_stride = io.gate_stride ? io.gate_stride : hd;
     a.rope_on = rope != nullptr;
     a.meta = meta;
     a.qrope = rope ? rope_dev(*rope, true) : RopeDev{};
@@ -1267,58 +1309,58 @@ using namespace thb;
 
 namespace {
 
-int attn_impl(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec, const thb_rope* rope,
-              const thb_rows* rows, void* stream) {
-    if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
-    if (spec->m == 0) return layer < pool->layers ? THB_OK : check_attn_call(pool, layer, q, y, *spec, rows);
-    if (int rc = check_attn_call(pool, layer, q, y, *spec, rows)) return rc;
+// Every attention entry point: optional append (fused into the launch where
+// the rows allow it), rotary embedding, query stride and output gate.
+int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_attn_spec* spec, const thb_rows* rows,
+              void* stream) {
+    if (!pool || !io || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, io, spec or rows");
+    if (spec->m == 0)
+        return layer < pool->layers ? THB_OK : check_attn_call(pool, layer, io->q_dev, io->y_dev, *spec, rows);
+    if (int rc = check_attn_call(pool, layer, io->q_dev, io->y_dev, *spec, rows)) return rc;
+    const uint32_t hd = pool->geom[layer].head_dim;
+    const uint32_t qes = spec->q_dtype == THB_DT_F32 ? 4u : 2u;
+    if (io->q_stride && (io->q_stride < hd || (io->q_stride * qes) % 16 != 0))
+        return fail(THB_ERR_INVALID, "q_stride " + std::to_string(io->q_stride) +
+                                         " must be 0 or at least head_dim, and a multiple of 16 bytes");
+    if (io->gate_dev && io->gate_stride && io->gate_stride < hd)
+        return fail(THB_ERR_INVALID, "gate_stride " + std::to_string(io->gate_stride) + " below head_dim");
+    const thb_rope* rope = io->rope;
     if (rope)
-        if (int rc = check_rope(rope, pool->geom[layer].head_dim, rows, spec->row_off, spec->m)) return rc;
-    return guarded([&]() -> int {
-        hipStream_t s = as_stream(stream);
-        pool_flush(pool, s);
-        AttnPlan* plan = nullptr;
-        if (int rc = get_plan(pool, rows, *spec, pool->geom[layer].head_dim, s, &plan)) return rc;
-        launch_plan(pool, layer, q, y, *spec, *plan, nullptr, rope, rows->dev + 8 * static_cast<size_t>(spec->row_off),
-                    s);
-        return THB_OK;
-    });
-}
-
-int attn_append_impl(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src, uint32_t src_dtype,
-                     const void* q, void* y, const thb_attn_spec* spec, const thb_rope* rope, const thb_rows* rows,
-                     void* stream) {
-    if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
-    if (spec->m == 0) return layer < pool->layers ? THB_OK : check_attn_call(pool, layer, q, y, *spec, rows);
-    if (int rc = check_attn_call(pool, layer, q, y, *spec, rows)) return rc;
-    if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
-    if (src_dtype > THB_DT_BF16) return fail(THB_ERR_INVALID, "unknown src_dtype " + std::to_string(src_dtype));
-    if (rope && src_dtype == THB_DT_BF16)
-        return fail(THB_ERR_INVALID, "rotary append takes f32 or f16 sources (src_dtype 2)");
-    if ((reinterpret_cast<uintptr_t>(k_src) & 15u) || (reinterpret_cast<uintptr_t>(v_src) & 15u))
-        return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
-    if (rope)
-        if (int rc = check_rope(rope, pool->geom[layer].head_dim, rows, spec->row_off, spec->m)) return rc;
-    // Pages must cover every appended token (thb_kv_store's check; the
-    // append takes each row's sequence from the row meta, kv_store.wgsl:39).
-    const Arena& arena = pool->arena.a;
-    for (uint32_t r = spec->row_off; r < spec->row_off + spec->m; r++) {
-        const uint32_t pos = rows->host[8 * r];
-        const uint32_t seq = rows->host[8 * r + 1];
-        if (seq >= arena.seqs())
-            return fail(THB_ERR_INVALID, "sequence " + std::to_string(seq) + " out of range (" +
-                                             std::to_string(arena.seqs()) + " sequences)");
-        if (pos == 0xFFFFFFFFu || !arena.covers(seq, pos + 1))
-            return fail(THB_ERR_MODEL, "pages must cover the chunk: sequence " + std::to_string(seq) + " holds " +
-                                           std::to_string(arena.table_of(seq).size() * arena.page_len()) +
-                                           " slots, needs " + std::to_string(static_cast<uint64_t>(pos) + 1));
+        if (int rc = check_rope(rope, hd, rows, spec->row_off, spec->m)) return rc;
+    const bool append = io->k_src_dev || io->v_src_dev;
+    if (append) {
+        if (!io->k_src_dev || !io->v_src_dev) return fail(THB_ERR_INVALID, "null source buffer");
+        if (io->src_dtype > THB_DT_BF16)
+            return fail(THB_ERR_INVALID, "unknown src_dtype " + std::to_string(io->src_dtype));
+        if (rope && io->src_dtype == THB_DT_BF16)
+            return fail(THB_ERR_INVALID, "rotary append takes f32 or f16 sources (src_dtype 2)");
+        if ((reinterpret_cast<uintptr_t>(io->k_src_dev) & 15u) || (reinterpret_cast<uintptr_t>(io->v_src_dev) & 15u))
+            return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
+        // Pages must cover every appended token (thb_kv_store's check; the
+        // append takes each row's sequence from the row meta, kv_store.wgsl:39).
+        const Arena& arena = pool->arena.a;
+        for (uint32_t r = spec->row_off; r < spec->row_off + spec->m; r++) {
+            const uint32_t pos = rows->host[8 * r];
+            const uint32_t seq = rows->host[8 * r + 1];
+            if (seq >= arena.seqs())
+                return fail(THB_ERR_INVALID, "sequence " + std::to_string(seq) + " out of range (" +
+                                                 std::to_string(arena.seqs()) + " sequences)");
+            if (pos == 0xFFFFFFFFu || !arena.covers(seq, pos + 1))
+                return fail(THB_ERR_MODEL, "pages must cover the chunk: sequence " + std::to_string(seq) +
+                                               " holds " + std::to_string(arena.table_of(seq).size() * arena.page_len()) +
+                                               " slots, needs " + std::to_string(static_cast<uint64_t>(pos) + 1));
+        }
     }
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
         AttnPlan* plan = nullptr;
-        if (int rc = get_plan(pool, rows, *spec, pool->geom[layer].head_dim, s, &plan)) return rc;
+        if (int rc = get_plan(pool, rows, *spec, hd, s, &plan)) return rc;
         const uint32_t* meta = rows->dev + 8 * static_cast<size_t>(spec->row_off);
+        if (!append) {
+            launch_plan(pool, layer, *io, *spec, *plan, false, meta, s);
+            return THB_OK;
+        }
         // The row meta's sequence must be the one the append uses: a fixed
         // AttnSpec.seq that differs from the rows' own seq is not fused.
         bool fuse = plan->fusable;
@@ -1326,41 +1368,64 @@ int attn_append_impl(thb_pool* pool, uint32_t layer, const void* k_src, const vo
             for (uint32_t r = spec->row_off; r < spec->row_off + spec->m && fuse; r++)
                 fuse = rows->host[8 * r + 1] == spec->seq;
         if (fuse) {
-            const AppendSrc app{k_src, v_src, src_dtype};
-            launch_plan(pool, layer, q, y, *spec, *plan, &app, rope, meta, s);
+            launch_plan(pool, layer, *io, *spec, *plan, true, meta, s);
             return THB_OK;
         }
-        const int rc = rope ? thb_kv_store_rope(pool, layer, k_src, v_src, src_dtype, rope, rows, spec->row_off,
-                                                spec->m, stream)
-                            : thb_kv_store(pool, layer, k_src, v_src, src_dtype, rows, spec->row_off, spec->m, stream);
+        const int rc = rope ? thb_kv_store_rope(pool, layer, io->k_src_dev, io->v_src_dev, io->src_dtype, rope, rows,
+                                                spec->row_off, spec->m, stream)
+                            : thb_kv_store(pool, layer, io->k_src_dev, io->v_src_dev, io->src_dtype, rows,
+                                           spec->row_off, spec->m, stream);
         if (rc) return rc;
-        launch_plan(pool, layer, q, y, *spec, *plan, nullptr, rope, meta, s);
+        launch_plan(pool, layer, *io, *spec, *plan, false, meta, s);
         return THB_OK;
     });
+}
+
+thb_attn_io make_io(const void* q, void* y, const void* k_src, const void* v_src, uint32_t src_dtype,
+                    const thb_rope* rope) {
+    thb_attn_io io{};
+    io.q_dev = q;
+    io.y_dev = y;
+    io.k_src_dev = k_src;
+    io.v_src_dev = v_src;
+    io.src_dtype = src_dtype;
+    io.rope = rope;
+    return io;
 }
 
 }  // namespace
 
 extern "C" int thb_attn(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec,
                         const thb_rows* rows, void* stream) {
-    return attn_impl(pool, layer, q, y, spec, nullptr, rows, stream);
+    const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
+    return step_impl(pool, layer, &io, spec, rows, stream);
 }
 
 extern "C" int thb_attn_rope(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec,
                              const thb_rope* rope, const thb_rows* rows, void* stream) {
     if (!rope) return fail(THB_ERR_INVALID, "null rope");
-    return attn_impl(pool, layer, q, y, spec, rope, rows, stream);
+    const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, rope);
+    return step_impl(pool, layer, &io, spec, rows, stream);
 }
 
 extern "C" int thb_attn_append(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src,
                                uint32_t src_dtype, const void* q, void* y, const thb_attn_spec* spec,
                                const thb_rows* rows, void* stream) {
-    return attn_append_impl(pool, layer, k_src, v_src, src_dtype, q, y, spec, nullptr, rows, stream);
+    if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
+    const thb_attn_io io = make_io(q, y, k_src, v_src, src_dtype, nullptr);
+    return step_impl(pool, layer, &io, spec, rows, stream);
 }
 
 extern "C" int thb_attn_append_rope(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src,
                                     uint32_t src_dtype, const void* q, void* y, const thb_attn_spec* spec,
                                     const thb_rope* rope, const thb_rows* rows, void* stream) {
     if (!rope) return fail(THB_ERR_INVALID, "null rope");
-    return attn_append_impl(pool, layer, k_src, v_src, src_dtype, q, y, spec, rope, rows, stream);
+    if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
+    const thb_attn_io io = make_io(q, y, k_src, v_src, src_dtype, rope);
+    return step_impl(pool, layer, &io, spec, rows, stream);
+}
+
+extern "C" int thb_attn_step(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_attn_spec* spec,
+                             const thb_rows* rows, void* stream) {
+    return step_impl(pool, layer, io, spec, rows, stream);
 }

@@ -84,6 +84,27 @@ def kv_store_attn(k_src, v_src, q, kv: KvPool, layer: int, y, spec: AttnSpec, st
                                 spec.args.handle, _stream_ptr(stream)))
 
 
+def attn_step(kv: KvPool, layer: int, spec: AttnSpec, q, y, q_stride: int = 0, gate=None, gate_stride: int = 0,
+              k_src=None, v_src=None, rope=None, stream=None) -> None:
+    """thb_attn_step: attention with every extension of the C ABI's
+    thb_attn_io.  q heads are q_stride elements apart (0 = head_dim; pass
+    2 * head_dim and a view of a fused q|gate projection); gate, when given,
+    multiplies the output by sigmoid(gate) (qwen35/layers.rs:231-238); k_src
+    and v_src are appended first; rope (flint_amd.rope.Rope) rotates q and k.
+    q, gate and y are device tensors or raw device addresses."""
+    c = _spec_c(spec, q, y)
+    io = _lib.AttnIoC()
+    io.q_dev, io.y_dev, io.q_stride = _ptr(q), _ptr(y), q_stride
+    io.gate_dev = _ptr(gate) if gate is not None else None
+    io.gate_stride = gate_stride
+    if k_src is not None:
+        io.k_src_dev, io.v_src_dev = _ptr(k_src), _ptr(v_src)
+        io.src_dtype = _dtype_code(getattr(k_src, "dtype", None))
+    io.rope = ctypes.pointer(rope._c) if rope is not None else None
+    check(lib().thb_attn_step(kv.handle, layer, ctypes.byref(io), ctypes.byref(c), spec.args.handle,
+                              _stream_ptr(stream)))
+
+
 def default_scale(head_dim: int) -> float:
     """forward.rs:328: attn_scale or 1/sqrt(head_dim)."""
     return 1.0 / math.sqrt(head_dim)
@@ -103,5 +124,5 @@ def block_copy(kv: KvPool, triples: Sequence[Sequence[int]], stream=None) -> Non
                                _stream_ptr(stream)))
 
 
-__all__ = ["AttnSpec", "ThubanError", "attn", "block_copy", "check_head_dim", "default_scale", "kv_gather",
+__all__ = ["AttnSpec", "ThubanError", "attn", "attn_step", "block_copy", "check_head_dim", "default_scale", "kv_gather",
            "kv_scatter", "kv_store", "kv_store_attn"]

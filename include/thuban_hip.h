@@ -54,7 +54,7 @@ extern "C" {
 const char* thb_last_error(void);
 /* ABI revision of this header. */
 uint32_t thb_abi_version(void);
-#define THB_ABI_VERSION 3u
+#define THB_ABI_VERSION 4u
 
 /* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90):
  * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]".  This backend also needs
@@ -211,8 +211,9 @@ typedef struct thb_attn_spec {
     uint32_t row_off;  /* first row in the row meta (the reference binds a
                           slice at row_off * 32 bytes, forward.rs:332) */
     float softcap;     /* extension: 0 = off, else s = cap * tanh(s / cap) */
-    uint32_t q_dtype;  /* THB_DT_F32 (reference) or THB_DT_F16 */
-    uint32_t y_dtype;  /* THB_DT_F32 (reference) or THB_DT_F16 */
+    uint32_t q_dtype;  /* THB_DT_F32 (reference), THB_DT_F16 or THB_DT_BF16 */
+    uint32_t y_dtype;  /* THB_DT_F32 (reference), THB_DT_F16 or THB_DT_BF16 (round to
+                          nearest even; the o_proj GEMM's operand type) */
 } thb_attn_spec;
 
 /* ops::attn (ops/attn.rs:18-51) / attn.wgsl:53-365.  q, y: [m, q_heads,
@@ -288,6 +289,33 @@ int thb_attn_rope(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev
 int thb_attn_append_rope(thb_pool* pool, uint32_t layer, const void* k_src_dev, const void* v_src_dev,
                          uint32_t src_dtype, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
                          const thb_rope* rope, const thb_rows* rows, void* stream);
+
+/* ------------------------------------------------------ the whole step */
+
+/* Inputs and outputs of one attention call beyond thb_attn_spec.  Only q_dev
+ * and y_dev are required; the other members extend the call. */
+typedef struct thb_attn_io {
+    const void* q_dev;     /* head h of row r at (r * q_heads + h) * q_stride elements (spec->q_dtype) */
+    uint32_t q_stride;     /* 0 = head_dim.  2 * head_dim reads the query straight out of a fused
+                              q|gate projection, as split_q_gate.wgsl lays it out (qwen35/layers.rs
+                              :138-149) */
+    void* y_dev;           /* [m, q_heads, head_dim] of spec->y_dtype */
+    const void* gate_dev;  /* output gate, or NULL: y = attention * 1 / (1 + exp(-gate))
+                              (sigmoid_mul.wgsl, qwen35/layers.rs:231-238), in spec->q_dtype */
+    uint32_t gate_stride;  /* 0 = head_dim; elements from one gate head to the next */
+    const void* k_src_dev; /* rows appended first, as thb_attn_append, or NULL */
+    const void* v_src_dev;
+    uint32_t src_dtype;
+    const thb_rope* rope;  /* rotary embedding of q (and of the appended k), or NULL */
+} thb_attn_io;
+
+/* thb_attn with every extension of io: the layer's attention from the
+ * projected q|gate and k, v to the gated output the o_proj GEMM consumes
+ * (transformer/forward.rs:184-351, qwen35/layers.rs:138-238), in one launch
+ * at decode.  thb_attn, thb_attn_rope, thb_attn_append and
+ * thb_attn_append_rope are this call with some members NULL. */
+int thb_attn_step(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_attn_spec* spec,
+                  const thb_rows* rows, void* stream);
 
 /* No reference counterpart.  Copies tokens [t0, t0 + n) of seq, layer
  * `layer`, into contiguous k_dst/v_dst [kv_heads, n, head_dim] in the KV type

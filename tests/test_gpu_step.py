@@ -1,0 +1,143 @@
+"""GPU parity of thb_attn_step, the whole attention step of a layer: the
+query read straight out of a fused q|gate projection (split_q_gate.wgsl
+layout), RMSNorm + rotary embedding, the append, attention and the sigmoid
+output gate of Qwen3.5 (qwen35/layers.rs:138-238), plus the bf16 query and
+output types the o_proj GEMM consumes.  Against the CPU oracle (exact
+softmax) within 2e-3; type conversions bit-exact."""
+
+import math
+import random
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import fill, make_pool, oracle_layer, say, scattered_alloc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+
+
+STEP_CASES = [
+    # name, nq, nkv, hd, rot, norm, rows per seq, lens
+    ("qwen35-decode", 16, 2, 256, 64, True, 1, [700, 1500, 33]),
+    ("qwen35-long-merge", 16, 2, 256, 64, True, 1, [9000, 50]),
+    ("qwen35-prefill-chunk", 8, 2, 128, 32, True, 48, [300, 20]),
+    ("gated-no-rope", 32, 8, 128, 0, False, 1, [1000, 64, 4100]),
+]
+
+
+@pytest.mark.parametrize("case", STEP_CASES, ids=[c[0] for c in STEP_CASES])
+def test_attn_step_qgate(torch_cuda, case):
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+    from flint_amd.rope import Rope, rope_tables
+
+    name, nq, nkv, hd, rot, norm, rps, lens = case
+    say("attn step", name)
+    seed = zlib.crc32(name.encode())
+    budget = [n + rps for n in lens]
+    pool = make_pool(budget, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype="f16", extra_pages=3)
+    scattered_alloc(pool, budget, random.Random(seed), 16)
+    rows = RowMeta(512)
+    fill(torch, pool, rows, lens, seed=5)
+    positions, seqs = [], []
+    for s, n in enumerate(lens):
+        positions += list(range(n, n + rps))
+        seqs += [s] * rps
+    m = len(seqs)
+    rng = np.random.default_rng(seed)
+    rope = cos = sin = qn = kn = None
+    if rot:
+        cos, sin = rope_tables(max(budget) + 1, rot, rot, 1e7)
+        qn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+        kn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+        rope = Rope(cos, sin, rot, q_norm=qn, k_norm=kn, eps=1e-6)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed & 0xFFFF)
+    qg = torch.randn(m, nq, 2 * hd, device="cuda", generator=g)  # [q | gate] per head
+    k_new = torch.randn(m, nkv, hd, device="cuda", generator=g)
+    v_new = torch.randn(m, nkv, hd, device="cuda", generator=g)
+    rows.write(positions, seqs, m)
+    # oracle: append (rotated keys), exact attention of the rotated queries, gate
+    ref = oracle_layer(torch, pool)
+    kr = k_new.cpu().numpy()
+    q = np.ascontiguousarray(qg[..., :hd].cpu().numpy())
+    gate = qg[..., hd:].cpu().numpy()
+    if rot:
+        kr = oracle.rope_rows(kr, positions, rot, cos, sin, w=kn)
+        q = oracle.rope_rows(q, positions, rot, cos, sin, w=qn)
+    ref.kv_store(np.ascontiguousarray(kr), v_new.cpu().numpy(), oracle.row_meta(positions, seqs), m, oracle.SRC_F32)
+    want = ref.attn(q, oracle.row_meta(positions, seqs), m, nq, 1 / math.sqrt(hd)) * _sigmoid(gate)
+    y = torch.empty(m, nq, hd, device="cuda")
+    spec = ops.AttnSpec(q_heads=nq, window=0, scale=1 / math.sqrt(hd), m=m, causal=True, seq=None, args=rows)
+    ops.attn_step(pool, 0, spec, qg, y, q_stride=2 * hd, gate=qg[..., hd:], gate_stride=2 * hd, k_src=k_new,
+                  v_src=v_new, rope=rope)
+    torch.cuda.synchronize()
+    k2, v2 = pool.read_layer(0)
+    assert np.array_equal(k2, ref.k) and np.array_equal(v2, ref.v), name
+    err = float(np.max(np.abs(y.cpu().numpy() - want)))
+    say("attn step", name, "max abs err", err)
+    assert err <= TOL, name
+
+
+def test_bf16_and_f16_io_are_exact_conversions(torch_cuda):
+    """A bf16 query is widened exactly, and f16 / bf16 outputs are the f32
+    output rounded to nearest even: bit-identical to converting the f32 run."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    say("bf16/f16 io")
+    lens = [5000, 700, 90]
+    pool = make_pool(lens, kv_heads=4, head_dim=128, page_len=16, kv_dtype="bf16", extra_pages=2)
+    scattered_alloc(pool, lens, random.Random(2), 16)
+    rows = RowMeta(64)
+    fill(torch, pool, rows, lens, seed=9)
+    positions = [n - 1 for n in lens]
+    seqs = list(range(len(lens)))
+    rows.write(positions, seqs, len(lens))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    qb = torch.randn(len(lens), 16, 128, device="cuda", generator=g).to(torch.bfloat16)
+    spec = ops.AttnSpec(q_heads=16, window=0, scale=1 / math.sqrt(128), m=len(lens), causal=True, seq=None,
+                        args=rows)
+    outs = {}
+    for name, qin, ydt in [("f32", qb.float(), torch.float32), ("bf16q", qb, torch.float32),
+                           ("bf16y", qb, torch.bfloat16), ("f16y", qb, torch.float16)]:
+        y = torch.empty(len(lens), 16, 128, device="cuda", dtype=ydt)
+        ops.attn(qin, pool, 0, y, spec)
+        outs[name] = y
+    torch.cuda.synchronize()
+    assert torch.equal(outs["f32"], outs["bf16q"])
+    assert torch.equal(outs["bf16y"], outs["f32"].to(torch.bfloat16))
+    assert torch.equal(outs["f16y"], outs["f32"].to(torch.float16))
+
+
+def test_attn_step_errors(torch_cuda):
+    torch = torch_cuda
+    from flint_amd import ThubanError, ops
+    from flint_amd.pool import RowMeta
+
+    pool = make_pool([40], kv_heads=2, head_dim=64, page_len=16)
+    pool.alloc(0, 0, 40)
+    rows = RowMeta(4)
+    rows.write([20], [0], 1)
+    q = torch.zeros(1, 4, 128, device="cuda")
+    y = torch.empty(1, 4, 64, device="cuda")
+    spec = ops.AttnSpec(q_heads=4, window=0, scale=0.125, m=1, causal=True, seq=None, args=rows)
+    with pytest.raises(ThubanError) as e:
+        ops.attn_step(pool, 0, spec, q, y, q_stride=32)  # below head_dim
+    assert "q_stride" in str(e.value)
+    with pytest.raises(ThubanError):
+        ops.attn_step(pool, 0, spec, q, y, q_stride=66)  # not a multiple of 16 bytes
+    ops.attn_step(pool, 0, spec, q, y, q_stride=128, gate=q[..., 64:], gate_stride=128)
+    torch.cuda.synchronize()
+    assert torch.allclose(y, torch.zeros_like(y))  # zero V: y = 0 whatever the gate
