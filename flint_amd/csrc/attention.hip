@@ -83,21 +83,26 @@ struct AttnArgs {
     uint32_t q_stride;         // elements from one query head to the next
     const void* gate;          // sigmoid gate of the output (q_dt), or null
     uint32_t gate_stride;      // elements from one gate head to the next
-    // Rotary position embedding (thb_attn_rope / thb_attn_append_rope): the
-    // query is normalised and rotated as it is loaded, the fused append
-    // rotates the key.  rope_on = 0: none.
+    // full = 1 selects the kernels with the extensions of thb_attn_io (query
+    // stride, gate, bf16 query/output, rope); the others take f32/f16 q and
+    // y only and are the lean path of the common call.
+    uint32_t full;
+    // Rotary position embedding (FULL kernels): the query is normalised and
+    // rotated as it is loaded, the fused append rotates the key.
     uint32_t rope_on;
     const uint32_t* meta;  // row meta of the call's rows (positions)
     RopeDev qrope, krope;
 };
 
-// Loads 8 query elements (f32, f16 or bf16) of dims [d0, d0 + 8) as f32.
+// Loads 8 query elements of dims [d0, d0 + 8) as f32: f32 or f16, and
+// bf16 in the FULL kernels.
+template <bool FULL>
 __device__ inline void load_q8(const AttnArgs& a, uint64_t qbase, uint32_t d0, float (&x)[8]) {
     if (a.q_dt == THB_DT_F16) {
         const f16x8 w = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.q) + qbase + d0);
 #pragma unroll
         for (int e = 0; e < 8; e++) x[e] = static_cast<float>(w[e]);
-    } else if (a.q_dt == THB_DT_BF16) {
+    } else if (FULL && a.q_dt == THB_DT_BF16) {
         const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qbase + d0);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -223,13 +228,14 @@ __device__ inline uint16_t f32_to_bf16_rne(float x) {
 
 // Writes n (1 or 4) output values of (row, head) at dims [d, d + n): y =
 // o / l, times the sigmoid gate 1 / (1 + exp(-g)) when there is one
-// (sigmoid_mul.wgsl), in the output type.
-template <int N>
+// (sigmoid_mul.wgsl), in the output type.  The gate and bf16 outputs exist
+// in the FULL kernels only.
+template <int N, bool FULL>
 __device__ inline void store_y(const AttnArgs& a, uint32_t row, uint32_t head, uint32_t d, const float (&v)[N]) {
     float yv[N];
 #pragma unroll
     for (int e = 0; e < N; e++) yv[e] = v[e];
-    if (a.gate) {
+    if (FULL && a.gate) {
         const uint64_t gi = (static_cast<uint64_t>(row) * a.q_heads + head) * a.gate_stride + d;
 #pragma unroll
         for (int e = 0; e < N; e++) yv[e] = yv[e] / (1.0f + __expf(-gate_at(a, gi + e)));
@@ -238,7 +244,7 @@ __device__ inline void store_y(const AttnArgs& a, uint32_t row, uint32_t head, u
     if constexpr (N == 4) {
         if (a.y_dt == THB_DT_F32) {
             *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + yi) = f32x4{yv[0], yv[1], yv[2], yv[3]};
-        } else if (a.y_dt == THB_DT_F16) {
+        } else if (!FULL || a.y_dt == THB_DT_F16) {
             f16x4 h;
 #pragma unroll
             for (int e = 0; e < 4; e++) h[e] = static_cast<_Float16>(yv[e]);
@@ -251,7 +257,7 @@ __device__ inline void store_y(const AttnArgs& a, uint32_t row, uint32_t head, u
     } else {
         if (a.y_dt == THB_DT_F32)
             static_cast<float*>(a.y)[yi] = yv[0];
-        else if (a.y_dt == THB_DT_F16)
+        else if (!FULL || a.y_dt == THB_DT_F16)
             static_cast<_Float16*>(a.y)[yi] = static_cast<_Float16>(yv[0]);
         else
             static_cast<uint16_t*>(a.y)[yi] = f32_to_bf16_rne(yv[0]);
@@ -261,17 +267,19 @@ __device__ inline void store_y(const AttnArgs& a, uint32_t row, uint32_t head, u
 // Q^T operand of a lane: column (row, head), dims 32j + 8 a4 .. + 8 of k-step
 // j, split into high and low halves.  The raw query is split and the f32
 // scores are scaled afterwards, so the low half stays out of the f16
-// subnormal range.  With rope on, the query head is first normalised
-// (q_norm; the four lanes of the column add their sums of squares) and
-// rotated at the row's position.  Every lane must call it (column sums).
-template <int KS, class O>
+// subnormal range.  In the FULL kernels: query heads q_stride apart and,
+// with rope on, the query head is first normalised (q_norm; the four lanes
+// of the column add their sums of squares) and rotated at the row's
+// position.  Every lane must call it (column sums).
+template <int KS, class O, bool FULL>
 __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_t head, uint32_t a4,
                               typename O::in8 (&qh)[KS], typename O::in8 (&ql)[KS]) {
     const uint32_t hd = a.head_dim;
-    const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * a.q_stride;
+    const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * (FULL ? a.q_stride : hd);
+    const bool rope = FULL && a.rope_on;
     uint32_t pos = 0;
     float inv = 1.0f;
-    if (a.rope_on) {
+    if (rope) {
         pos = con ? a.meta[8 * row] : 0u;
         if (a.qrope.w) {
             float ss = 0.0f;
@@ -280,7 +288,7 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
                 const uint32_t d0 = 32u * j + 8u * a4;
                 if (con && d0 < hd) {
                     float x[8];
-                    load_q8(a, qbase, d0, x);
+                    load_q8<FULL>(a, qbase, d0, x);
                     ss += sumsq8(x);
                 }
             }
@@ -292,13 +300,13 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
         const uint32_t d0 = 32u * j + 8u * a4;
         float x[8];
         if (con && d0 < hd) {
-            load_q8(a, qbase, d0, x);
-            if (a.rope_on) {
+            load_q8<FULL>(a, qbase, d0, x);
+            if (rope) {
                 if (a.qrope.w) norm8(x, inv, a.qrope.w + d0);
                 if (d0 < a.qrope.rot) {
                     const uint32_t dp = d0 < a.qrope.half ? d0 + a.qrope.half : d0 - a.qrope.half;
                     float y[8];
-                    load_q8(a, qbase, dp, y);
+                    load_q8<FULL>(a, qbase, dp, y);
                     if (a.qrope.w) norm8(y, inv, a.qrope.w + dp);
                     rotate8(x, y, d0, pos, a.qrope);
                 }
@@ -314,7 +322,7 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
 // One (group, partition, KV head) per workgroup of W waves.  NB tiles of
 // loads are kept in flight per wave: tile i + NB is requested as soon as
 // tile i has been consumed.
-template <int HD, bool F16, int W, int NB>
+template <int HD, bool F16, int W, int NB, bool FULL>
 __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 
     // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8], split hi/lo.
     in8 qh[KS], ql[KS];
-    load_q<KS, O>(a, con, row, head, a4, qh, ql);
+    load_q<KS, O, FULL>(a, con, row, head, a4, qh, ql);
 
 
     // This wave's run of 16-token tiles inside [tb, te).
@@ -418,38 +426,41 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     uint64_t app_e = 0;
     bool app_v = false, app_own = false;
     uint4 app_w = make_uint4(0u, 0u, 0u, 0u);
-    if (lane < app_items && !a.rope_on) {
+    const bool rope = FULL && a.rope_on;
+    if (lane < app_items && !rope) {
         app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
         if (app_own) app_w = load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e);
     }
     __syncthreads();
-    if (app_items != 0 && a.rope_on) {
-        // Rotary append: the key head of each row this wave owns, one chunk
-        // of 8 dims per lane (the norm and the rotation need the whole head),
-        // exactly as kv_store_rope_kernel.
-        for (uint32_t ar = 0; ar < R; ar++) {
-            const uint32_t pos = a.ranges[2 * (r0 + ar) + 1] - 1;
-            if (pos < ws || pos >= we) continue;  // wave-uniform
-            const uint64_t e = (static_cast<uint64_t>(r0 + ar) * a.n_kvh + kvh) * hd + 8u * lane;
-            float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-            if (lane < cpr) load8_f32(a.src_dtype, a.k_src, e, x);
-            rope_head_wave(x, lane, cpr, pos, a.krope);
-            if (lane < cpr) {
-                uint32_t w[4];
+    if (rope) {
+        if (app_items != 0) {
+            // Rotary append: the key head of each row this wave owns, one chunk
+            // of 8 dims per lane (the norm and the rotation need the whole head),
+            // exactly as kv_store_rope_kernel.
+            for (uint32_t ar = 0; ar < R; ar++) {
+                const uint32_t pos = a.ranges[2 * (r0 + ar) + 1] - 1;
+                if (pos < ws || pos >= we) continue;  // wave-uniform
+                const uint64_t e = (static_cast<uint64_t>(r0 + ar) * a.n_kvh + kvh) * hd + 8u * lane;
+                float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+                if (lane < cpr) load8_f32(a.src_dtype, a.k_src, e, x);
+                rope_head_wave(x, lane, cpr, pos, a.krope);
+                if (lane < cpr) {
+                    uint32_t w[4];
 #pragma unroll
-                for (int q2 = 0; q2 < 4; q2++) {
-                    if (a.src_dtype == THB_DT_F16)
-                        w[q2] = conv16<THB_DT_F16, KVE>(f32_to_f16_rne(x[2 * q2])) |
-                                (conv16<THB_DT_F16, KVE>(f32_to_f16_rne(x[2 * q2 + 1])) << 16);
-                    else
-                        w[q2] = conv32<KVE>(__float_as_uint(x[2 * q2])) |
-                                (conv32<KVE>(__float_as_uint(x[2 * q2 + 1])) << 16);
+                    for (int q2 = 0; q2 < 4; q2++) {
+                        if (a.src_dtype == THB_DT_F16)
+                            w[q2] = conv16<THB_DT_F16, KVE>(f32_to_f16_rne(x[2 * q2])) |
+                                    (conv16<THB_DT_F16, KVE>(f32_to_f16_rne(x[2 * q2 + 1])) << 16);
+                        else
+                            w[q2] = conv32<KVE>(__float_as_uint(x[2 * q2])) |
+                                    (conv32<KVE>(__float_as_uint(x[2 * q2 + 1])) << 16);
+                    }
+                    app_store(pos, false, 8u * lane, make_uint4(w[0], w[1], w[2], w[3]));
+                    app_store(pos, true, 8u * lane, load_encode8_rt<KVE>(a.src_dtype, a.v_src, e));
                 }
-                app_store(pos, false, 8u * lane, make_uint4(w[0], w[1], w[2], w[3]));
-                app_store(pos, true, 8u * lane, load_encode8_rt<KVE>(a.src_dtype, a.v_src, e));
             }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     } else if (app_items != 0) {
         if (app_own) app_store(app_pos, app_v, app_d, app_w);
         for (uint32_t t = lane + 64; t < app_items; t += 64) {
@@ -588,7 +599,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
             if (d >= hd) continue;
             const f32x4 yv = o[i] * inv;
             const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
-            store_y<4>(a, row, head, d, v4);
+            store_y<4, FULL>(a, row, head, d, v4);
         }
         return;
     }
@@ -606,7 +617,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 
 // Merges the partitions of every group that has more than one, in
 // partition order.  One workgroup per (group, KV head).
-template <int HD>
+template <int HD, bool FULL>
 __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
     __shared__ float s_w[kMaxParts * kCols];
     __shared__ float s_inv[kCols];
@@ -640,7 +651,7 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
         for (uint32_t pi = 0; pi < n_parts; pi++) acc += s_w[pi * kCols + c] * src[pi * step];
         const float yv[1] = {acc * s_inv[c]};
         const uint32_t rr = c / H, hh = c - rr * H;
-        store_y<1>(a, r0 + rr, kvh * a.nq_per_kv + h0 + hh, d, yv);
+        store_y<1, FULL>(a, r0 + rr, kvh * a.nq_per_kv + h0 + hh, d, yv);
     }
 }
 
@@ -659,7 +670,7 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
 //   V tile in LDS: [TT/16 slices][HD dims][4 groups of 4 tokens] x 8 bytes,
 //     the group index XOR-ed with (dim / 8) % 4 so that the 16 lanes of a
 //     PV operand read hit distinct banks.
-template <int HD, bool F16, int W>
+template <int HD, bool F16, int W, bool FULL>
 __global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
@@ -721,7 +732,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
         chi = min(a.ranges[2 * row + 1], te);
     }
     in8 qh[KS], ql[KS];
-    load_q<KS, O>(a, con, row, head, a4, qh, ql);
+    load_q<KS, O, FULL>(a, con, row, head, a4, qh, ql);
 
     const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
     const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
@@ -858,7 +869,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
             if (d >= hd) continue;
             const f32x4 yv = o[i] * inv;
             const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
-            store_y<4>(a, row, head, d, v4);
+            store_y<4, FULL>(a, row, head, d, v4);
         }
         return;
     }
@@ -891,7 +902,10 @@ constexpr int ring_for(int hd) { return hd >= 512 ? 1 : hd >= 256 ? 2 : THB_ATTN
 template <int HD, bool F16>
 void launch_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
     constexpr int W = waves_for(HD);
-    hipLaunchKernelGGL((attn_mfma<HD, F16, W, ring_for(HD)>), grid, dim3(64 * W), 0, s, a);
+    if (a.full)
+        hipLaunchKernelGGL((attn_mfma<HD, F16, W, ring_for(HD), true>), grid, dim3(64 * W), 0, s, a);
+    else
+        hipLaunchKernelGGL((attn_mfma<HD, F16, W, ring_for(HD), false>), grid, dim3(64 * W), 0, s, a);
 }
 
 void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
@@ -906,7 +920,10 @@ void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s
 template <int HD, bool F16>
 void launch_prefill_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
     constexpr int W = waves_for(HD);
-    hipLaunchKernelGGL((attn_prefill<HD, F16, W>), grid, dim3(64 * W), 0, s, a);
+    if (a.full)
+        hipLaunchKernelGGL((attn_prefill<HD, F16, W, true>), grid, dim3(64 * W), 0, s, a);
+    else
+        hipLaunchKernelGGL((attn_prefill<HD, F16, W, false>), grid, dim3(64 * W), 0, s, a);
 }
 
 void launch_prefill(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
@@ -918,12 +935,20 @@ void launch_prefill(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipSt
     }
 }
 
+template <int HD>
+void launch_merge_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
+    if (a.full)
+        hipLaunchKernelGGL((attn_merge<HD, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((attn_merge<HD, false>), grid, dim3(256), 0, s, a);
+}
+
 void launch_merge(uint32_t hd_t, dim3 grid, const AttnArgs& a, hipStream_t s) {
     switch (hd_t) {
-        case 64: hipLaunchKernelGGL(attn_merge<64>, grid, dim3(256), 0, s, a); break;
-        case 128: hipLaunchKernelGGL(attn_merge<128>, grid, dim3(256), 0, s, a); break;
-        case 256: hipLaunchKernelGGL(attn_merge<256>, grid, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL(attn_merge<512>, grid, dim3(256), 0, s, a); break;
+        case 64: launch_merge_hd<64>(grid, a, s); break;
+        case 128: launch_merge_hd<128>(grid, a, s); break;
+        case 256: launch_merge_hd<256>(grid, a, s); break;
+        default: launch_merge_hd<512>(grid, a, s); break;
     }
 }
 
@@ -1269,6 +1294,8 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.gate = io.gate_dev;
     a.gate_stride = io.gate_stride ? io.gate_stride : hd;
     a.rope_on = rope != nullptr;
+    a.full = rope != nullptr || io.gate_dev != nullptr || a.q_stride != hd || sp.q_dtype == THB_DT_BF16 ||
+             sp.y_dtype == THB_DT_BF16;
     a.meta = meta;
     a.qrope = rope ? rope_dev(*rope, true) : RopeDev{};
     a.krope = rope ? rope_dev(*rope, false) : RopeDev{};
