@@ -368,6 +368,30 @@ def run_secondary(args):
         out["prefill"] = {"us_per_layer": round(pus, 1), "TFLOPs": round(flops / (pus * 1e-6) / 1e12, 1),
                           "mfma_frac_of_2.5PF": round(flops / (pus * 1e-6) / 2.5e15, 4),
                           "flops": flops, "note": "8 x 512 causal rows; unmasked (q,k) pairs x 4 x nq x hd"}
+        # Qwen3's layer step proper: q_norm/k_norm + rotation (norm_rope), append, attention,
+        # as the reference's four dispatches vs one thb_attn_step
+        from flint_amd.rope import Rope, kv_store_rope, rope_rows
+        wq = torch.rand(hd, device=dev, generator=g) + 0.5
+        wk = torch.rand(hd, device=dev, generator=g) + 0.5
+        rope = Rope.from_theta(max(positions) + 1, hd, 1e6, q_norm=wq, k_norm=wk)
+        qr, kr = q.clone(), k.clone()
+
+        def unfused():
+            for layer in range(L):
+                rope_rows(qr, nq, rope, rows, m, norm_w=wq)
+                rope_rows(kr, nkv, rope, rows, m, norm_w=wk)
+                ops.kv_store(kr, v, pool, layer, m, rows)
+                ops.attn(qr, pool, layer, y, sp)
+
+        def fused():
+            for layer in range(L):
+                ops.attn_step(pool, layer, sp, q, y, k_src=k, v_src=v, rope=rope)
+
+        r_un = _time_steps(torch, unfused, args.steps, args.warmup) / L
+        r_fu = _time_steps(torch, fused, args.steps, args.warmup) / L
+        out["norm_rope_step"] = {"fused_us_per_layer": round(r_fu, 1), "unfused_us_per_layer": round(r_un, 1),
+                                 "note": "the same mixed call with q/k RMSNorm + rotation: rope_rows(q), "
+                                         "rope_rows(k), kv_store, attn vs one thb_attn_step"}
         out["config"] = {"workload": "qwen3-8b C3: 64 decode rows (log-normal ctx in [256, 32768], median 2048) "
                                      "+ 8 x 512-token causal prefill chunks in one call per layer, 32q/8kv/hd128, "
                                      f"page 16, f16 KV, pool {pages} pages 60% pre-occupied, {L} layers cycled"}

@@ -277,46 +277,78 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
     const uint32_t hd = a.head_dim;
     const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * (FULL ? a.q_stride : hd);
     const bool rope = FULL && a.rope_on;
-    uint32_t pos = 0;
-    float inv = 1.0f;
-    if (rope) {
-        pos = con ? a.meta[8 * row] : 0u;
-        if (a.qrope.w) {
-            float ss = 0.0f;
+    if (!rope) {
 #pragma unroll
-            for (int j = 0; j < KS; j++) {
-                const uint32_t d0 = 32u * j + 8u * a4;
-                if (con && d0 < hd) {
-                    float x[8];
-                    load_q8<FULL>(a, qbase, d0, x);
-                    ss += sumsq8(x);
-                }
+        for (int j = 0; j < KS; j++) {
+            const uint32_t d0 = 32u * j + 8u * a4;
+            float x[8];
+            if (con && d0 < hd) {
+                load_q8<FULL>(a, qbase, d0, x);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = 0.0f;
             }
-            inv = rms_inv(col_sum(ss), hd, a.qrope.eps);
+            O::split8(x, qh[j], ql[j]);
         }
+        return;
     }
+    // Rotary path: the lane's chunks in registers, normalised in place.
+    const RopeDev& r = a.qrope;
+    const uint32_t pos = con ? a.meta[8 * row] : 0u;
+    float x[KS][8];
 #pragma unroll
     for (int j = 0; j < KS; j++) {
         const uint32_t d0 = 32u * j + 8u * a4;
-        float x[8];
         if (con && d0 < hd) {
-            load_q8<FULL>(a, qbase, d0, x);
-            if (rope) {
-                if (a.qrope.w) norm8(x, inv, a.qrope.w + d0);
-                if (d0 < a.qrope.rot) {
-                    const uint32_t dp = d0 < a.qrope.half ? d0 + a.qrope.half : d0 - a.qrope.half;
-                    float y[8];
-                    load_q8<FULL>(a, qbase, dp, y);
-                    if (a.qrope.w) norm8(y, inv, a.qrope.w + dp);
-                    rotate8(x, y, d0, pos, a.qrope);
-                }
-            }
+            load_q8<FULL>(a, qbase, d0, x[j]);
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++) x[e] = 0.0f;
+            for (int e = 0; e < 8; e++) x[j][e] = 0.0f;
         }
-        O::split8(x, qh[j], ql[j]);
     }
+    float inv = 1.0f;
+    if (r.w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KS; j++) ss += sumsq8(x[j]);
+        inv = rms_inv(col_sum(ss), hd, r.eps);
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const uint32_t d0 = 32u * j + 8u * a4;
+            if (con && d0 < hd) norm8(x[j], inv, r.w + d0);
+        }
+    }
+    if (r.rot == hd && hd == 32u * KS) {
+        // Full rotation at the template width: the partner of chunk j is
+        // chunk j + KS / 2 of the same lane.
+#pragma unroll
+        for (int j = 0; j < KS / 2; j++) {
+            float lo[8], hi[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                lo[e] = x[j][e];
+                hi[e] = x[j + KS / 2][e];
+            }
+            const uint32_t d0 = 32u * j + 8u * a4;
+            rotate8(x[j], hi, d0, pos, r);
+            rotate8(x[j + KS / 2], lo, d0 + r.half, pos, r);
+        }
+    } else {
+        // Partial rotation or a narrower head: partners from memory.
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const uint32_t d0 = 32u * j + 8u * a4;
+            if (con && d0 < r.rot) {
+                const uint32_t dp = d0 < r.half ? d0 + r.half : d0 - r.half;
+                float y[8];
+                load_q8<FULL>(a, qbase, dp, y);
+                if (r.w) norm8(y, inv, r.w + dp);
+                rotate8(x[j], y, d0, pos, r);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < KS; j++) O::split8(x[j], qh[j], ql[j]);
 }
 
 // One (group, partition, KV head) per workgroup of W waves.  NB tiles of
@@ -443,7 +475,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
                 const uint64_t e = (static_cast<uint64_t>(r0 + ar) * a.n_kvh + kvh) * hd + 8u * lane;
                 float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
                 if (lane < cpr) load8_f32(a.src_dtype, a.k_src, e, x);
-                rope_head_wave(x, lane, cpr, pos, a.krope);
+                rope_head_seg(x, lane, cpr, 0, pos, a.krope);
                 if (lane < cpr) {
                     uint32_t w[4];
 #pragma unroll
@@ -732,7 +764,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
         chi = min(a.ranges[2 * row + 1], te);
     }
     in8 qh[KS], ql[KS];
-    load_q<KS, O, FULL>(a, con, row, head, a4, qh, ql);
 
     const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
     const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
@@ -844,10 +875,11 @@ __global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
     __syncthreads();  // s_page complete
     {
         u32x4 kr[KPT], vr[VPT];
-        if (n_tiles) {
-            load(t_first, kr, vr);
-            store(0, kr, vr);
-        }
+        // The first tile's loads are in flight while the query is loaded
+        // (and normalised / rotated, which takes dependent round trips).
+        if (n_tiles) load(t_first, kr, vr);
+        load_q<KS, O, FULL>(a, con, row, head, a4, qh, ql);
+        if (n_tiles) store(0, kr, vr);
         __syncthreads();
         for (uint32_t i = 0; i < n_tiles; i++) {
             const uint32_t t0 = t_first + i * TT;

@@ -131,30 +131,34 @@ struct RopeStoreArgs {
     const uint32_t* table;
     uint64_t plane;
     uint32_t max_pages, page_shift, head_dim, kv_heads, m;
-    uint32_t do_v;  // 0: K only (V is written by the run kernel)
+    uint32_t seg_shift;  // log2 of the lanes per head (the power of two >= head_dim / 8)
+    uint32_t do_v;       // 0: K only (V is written by the run kernel)
     RopeDev rope;
 };
 
-// Rotary append: one wavefront per (row, KV head), lane u holding dims
-// [8u, 8u + 8).  K is normalised (with a weight), rotated at the row's
-// position, rounded to the source type and encoded into its page chunk; V
-// is stored as by kv_store_kernel.  Grid: ceil(m * kv_heads / 4) x 256.
+// Rotary append: each wavefront holds 64 >> seg_shift (row, KV head) pairs
+// in lane segments, lane u of a segment holding dims [8u, 8u + 8).  K is
+// normalised (with a weight), rotated at the row's position, rounded to the
+// source type and encoded into its page chunk; V is stored as by
+// kv_store_kernel.  Grid: ceil(pairs / (4 * heads per wave)) x 256.
 template <uint32_t SRC, uint32_t KV>
 __global__ __launch_bounds__(256) void kv_store_rope_kernel(RopeStoreArgs a) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wi >= a.m * a.kv_heads) return;  // whole wavefront
-    const uint32_t row = wi / a.kv_heads, h = wi - row * a.kv_heads;
+    const uint32_t seg = lane >> a.seg_shift, u = lane & ((1u << a.seg_shift) - 1u);
+    const uint32_t pair = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (64u >> a.seg_shift) + seg;
     const uint32_t cph = a.head_dim >> 3;
-    const uint32_t pos = a.meta[8 * row], seq = a.meta[8 * row + 1];
+    const bool act = pair < a.m * a.kv_heads && u < cph;
+    const uint32_t row = act ? pair / a.kv_heads : 0u, h = act ? pair - row * a.kv_heads : 0u;
+    const uint32_t pos = act ? a.meta[8 * row] : 0u;
+    const uint64_t e = (static_cast<uint64_t>(row) * a.kv_heads + h) * a.head_dim + 8u * u;
+    float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (act) load8_f32(SRC, a.k_src, e, x);
+    rope_head_seg(x, act ? u : cph, cph, seg << a.seg_shift, pos, a.rope);
+    if (!act) return;
+    const uint32_t seq = a.meta[8 * row + 1];
     const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (pos >> a.page_shift)];
     const uint32_t j = pos & ((1u << a.page_shift) - 1u);
-    const uint64_t e = (static_cast<uint64_t>(row) * a.kv_heads + h) * a.head_dim + 8u * lane;
-    const uint64_t pbase = h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + 8u * lane) << a.page_shift);
-    float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    if (lane < cph) load8_f32(SRC, a.k_src, e, x);
-    rope_head_wave(x, lane, cph, pos, a.rope);
-    if (lane >= cph) return;
+    const uint64_t pbase = h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + 8u * u) << a.page_shift);
     uint32_t w[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -179,24 +183,25 @@ __global__ __launch_bounds__(256) void kv_store_rope_kernel(RopeStoreArgs a) {
 struct RopeRowsArgs {
     void* x;  // [m, heads, head_dim], f32 or f16, in place
     const uint32_t* meta;
-    uint32_t m, heads, head_dim;
+    uint32_t m, heads, head_dim, seg_shift;
     RopeDev rope;
 };
 
-// ops::rope / ops::norm_rope in place: one wavefront per (row, head).
+// ops::rope / ops::norm_rope in place: 64 >> seg_shift (row, head) vectors
+// per wavefront, one per lane segment.
 template <uint32_t DT>
 __global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wi >= a.m * a.heads) return;  // whole wavefront
-    const uint32_t row = wi / a.heads;
+    const uint32_t seg = lane >> a.seg_shift, u = lane & ((1u << a.seg_shift) - 1u);
+    const uint32_t vec = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (64u >> a.seg_shift) + seg;
     const uint32_t cph = a.head_dim >> 3;
-    const uint32_t pos = a.meta[8 * row];
-    const uint64_t e = static_cast<uint64_t>(wi) * a.head_dim + 8u * lane;
+    const bool act = vec < a.m * a.heads && u < cph;
+    const uint32_t pos = act ? a.meta[8 * (vec / a.heads)] : 0u;
+    const uint64_t e = static_cast<uint64_t>(vec) * a.head_dim + 8u * u;
     float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    if (lane < cph) load8_f32(DT, a.x, e, x);
-    rope_head_wave(x, lane, cph, pos, a.rope);
-    if (lane >= cph) return;
+    if (act) load8_f32(DT, a.x, e, x);
+    rope_head_seg(x, act ? u : cph, cph, seg << a.seg_shift, pos, a.rope);
+    if (!act) return;
     if constexpr (DT == THB_DT_F16) {
         uint32_t w[4];
 #pragma unroll
@@ -207,6 +212,14 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
         p[0] = f32x4{x[0], x[1], x[2], x[3]};
         p[1] = f32x4{x[4], x[5], x[6], x[7]};
     }
+}
+
+// log2 of the lanes a head of head_dim elements takes (8 per lane, a power
+// of two).
+inline uint32_t seg_shift_for(uint32_t head_dim) {
+    uint32_t sh = 3;
+    while ((1u << sh) < head_dim / 8) sh++;
+    return sh;
 }
 
 struct GatherArgs {
@@ -777,7 +790,9 @@ int thb_rope_rows(void* x, uint32_t dtype, uint32_t m, uint32_t heads, uint32_t 
         a.head_dim = head_dim;
         a.rope = rope_dev(*rope, true);
         a.rope.w = norm_w;
-        const dim3 grid(static_cast<uint32_t>((waves + 3) / 4));
+        a.seg_shift = seg_shift_for(head_dim);
+        const uint64_t per_block = 4ull * (64u >> a.seg_shift);
+        const dim3 grid(static_cast<uint32_t>((waves + per_block - 1) / per_block));
         if (dtype == THB_DT_F16)
             hipLaunchKernelGGL(rope_rows_kernel<THB_DT_F16>, grid, dim3(256), 0, s, a);
         else
@@ -828,7 +843,9 @@ int thb_kv_store_rope(thb_pool* pool, uint32_t layer, const void* k_src, const v
                                              pool->page_shift, runs);
         const bool by_runs = 2 * static_cast<uint64_t>(long_rows) >= m;
         a.do_v = by_runs ? 0u : 1u;
-        const dim3 grid(static_cast<uint32_t>((waves + 3) / 4));
+        a.seg_shift = seg_shift_for(g.head_dim);
+        const uint64_t per_block = 4ull * (64u >> a.seg_shift);
+        const dim3 grid(static_cast<uint32_t>((waves + per_block - 1) / per_block));
         if (src_dtype == THB_DT_F16)
             launch_store_rope<THB_DT_F16>(pool->kv_dtype, grid, a, s);
         else

@@ -94,25 +94,27 @@ __device__ inline void load8_f32(uint32_t dtype, const void* src, uint64_t e, fl
     }
 }
 
-// One head vector per wavefront: lane u < cph holds dims [8u, 8u + 8) in x.
+// Head vectors in lane segments: the segment starting at lane seg_base
+// holds one head, lane seg_base + u (u < cph) its dims [8u, 8u + 8) in x.
 // Applies the RMSNorm (when r.w is set; the sum of squares runs over the
 // chunks in order) and the rotation at position pos.  Every lane of the
-// wavefront must call it (cross-lane reads); lanes >= cph carry no data.
-__device__ inline void rope_head_wave(float (&x)[8], uint32_t lane, uint32_t cph, uint32_t pos, const RopeDev& r) {
+// wavefront must call it (cross-lane reads); lanes with u >= cph carry no
+// data and read none.
+__device__ inline void rope_head_seg(float (&x)[8], uint32_t u, uint32_t cph, uint32_t seg_base, uint32_t pos,
+                                     const RopeDev& r) {
     if (r.w) {
-        const float s = lane < cph ? sumsq8(x) : 0.0f;
+        const float s = u < cph ? sumsq8(x) : 0.0f;
         float ss = 0.0f;
-        for (uint32_t i = 0; i < cph; i++)
-            ss = ss + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), static_cast<int>(i)));
+        for (uint32_t i = 0; i < cph; i++) ss = ss + __shfl(s, static_cast<int>(seg_base + i));
         const float inv = rms_inv(ss, 8u * cph, r.eps);
-        if (lane < cph) norm8(x, inv, r.w + 8u * lane);
+        if (u < cph) norm8(x, inv, r.w + 8u * u);
     }
     const uint32_t hc = r.half >> 3;  // chunks per half
-    const uint32_t partner = lane < hc ? lane + hc : lane - hc;
+    const uint32_t partner = seg_base + (u < hc ? u + hc : u - hc);
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) y[e] = __shfl(x[e], static_cast<int>(partner & 63u));
-    if (8u * lane < r.rot) rotate8(x, y, 8u * lane, pos, r);
+    if (u < cph && 8u * u < r.rot) rotate8(x, y, 8u * u, pos, r);
 }
 
 // f32 -> f16 bits, round to nearest even (thuban_num::f32_to_f16).

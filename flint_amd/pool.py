@@ -68,9 +68,13 @@ class KvArena:
         self._own = True
 
     def __del__(self):
-        if getattr(self, "_own", False) and self._h:
-            lib().thb_arena_destroy(self._h)
-            self._h = None
+        # at interpreter shutdown the loader may already be gone: nothing to release then
+        try:
+            if getattr(self, "_own", False) and self._h:
+                lib().thb_arena_destroy(self._h)
+                self._h = None
+        except (AttributeError, ImportError, TypeError):
+            pass
 
     def alloc(self, seq: int, pos: int, tokens: int) -> None:
         check(lib().thb_arena_alloc(self._h, seq, pos, tokens))
@@ -166,7 +170,10 @@ class KvPool:
             self._h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except (AttributeError, ImportError, TypeError):  # interpreter shutdown
+            pass
 
     @property
     def handle(self) -> int:
@@ -293,7 +300,10 @@ class RowMeta:
             self._h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except (AttributeError, ImportError, TypeError):  # interpreter shutdown
+            pass
 
     @property
     def handle(self) -> int:
