@@ -703,7 +703,7 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
 //     the group index XOR-ed with (dim / 8) % 4 so that the 16 lanes of a
 //     PV operand read hit distinct banks.
 template <int HD, bool F16, int W, bool FULL>
-__global__ __launch_bounds__(64 * W) void attn_prefill(AttnArgs a) {
+__global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnArgs a) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
     typedef typename O::in4 in4;
@@ -1336,22 +1336,15 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     const uint64_t n_pwg = static_cast<uint64_t>(plan.n_bitems) * pool->kv_heads;
     if (n_wg > 0x7FFFFFFFull || n_pwg > 0x7FFFFFFFull)
         throw HipError{hipErrorInvalidConfiguration, "attention grid too large"};
-    if (n_wg && n_pwg) {
-        // A mixed call: the HBM-bound decode items and the matrix-core-bound
-        // prefill blocks are independent, so the prefill kernel runs on the
-        // pool's second stream, forked from and joined back into s.
-        THB_HIP(hipEventRecord(pool->fork_ev, s));
-        THB_HIP(hipStreamWaitEvent(pool->aux, pool->fork_ev, 0));
-        launch_prefill(hd_t, f16, dim3(static_cast<uint32_t>(n_pwg)), a, pool->aux);
-        THB_HIP(hipGetLastError());
+    // A mixed call runs the decode items, then the prefill blocks, on the
+    // caller's stream.  (Running the prefill kernel concurrently on a second
+    // stream measured slower once the prefill kernel ran two workgroups per
+    // CU: 262 vs 248 us per C3 layer.)
+    if (n_wg) {
         launch(hd_t, f16, dim3(static_cast<uint32_t>(n_wg)), a, s);
         THB_HIP(hipGetLastError());
-        THB_HIP(hipEventRecord(pool->join_ev, pool->aux));
-        THB_HIP(hipStreamWaitEvent(s, pool->join_ev, 0));
-    } else if (n_wg) {
-        launch(hd_t, f16, dim3(static_cast<uint32_t>(n_wg)), a, s);
-        THB_HIP(hipGetLastError());
-    } else if (n_pwg) {
+    }
+    if (n_pwg) {
         launch_prefill(hd_t, f16, dim3(static_cast<uint32_t>(n_pwg)), a, s);
         THB_HIP(hipGetLastError());
     }

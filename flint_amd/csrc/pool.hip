@@ -334,9 +334,6 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
         void* gd = p->geom_buf.reserve(dl.size() * sizeof(DevLayer), false);
         THB_HIP(hipMemcpy(gd, dl.data(), dl.size() * sizeof(DevLayer), hipMemcpyHostToDevice));
         p->arena.a.clear_dirty();
-        THB_HIP(hipStreamCreateWithFlags(&p->aux, hipStreamNonBlocking));  // default priority
-        THB_HIP(hipEventCreateWithFlags(&p->fork_ev, hipEventDisableTiming));
-        THB_HIP(hipEventCreateWithFlags(&p->join_ev, hipEventDisableTiming));
         THB_HIP(hipDeviceSynchronize());
         *out = p.release();
         return THB_OK;
@@ -346,9 +343,6 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
 void thb_pool_destroy(thb_pool* pool) {
     if (!pool) return;
     (void)hipDeviceSynchronize();
-    if (pool->fork_ev) (void)hipEventDestroy(pool->fork_ev);
-    if (pool->join_ev) (void)hipEventDestroy(pool->join_ev);
-    if (pool->aux) (void)hipStreamDestroy(pool->aux);
     if (pool->owns_mem && pool->mem) (void)hipFree(pool->mem);
     if (pool->table_dev) (void)hipFree(pool->table_dev);
     delete pool;

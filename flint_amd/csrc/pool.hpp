@@ -74,10 +74,6 @@ struct thb_pool {
     std::array<thb::AttnPlan, 4> plans;
     uint64_t plan_clock = 0;
     int device = 0;
-    // Second stream for the prefill kernel of a mixed call, forked from and
-    // joined back into the caller's stream with these events.
-    hipStream_t aux = nullptr;
-    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
 };
 
 namespace thb {
