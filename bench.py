@@ -109,7 +109,7 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
     exactly its sequences' pages).  HIP events around `reps` replays of a
     captured graph of the B gather (scatter) calls, and around `reps`
     block-copy calls; algorithmic bytes = 2 x bytes moved."""
-    from flint_amd.pool import ArenaSpec, KvPool
+    from flint_amd.pool import ArenaSpec, KvPool, RowMeta
 
     kb = torch.empty(B, nkv, ctx, hd, dtype=torch.int16, device=dev)
     vb = torch.empty_like(kb)
@@ -119,20 +119,20 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
         for s in range(B):
             fn(pool, layer, s, 0, ctx, kb[s], vb[s])
 
-    def graph_of(fn):
-        # one graph of the B calls: Python issues a call in ~10 us, longer than the kernel
+    def graph_of_fn(work):
+        # one graph of many calls: Python issues a call in ~10 us, longer than the kernel
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(side):
-            sweep(fn)  # warm
+            work()  # warm
             side.synchronize()
             with torch.cuda.graph(graph, stream=side):
-                sweep(fn)
+                work()
         torch.cuda.current_stream().wait_stream(side)
         return graph
 
-    gg, gs = graph_of(ops.kv_gather), graph_of(ops.kv_scatter)
+    gg, gs = graph_of_fn(lambda: sweep(ops.kv_gather)), graph_of_fn(lambda: sweep(ops.kv_scatter))
     gg.replay()
     gs.replay()
     torch.cuda.synchronize()
@@ -169,6 +169,28 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
     torch.cuda.synchronize()
     c_us = c0.elapsed_time(c1) / reps * 1e3
     c_moved = len(triples) * pool.layers * 2 * nkv * pl * hd * 2
+    # bulk append: a prefill-sized call (8 sequences x 512 consecutive positions) into the
+    # second pool, f16 sources, one layer per call, all layers in turn
+    rows_b = RowMeta(4096)
+    rows_b.write([p for _ in range(8) for p in range(512)], [s for s in range(8) for _ in range(512)], 4096)
+    kb = torch.randn(4096, nkv, hd, device=dev).half()
+    vb2 = torch.randn(4096, nkv, hd, device=dev).half()
+    def append_all():
+        for layer in range(pool.layers):
+            ops.kv_store(kb, vb2, cpool, layer, 4096, rows_b)
+
+    ga = graph_of_fn(append_all)  # the runs are uploaded by the warm call, outside the graph
+    ga.replay()
+    torch.cuda.synchronize()
+    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    b0.record()
+    for _ in range(reps):
+        ga.replay()
+    b1.record()
+    torch.cuda.synchronize()
+    del ga
+    a_us = b0.elapsed_time(b1) / (reps * pool.layers) * 1e3
+    a_bytes = 4096 * nkv * hd * 2 * (2 + 2)  # K and V: f16 source read + f16 page write
     cpool.close()
 
     def rec(us, nbytes, note):
@@ -180,7 +202,12 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
                                        f"({B} calls, one graph) into [kv_heads, ctx, head_dim]"),
             "scatter": rec(s_us, moved, f"kv_scatter of the same {B} buffers back ({B} calls, one graph)"),
             "block_copy": rec(c_us, c_moved, f"one block_copy call of {len(triples)} whole pages x "
-                                             f"{pool.layers} layers x K,V x {nkv} heads")}
+                                             f"{pool.layers} layers x K,V x {nkv} heads"),
+            "append_bulk": {"us_per_call": round(a_us, 2), "GBps": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
+                            "frac": round(a_bytes / (a_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4), "bytes": a_bytes,
+                            "note": "kv_store of a 4096-row prefill call (8 seqs x 512 positions), f16 source, "
+                                    "one graph of a call per layer; bytes = rows x kv_heads x head_dim x "
+                                    "(2 B read + 2 B write) x K,V"}}
 
 
 def time_rope_step(torch, ops, pool, rows, positions, seqs, q, k_new, v_new, L, B, nq, hd, scale, steps=5):

@@ -74,49 +74,82 @@ struct RunArgs {
     uint32_t do_k;  // 0: V only (K is written by the rotary append kernel)
 };
 
-constexpr uint32_t kMaxRun = 64;  // tokens of one run (LDS: kMaxRun * head_dim * 2 bytes)
+// Tokens per run.  A 4096-row prefill call at head_dim 128 (8 KV heads) took
+// 11.1 / 9.8 / 8.2 / 9.8 us with runs of 64 / 32 / 16 / 8 tokens: 16 gives
+// 2048 workgroups, enough to keep every CU's loads in flight.
+constexpr uint32_t kRunTokens = 16;
+constexpr uint32_t kMaxRunPages = kRunTokens / 8 + 1;  // pages a run touches (page_len >= 8)
 
 // Append of runs: consecutive rows of one sequence whose positions are
-// consecutive and inside one page (a prefill chunk).  One workgroup per
-// (run, KV head).  K: the run's tokens of each chunk row are contiguous
-// 16-byte units.  V: the encoded rows are staged in LDS as [token][dim] and
-// written as the page's [dim][token] rows, 8 tokens (16 bytes) per store
-// where a whole aligned group of 8 lies inside the run, 2 bytes at its ends.
+// consecutive (a prefill chunk), up to kRunTokens tokens, across pages.  One
+// workgroup per (run, KV head).  K: the run's tokens of each chunk row are
+// contiguous 16-byte units within a page.  V: the encoded rows are staged in
+// LDS as [token][dim] (rows padded by one word, so the 8 tokens of a group
+// hit distinct banks) and written as the pages' [dim][token] rows, 8 tokens
+// (16 bytes) per store where a whole aligned group of 8 lies inside the run,
+// 2 bytes at its ends.
 template <uint32_t SRC, uint32_t KV>
 __global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
-    __shared__ uint4 s_v[kMaxRun * 512 / 8];
+    extern __shared__ uint32_t s_run[];  // [len][head_dim + 2] 16-bit V slots
+    __shared__ uint32_t s_pg[kMaxRunPages];
     const uint32_t run = blockIdx.x / a.kv_heads, h = blockIdx.x - run * a.kv_heads;
     const uint32_t* R = a.runs + 4 * run;
     const uint32_t row0 = R[0], len = R[1], seq = R[2], pos0 = R[3];
-    const uint32_t shift = a.page_shift, hd = a.head_dim, cph = hd >> 3;
-    const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (pos0 >> shift)];
-    const uint32_t j0 = pos0 & ((1u << shift) - 1u);
-    const uint64_t pbase = static_cast<uint64_t>(h) * a.plane + ((static_cast<uint64_t>(page) * hd) << shift);
-    for (uint32_t u = threadIdx.x; u < len * cph; u += 256) {
-        const uint32_t ch = u / len, t = u - ch * len;
-        const uint64_t e = ((static_cast<uint64_t>(row0 + t)) * a.kv_heads + h) * hd + 8u * ch;
-        if (a.do_k)
-            *reinterpret_cast<uint4*>(a.k + pbase + (static_cast<uint64_t>(8u * ch) << shift) + ((j0 + t) << 3)) =
-                load_encode8<SRC, KV>(a.k_src, e);
-        s_v[t * cph + ch] = load_encode8<SRC, KV>(a.v_src, e);
+    const uint32_t shift = a.page_shift, hd = a.head_dim, cph = hd >> 3, mask = (1u << shift) - 1u;
+    const uint32_t lp0 = pos0 >> shift, np = ((pos0 + len - 1) >> shift) - lp0 + 1;
+    if (threadIdx.x < np) s_pg[threadIdx.x] = a.table[static_cast<uint64_t>(seq) * a.max_pages + lp0 + threadIdx.x];
+    __syncthreads();
+    const uint64_t hbase = static_cast<uint64_t>(h) * a.plane;
+    auto page_base = [&](uint32_t pos) {
+        return hbase + ((static_cast<uint64_t>(s_pg[(pos >> shift) - lp0]) * hd) << shift);
+    };
+    const uint32_t rs = (hd + 2) >> 1;  // LDS row stride in 32-bit words
+    // Four (token, chunk) units per lane at a time: all their source loads are
+    // issued before the first store.
+    const uint32_t units = len * cph;
+    for (uint32_t u0 = threadIdx.x; u0 < units; u0 += 4 * 256) {
+        uint4 kw[4], vw[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t u = u0 + 256 * i;
+            if (u >= units) continue;
+            const uint32_t ch = u / len, t = u - ch * len;
+            const uint64_t e = ((static_cast<uint64_t>(row0 + t)) * a.kv_heads + h) * hd + 8u * ch;
+            if (a.do_k) kw[i] = load_encode8<SRC, KV>(a.k_src, e);
+            vw[i] = load_encode8<SRC, KV>(a.v_src, e);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t u = u0 + 256 * i;
+            if (u >= units) continue;
+            const uint32_t ch = u / len, t = u - ch * len, pos = pos0 + t;
+            if (a.do_k)
+                *reinterpret_cast<uint4*>(a.k + page_base(pos) + (static_cast<uint64_t>(8u * ch) << shift) +
+                                          ((pos & mask) << 3)) = kw[i];
+            uint32_t* dst = s_run + t * rs + 4u * ch;
+            dst[0] = vw[i].x;
+            dst[1] = vw[i].y;
+            dst[2] = vw[i].z;
+            dst[3] = vw[i].w;
+        }
     }
     __syncthreads();
-    const uint16_t* sv = reinterpret_cast<const uint16_t*>(s_v);
-    const uint32_t g0 = j0 >> 3, ng = ((j0 + len - 1) >> 3) - g0 + 1;
+    const uint16_t* sv = reinterpret_cast<const uint16_t*>(s_run);
+    const uint32_t G0 = pos0 >> 3, ng = ((pos0 + len - 1) >> 3) - G0 + 1;  // aligned groups of 8 positions
     for (uint32_t u = threadIdx.x; u < hd * ng; u += 256) {
-        const uint32_t d = u / ng, jg = (g0 + (u - d * ng)) << 3;
-        uint16_t* dst = a.v + pbase + (static_cast<uint64_t>(d) << shift) + jg;
-        if (jg >= j0 && jg + 8 <= j0 + len) {
+        const uint32_t d = u / ng, p8 = (G0 + (u - d * ng)) << 3;
+        uint16_t* dst = a.v + page_base(p8) + (static_cast<uint64_t>(d) << shift) + (p8 & mask);
+        if (p8 >= pos0 && p8 + 8 <= pos0 + len) {
             uint32_t w[4];
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                w[q] = static_cast<uint32_t>(sv[(jg - j0 + 2 * q) * hd + d]) |
-                       (static_cast<uint32_t>(sv[(jg - j0 + 2 * q + 1) * hd + d]) << 16);
+                w[q] = static_cast<uint32_t>(sv[(p8 - pos0 + 2 * q) * 2 * rs + d]) |
+                       (static_cast<uint32_t>(sv[(p8 - pos0 + 2 * q + 1) * 2 * rs + d]) << 16);
             *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
         } else {
             for (uint32_t e = 0; e < 8; e++) {
-                const uint32_t j = jg + e;
-                if (j >= j0 && j < j0 + len) dst[e] = sv[(j - j0) * hd + d];
+                const uint32_t p = p8 + e;
+                if (p >= pos0 && p < pos0 + len) dst[e] = sv[(p - pos0) * 2 * rs + d];
             }
         }
     }
@@ -482,29 +515,55 @@ void launch_store(uint32_t kv, dim3 grid, const StoreArgs& a, hipStream_t s) {
 
 template <uint32_t SRC>
 void launch_runs(uint32_t kv, dim3 grid, const RunArgs& a, hipStream_t s) {
+    const size_t lds = static_cast<size_t>(kRunTokens) * (a.head_dim + 2) * 2;
     if (kv == THB_KV_F16_RNE)
-        hipLaunchKernelGGL((kv_store_runs_kernel<SRC, THB_KV_F16_RNE>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((kv_store_runs_kernel<SRC, THB_KV_F16_RNE>), grid, dim3(256), lds, s, a);
     else
-        hipLaunchKernelGGL((kv_store_runs_kernel<SRC, THB_KV_BF16_TRUNC>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((kv_store_runs_kernel<SRC, THB_KV_BF16_TRUNC>), grid, dim3(256), lds, s, a);
 }
 
 // Cuts rows [0, m) of the call into runs (consecutive rows of one sequence,
-// consecutive positions, one page, at most kMaxRun tokens).  Returns the
-// number of rows in runs of 8 or more tokens.
-uint32_t make_runs(const uint32_t* meta, uint32_t m, uint32_t page_shift, std::vector<uint32_t>& runs) {
+// consecutive positions, at most max_run tokens).  Returns the number of
+// rows in runs of 8 or more tokens.
+uint32_t make_runs(const uint32_t* meta, uint32_t m, uint32_t max_run, std::vector<uint32_t>& runs) {
     uint32_t long_rows = 0;
     uint32_t r = 0;
     while (r < m) {
         const uint32_t seq = meta[8 * r + 1], pos0 = meta[8 * r];
         uint32_t len = 1;
-        while (r + len < m && len < kMaxRun && meta[8 * (r + len) + 1] == seq &&
-               meta[8 * (r + len)] == pos0 + len && ((pos0 + len) >> page_shift) == (pos0 >> page_shift))
+        while (r + len < m && len < max_run && meta[8 * (r + len) + 1] == seq && meta[8 * (r + len)] == pos0 + len)
             len++;
         runs.insert(runs.end(), {r, len, seq, pos0});
         if (len >= 8) long_rows += len;
         r += len;
     }
     return long_rows;
+}
+
+// The runs of rows [row_off, row_off + m) on the device (cut and uploaded
+// once per row-meta write).  Sets *n_runs; returns null when fewer than half
+// of the rows lie in runs of 8 or more (decode-shaped calls), which use the
+// row kernel instead.
+const uint32_t* device_runs(thb_pool* p, const thb_rows* rows, uint32_t row_off, uint32_t m, uint32_t max_run,
+                            hipStream_t s, uint32_t* n_runs) {
+    if (p->runs_rows != rows || p->runs_version != rows->version || p->runs_off != row_off || p->runs_m != m ||
+        p->runs_max != max_run) {
+        std::vector<uint32_t> runs;
+        p->runs_long = make_runs(rows->host.data() + 8 * static_cast<size_t>(row_off), m, max_run, runs);
+        p->runs_n = static_cast<uint32_t>(runs.size() / 4);
+        p->runs_rows = nullptr;  // invalid until the upload below is queued
+        if (2 * static_cast<uint64_t>(p->runs_long) >= m) {
+            void* dev = p->run_buf.reserve(runs.size() * 4, false);
+            p->stager.upload(dev, runs.data(), runs.size() * 4, s);
+        }
+        p->runs_rows = rows;
+        p->runs_version = rows->version;
+        p->runs_off = row_off;
+        p->runs_m = m;
+        p->runs_max = max_run;
+    }
+    *n_runs = p->runs_n;
+    return 2 * static_cast<uint64_t>(p->runs_long) >= m ? static_cast<const uint32_t*>(p->run_buf.get()) : nullptr;
 }
 
 int check_layer(const thb_pool* p, uint32_t layer) {
@@ -625,19 +684,14 @@ int thb_kv_store(thb_pool* pool, uint32_t layer, const void* k_src, const void* 
         const size_t esize = src_dtype == THB_DT_F32 ? 4 : 2;
         // Mostly long runs (prefill chunks): the run kernel writes whole V
         // page rows; otherwise (decode) one lane per 8 elements of a row.
-        std::vector<uint32_t> runs;
-        const uint32_t long_rows = make_runs(rows->host.data() + 8 * static_cast<size_t>(row_off), m,
-                                             pool->page_shift, runs);
-        if (2 * static_cast<uint64_t>(long_rows) >= m) {
-            const uint32_t n_runs = static_cast<uint32_t>(runs.size() / 4);
-            void* dev = pool->run_buf.reserve(runs.size() * 4, false);
-            pool->stager.upload(dev, runs.data(), runs.size() * 4, s);
+        uint32_t n_runs = 0;
+        if (const uint32_t* dev = device_runs(pool, rows, row_off, m, kRunTokens, s, &n_runs)) {
             RunArgs ra;
             ra.k_src = k_src;
             ra.v_src = v_src;
             ra.k = a.k;
             ra.v = a.v;
-            ra.runs = static_cast<const uint32_t*>(dev);
+            ra.runs = dev;
             ra.table = a.table;
             ra.plane = a.plane;
             ra.max_pages = a.max_pages;
@@ -838,10 +892,9 @@ int thb_kv_store_rope(thb_pool* pool, uint32_t layer, const void* k_src, const v
         a.m = m;
         a.rope = rope_dev(*rope, false);
         // Prefill chunks: V goes through the run kernel (whole page rows).
-        std::vector<uint32_t> runs;
-        const uint32_t long_rows = make_runs(rows->host.data() + 8 * static_cast<size_t>(row_off), m,
-                                             pool->page_shift, runs);
-        const bool by_runs = 2 * static_cast<uint64_t>(long_rows) >= m;
+        uint32_t n_runs = 0;
+        const uint32_t* run_dev = device_runs(pool, rows, row_off, m, kRunTokens, s, &n_runs);
+        const bool by_runs = run_dev != nullptr;
         a.do_v = by_runs ? 0u : 1u;
         a.seg_shift = seg_shift_for(g.head_dim);
         const uint64_t per_block = 4ull * (64u >> a.seg_shift);
@@ -852,15 +905,12 @@ int thb_kv_store_rope(thb_pool* pool, uint32_t layer, const void* k_src, const v
             launch_store_rope<THB_DT_F32>(pool->kv_dtype, grid, a, s);
         THB_HIP(hipGetLastError());
         if (by_runs) {
-            const uint32_t n_runs = static_cast<uint32_t>(runs.size() / 4);
-            void* dev = pool->run_buf.reserve(runs.size() * 4, false);
-            pool->stager.upload(dev, runs.data(), runs.size() * 4, s);
             RunArgs ra;
             ra.k_src = k_src;
             ra.v_src = v_src;
             ra.k = a.k;
             ra.v = a.v;
-            ra.runs = static_cast<const uint32_t*>(dev);
+            ra.runs = run_dev;
             ra.table = a.table;
             ra.plane = a.plane;
             ra.max_pages = a.max_pages;

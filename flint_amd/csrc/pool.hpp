@@ -70,7 +70,12 @@ struct thb_pool {
     thb::DevBuf copy_buf;            // copy triples
     thb::DevBuf geom_buf;            // per-layer DevLayer records
     thb::DevBuf partials;            // split-K partial results
-    thb::DevBuf run_buf;             // append runs of the last run-kernel call
+    thb::DevBuf run_buf;             // append runs of the last row meta the append cut into runs
+    // Key of run_buf's contents: the model appends the same rows to every
+    // layer, so the runs are cut and uploaded once per row-meta write.
+    const void* runs_rows = nullptr;
+    uint64_t runs_version = ~0ull;
+    uint32_t runs_off = 0, runs_m = 0, runs_max = 0, runs_n = 0, runs_long = 0;
     std::array<thb::AttnPlan, 4> plans;
     uint64_t plan_clock = 0;
     int device = 0;
