@@ -19,17 +19,18 @@
 //    Work items are launched longest first.
 //  * Scores come from MFMA: S^T[16 tokens x 16 columns] = K Q^T with
 //    v_mfma_f32_16x16x32_{f16,bf16}.  The A operand is 16 bytes of one key
-//    per lane; the pool keeps K pages chunk-major ([head_dim/8][page_len][8])
-//    so that one load instruction covers 1 KiB of contiguous memory.  The B
+//    per lane; the pool keeps K pages in 32-dimension groups ([head_dim/32]
+//    [page_len][32], layout.hpp) so that one load instruction covers 1 KiB of
+//    contiguous memory.  The B
 //    operand is Q^T held in registers.  Q is split into a high and a low
 //    half-precision part and both are multiplied, which keeps the products
 //    at f32 accuracy; the softmax scale is applied to the f32 scores.
 //  * S^T leaves lane (a, c) holding tokens 4a..4a+3 of column c.  That is
 //    exactly the B-operand layout of v_mfma_f32_16x16x16 for P^T, so the
 //    probabilities feed the PV product without any lane exchange.  The A
-//    operand is V^T: the pool stores V transposed inside each page
-//    ([head_dim][page_len]), so 4 consecutive tokens of one dimension are 8
-//    contiguous bytes.  P is split into high and low halves as well.
+//    operand is V^T: the pool stores V in 4-slot groups inside each page
+//    ([page_len/4][head_dim][4]), so 4 consecutive tokens of one dimension
+//    are 8 contiguous bytes.  P is split into high and low halves as well.
 //  * Online softmax per column with a lazy rescale (the running max moves
 //    only when a score beats it by more than 2^8).  The waves' states are
 //    merged through LDS in a fixed tree.  A group split over several
@@ -39,6 +40,7 @@
 #include <string>
 
 #include "codec.hpp"
+#include "layout.hpp"
 #include "pool.hpp"
 #include "rope.hpp"
 
@@ -424,10 +426,10 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     // hi - 1 of the row, and the only wave that ever loads it is the wave
     // whose run holds that position.  That wave encodes and stores the row's
     // K and V of this KV head (exactly as kv_store) before its first tile
-    // load; one wave's accesses to an address are ordered, so no barrier is
-    // needed.  Work item t of the group: row t / (2 cpr), K or V, 8-element
-    // chunk.  The first item of each lane is loaded before the barrier,
-    // under the latency of the query loads.
+    // load: the first item of each lane before the workgroup barrier (whose
+    // wait covers the stores), further items (more than 64) after it, where
+    // one wave's accesses to an address are ordered.  Work item t of the
+    // group: row t / (2 cpr), K or V, 8-element chunk.
     const uint32_t cpr = hd >> 3;
     const uint32_t app_items = a.k_src != nullptr ? R * 2 * cpr : 0u;
     constexpr uint32_t KVE = F16 ? THB_KV_F16_RNE : THB_KV_BF16_TRUNC;
@@ -439,29 +441,39 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
         e = (static_cast<uint64_t>(r0 + ar) * a.n_kvh + kvh) * hd + d;
         return pos >= ws && pos < we;
     };
-    auto app_store = [&](uint32_t pos, bool is_v, uint32_t d, const uint4& w) {
-        const uint64_t base = ((static_cast<uint64_t>(s_page[(pos - pbeg) >> pshift]) * hd + d) << pshift) +
-                              static_cast<uint64_t>(kvh) * a.plane;
+    auto app_store_at = [&](uint32_t page, uint32_t pos, bool is_v, uint32_t d, const uint4& w) {
+        const uint64_t base = ((static_cast<uint64_t>(page) * hd) << pshift) + static_cast<uint64_t>(kvh) * a.plane;
         if (!is_v) {
-            *reinterpret_cast<uint4*>(a.k + base + ((pos & pmask) << 3)) = w;
+            *reinterpret_cast<uint4*>(a.k + base + k_off(pos & pmask, d, hd, pshift)) = w;
         } else {
-            uint16_t* dst = a.v + base + (pos & pmask);
+            uint16_t* dst = a.v + base + v_off(pos & pmask, d, hd);  // dim d + e at + 4 e
             const uint32_t ws4[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
             for (int q2 = 0; q2 < 4; q2++) {
-                dst[static_cast<uint64_t>(2 * q2) << pshift] = static_cast<uint16_t>(ws4[q2] & 0xffffu);
-                dst[static_cast<uint64_t>(2 * q2 + 1) << pshift] = static_cast<uint16_t>(ws4[q2] >> 16);
+                dst[8 * q2] = static_cast<uint16_t>(ws4[q2] & 0xffffu);
+                dst[8 * q2 + 4] = static_cast<uint16_t>(ws4[q2] >> 16);
             }
         }
+    };
+    auto app_store = [&](uint32_t pos, bool is_v, uint32_t d, const uint4& w) {
+        app_store_at(s_page[(pos - pbeg) >> pshift], pos, is_v, d, w);
     };
     uint32_t app_pos = 0, app_d = 0;
     uint64_t app_e = 0;
     bool app_v = false, app_own = false;
-    uint4 app_w = make_uint4(0u, 0u, 0u, 0u);
     const bool rope = FULL && a.rope_on;
     if (lane < app_items && !rope) {
+        // First item of each lane, stored before the barrier: the barrier's
+        // wait for outstanding memory operations then covers the stores, which
+        // otherwise held up the owning wave's first tile waits (~1 us per
+        // store instruction).  The page comes straight from the block table
+        // (s_page is complete only after the barrier).
         app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
-        if (app_own) app_w = load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e);
+        if (app_own) {
+            const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (app_pos >> pshift)];
+            app_store_at(page, app_pos, app_v, app_d,
+                         load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e));
+        }
     }
     __syncthreads();
     if (rope) {
@@ -493,8 +505,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
             }
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         }
-    } else if (app_items != 0) {
-        if (app_own) app_store(app_pos, app_v, app_d, app_w);
+    } else if (app_items > 64) {
         for (uint32_t t = lane + 64; t < app_items; t += 64) {
             if (app_decode(t, app_pos, app_v, app_d, app_e))
                 app_store(app_pos, app_v, app_d,
@@ -514,28 +525,29 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     // Loads one 16-token tile.  Tokens outside [tb, te) are clamped into
     // it (their scores are masked), so every address is inside a page of
     // the sequence.
-    // K pages are [hd/8][page_len][8]: for a fixed k-step j the 64 lanes read
-    // 4 chunk rows x 16 tokens x 16 bytes, 1 KiB contiguous when page_len is
-    // 16.  The loads are non-temporal: every byte is read once.
+    // K pages hold 32-dimension groups ([hd/32][page_len][32]): for a fixed
+    // k-step j the 64 lanes read 16 tokens x 64 bytes, 1 KiB contiguous.  V
+    // pages hold 4-slot groups ([page_len/4][hd][4]): a lane's 4 slots of one
+    // dim are 8 bytes, and 16 lanes read 128 contiguous bytes.  The loads are
+    // non-temporal: every byte is read once.
     auto load = [&](uint32_t t0, u32x4 (&kr)[KS], u32x2 (&vr)[MT]) {
         const uint32_t tk = min(max(t0 + c, tb), last);
         const uint32_t kpage = s_page[(tk - pbeg) >> pshift];
-        const uint16_t* kbase = kplane + (static_cast<uint64_t>(kpage) * hd << pshift) + ((tk & pmask) << 3);
+        const uint16_t* kbase = kplane + (static_cast<uint64_t>(kpage) * hd << pshift);
 #pragma unroll
         for (int j = 0; j < KS; j++) {
             const uint32_t d0 = 32u * j + 8u * a4;
             kr[j] = d0 < hd ? __builtin_nontemporal_load(
-                                  reinterpret_cast<const u32x4*>(kbase + (static_cast<uint64_t>(d0) << pshift)))
+                                  reinterpret_cast<const u32x4*>(kbase + k_off(tk & pmask, d0, hd, pshift)))
                             : u32x4{0u, 0u, 0u, 0u};
         }
         const uint32_t tv = min(max(t0 + 4u * a4, tb & ~3u), last & ~3u);
         const uint32_t vpage = s_page[(tv - pbeg) >> pshift];
-        const uint16_t* vbase = vplane + (static_cast<uint64_t>(vpage) * hd << pshift) + (tv & pmask);
+        const uint16_t* vbase = vplane + (static_cast<uint64_t>(vpage) * hd << pshift) + v_off(tv & pmask, 0, hd);
 #pragma unroll
         for (int i = 0; i < MT; i++) {
             const uint32_t d = 16u * i + c;
-            vr[i] = d < hd ? __builtin_nontemporal_load(
-                                 reinterpret_cast<const u32x2*>(vbase + (static_cast<uint64_t>(d) << pshift)))
+            vr[i] = d < hd ? __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vbase + 4u * d))
                            : u32x2{0u, 0u};
         }
     };
@@ -696,9 +708,8 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
 // waves; each wave skips the 16-token slices outside its group's keys (the
 // causal triangle).  The per-slice arithmetic is the decode kernel's: split
 // Q and P, MFMA, online softmax with the lazy rescale.
-//   K tile in LDS: [TT/16 slices][HD/8 chunks][16 tokens] x 16 bytes, the
-//     order of a chunk-major page, so 8 lanes of an operand read are 128
-//     contiguous bytes.
+//   K tile in LDS: [TT/16 slices][HD/8 chunks][16 tokens] x 16 bytes, so 8
+//     lanes of an operand read are 128 contiguous bytes.
 //   V tile in LDS: [TT/16 slices][HD dims][4 groups of 4 tokens] x 8 bytes,
 //     the group index XOR-ed with (dim / 8) % 4 so that the 16 lanes of a
 //     PV operand read hit distinct banks.
@@ -781,19 +792,19 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
             const uint32_t page = s_page[(t - pbeg) >> pshift];
             const bool ok = u < static_cast<uint32_t>(KU) && 8u * ch < hd;
             kr[k] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                             kplane + ((static_cast<uint64_t>(page) * hd + 8u * ch) << pshift) + ((t & pmask) << 3)))
+                             kplane + ((static_cast<uint64_t>(page) * hd) << pshift) + k_off(t & pmask, 8u * ch, hd, pshift)))
                        : u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int k = 0; k < VPT; k++) {
+        for (int k = 0; k < VPT; k++) {  // unit: dims (d, d + 1) x 4-slot group g4 of a 16-token slice
             const uint32_t u = tid + k * NT;
             const uint32_t st = u / (2 * HD), rem = u - st * (2 * HD);
-            const uint32_t d = rem >> 1, h8 = rem & 1u;
-            const uint32_t t = min(max(t0 + 16u * st + 8u * h8, tb & ~7u), last & ~7u);
+            const uint32_t g4 = rem / (HD / 2), d = 2u * (rem - g4 * (HD / 2));
+            const uint32_t t = min(max(t0 + 16u * st + 4u * g4, tb & ~3u), last & ~3u);
             const uint32_t page = s_page[(t - pbeg) >> pshift];
             const bool ok = u < static_cast<uint32_t>(VU) && d < hd;
             vr[k] = ok ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                             vplane + ((static_cast<uint64_t>(page) * hd + d) << pshift) + (t & pmask)))
+                             vplane + ((static_cast<uint64_t>(page) * hd) << pshift) + v_off(t & pmask, d, hd)))
                        : u32x4{0u, 0u, 0u, 0u};
         }
     };
@@ -808,11 +819,10 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
             const uint32_t u = tid + k * NT;
             if (u >= static_cast<uint32_t>(VU)) continue;
             const uint32_t st = u / (2 * HD), rem = u - st * (2 * HD);
-            const uint32_t d = rem >> 1, h8 = rem & 1u;
-            const uint32_t sw = (d >> 3) & 3u;
-            u32x2* row4 = &s_v[buf][(st * HD + d) * 4];
-            row4[(2u * h8) ^ sw] = u32x2{vr[k].x, vr[k].y};
-            row4[(2u * h8 + 1u) ^ sw] = u32x2{vr[k].z, vr[k].w};
+            const uint32_t g4 = rem / (HD / 2), d = 2u * (rem - g4 * (HD / 2));
+            const uint32_t sw = (d >> 3) & 3u;  // the same for d and d + 1
+            s_v[buf][(st * HD + d) * 4 + (g4 ^ sw)] = u32x2{vr[k].x, vr[k].y};
+            s_v[buf][(st * HD + d + 1u) * 4 + (g4 ^ sw)] = u32x2{vr[k].z, vr[k].w};
         }
     };
 

@@ -1,16 +1,15 @@
 // KV append/scatter (kv_store), gather, scatter and page copy kernels.
 //
 // One lane owns 8 consecutive head_dim elements of one token of one head.
-// K pages are chunk-major ([head_dim / 8][page_len][8] per page), so a lane's
-// 8 K elements are one 16-byte vector.  V pages are transposed ([head_dim]
-// [page_len] per page, the operand layout of the attention kernel's PV
-// product), so the lane's 8 V elements are 8 16-bit accesses page_len
-// elements apart.  In both, element (slot s, dim d) of page p starts from
-// the offset (p * head_dim + d) * page_len.
+// Pages follow layout.hpp: K in 32-dimension groups ([hd/32][P][32]), so a
+// lane's 8 K elements are one 16-byte vector; V in 4-slot groups
+// ([P/4][hd][4], the operand layout of the attention kernel's PV product),
+// so the lane's 8 V elements are 8 16-bit accesses 8 bytes apart.
 #include <algorithm>
 #include <string>
 
 #include "codec.hpp"
+#include "layout.hpp"
 #include "pool.hpp"
 #include "rope.hpp"
 
@@ -45,20 +44,19 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
     const uint32_t h = c / cph, d = (c - h * cph) << 3;
     const uint64_t src_e = (static_cast<uint64_t>(row) * a.chunks + c) << 3;
     const uint4 w = load_encode8<SRC, KV>(is_v ? a.v_src : a.k_src, src_e);
+    const uint32_t j = pos & ((1u << a.page_shift) - 1u);
+    const uint64_t pbase = h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim) << a.page_shift);
     if (!is_v) {
-        *reinterpret_cast<uint4*>(a.k + h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + d) << a.page_shift) +
-                                  ((pos & ((1u << a.page_shift) - 1u)) << 3)) = w;
+        *reinterpret_cast<uint4*>(a.k + pbase + k_off(j, d, a.head_dim, a.page_shift)) = w;
         return;
     }
-    // V^T: element (slot, d + e) of the page lives at (page * hd + d + e) *
-    // page_len + slot % page_len.
-    uint16_t* dst = a.v + h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + d) << a.page_shift) +
-                    (pos & ((1u << a.page_shift) - 1u));
+    // V: element (j, d + e) at v_off(j, d, hd) + 4 e.
+    uint16_t* dst = a.v + pbase + v_off(j, d, a.head_dim);
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const uint32_t x = e == 0 ? w.x : e == 1 ? w.y : e == 2 ? w.z : w.w;
-        dst[static_cast<uint64_t>(2 * e) << a.page_shift] = static_cast<uint16_t>(x & 0xffffu);
-        dst[static_cast<uint64_t>(2 * e + 1) << a.page_shift] = static_cast<uint16_t>(x >> 16);
+        dst[8 * e] = static_cast<uint16_t>(x & 0xffffu);
+        dst[8 * e + 4] = static_cast<uint16_t>(x >> 16);
     }
 }
 
@@ -82,12 +80,10 @@ constexpr uint32_t kMaxRunPages = kRunTokens / 8 + 1;  // pages a run touches (p
 
 // Append of runs: consecutive rows of one sequence whose positions are
 // consecutive (a prefill chunk), up to kRunTokens tokens, across pages.  One
-// workgroup per (run, KV head).  K: the run's tokens of each chunk row are
-// contiguous 16-byte units within a page.  V: the encoded rows are staged in
-// LDS as [token][dim] (rows padded by one word, so the 8 tokens of a group
-// hit distinct banks) and written as the pages' [dim][token] rows, 8 tokens
-// (16 bytes) per store where a whole aligned group of 8 lies inside the run,
-// 2 bytes at its ends.
+// workgroup per (run, KV head).  K: one 16-byte store per (token, 8 dims).
+// V: the encoded rows are staged in LDS as [token][dim] and written as the
+// pages' 4-slot groups, 16 bytes (2 dims x 4 slots) per store where a whole
+// group lies inside the run, 2 bytes at its ends.
 template <uint32_t SRC, uint32_t KV>
 __global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
     extern __shared__ uint32_t s_run[];  // [len][head_dim + 2] 16-bit V slots
@@ -123,9 +119,7 @@ __global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
             const uint32_t u = u0 + 256 * i;
             if (u >= units) continue;
             const uint32_t ch = u / len, t = u - ch * len, pos = pos0 + t;
-            if (a.do_k)
-                *reinterpret_cast<uint4*>(a.k + page_base(pos) + (static_cast<uint64_t>(8u * ch) << shift) +
-                                          ((pos & mask) << 3)) = kw[i];
+            if (a.do_k) *reinterpret_cast<uint4*>(a.k + page_base(pos) + k_off(pos & mask, 8u * ch, hd, shift)) = kw[i];
             uint32_t* dst = s_run + t * rs + 4u * ch;
             dst[0] = vw[i].x;
             dst[1] = vw[i].y;
@@ -135,21 +129,30 @@ __global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
     }
     __syncthreads();
     const uint16_t* sv = reinterpret_cast<const uint16_t*>(s_run);
-    const uint32_t G0 = pos0 >> 3, ng = ((pos0 + len - 1) >> 3) - G0 + 1;  // aligned groups of 8 positions
-    for (uint32_t u = threadIdx.x; u < hd * ng; u += 256) {
-        const uint32_t d = u / ng, p8 = (G0 + (u - d * ng)) << 3;
-        uint16_t* dst = a.v + page_base(p8) + (static_cast<uint64_t>(d) << shift) + (p8 & mask);
-        if (p8 >= pos0 && p8 + 8 <= pos0 + len) {
+    const uint32_t S = hd + 2;                                               // LDS row stride (16-bit)
+    const uint32_t Q0 = pos0 >> 2, nq = ((pos0 + len - 1) >> 2) - Q0 + 1;  // aligned 4-slot groups
+    const uint32_t dpairs = hd >> 1;
+    // One 16-byte unit per lane: dims (d, d + 1) x the 4 slots of a group;
+    // consecutive lanes write consecutive units.
+    for (uint32_t u = threadIdx.x; u < dpairs * nq; u += 256) {
+        const uint32_t q = u / dpairs, d = 2u * (u - q * dpairs), p4 = (Q0 + q) << 2;
+        uint16_t* dst = a.v + page_base(p4) + v_off(p4 & mask, d, hd);
+        if (p4 >= pos0 && p4 + 4 <= pos0 + len) {
+            const uint32_t t = p4 - pos0;
             uint32_t w[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-                w[q] = static_cast<uint32_t>(sv[(p8 - pos0 + 2 * q) * 2 * rs + d]) |
-                       (static_cast<uint32_t>(sv[(p8 - pos0 + 2 * q + 1) * 2 * rs + d]) << 16);
+            for (int q2 = 0; q2 < 2; q2++)
+#pragma unroll
+                for (int h2 = 0; h2 < 2; h2++)
+                    w[2 * q2 + h2] = static_cast<uint32_t>(sv[(t + 2 * h2) * S + d + q2]) |
+                                     (static_cast<uint32_t>(sv[(t + 2 * h2 + 1) * S + d + q2]) << 16);
             *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
         } else {
-            for (uint32_t e = 0; e < 8; e++) {
-                const uint32_t p = p8 + e;
-                if (p >= pos0 && p < pos0 + len) dst[e] = sv[(p - pos0) * 2 * rs + d];
+            for (uint32_t e = 0; e < 4; e++) {
+                const uint32_t p = p4 + e;
+                if (p < pos0 || p >= pos0 + len) continue;
+                dst[e] = sv[(p - pos0) * S + d];
+                dst[4 + e] = sv[(p - pos0) * S + d + 1];
             }
         }
     }
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(256) void kv_store_rope_kernel(RopeStoreArgs a) {
     const uint32_t seq = a.meta[8 * row + 1];
     const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (pos >> a.page_shift)];
     const uint32_t j = pos & ((1u << a.page_shift) - 1u);
-    const uint64_t pbase = h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim + 8u * u) << a.page_shift);
+    const uint64_t pbase = h * a.plane + ((static_cast<uint64_t>(page) * a.head_dim) << a.page_shift);
     uint32_t w[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -201,15 +204,16 @@ __global__ __launch_bounds__(256) void kv_store_rope_kernel(RopeStoreArgs a) {
         else
             w[q] = conv32<KV>(__float_as_uint(x[2 * q])) | (conv32<KV>(__float_as_uint(x[2 * q + 1])) << 16);
     }
-    *reinterpret_cast<uint4*>(a.k + pbase + (j << 3)) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(a.k + pbase + k_off(j, 8u * u, a.head_dim, a.page_shift)) =
+        make_uint4(w[0], w[1], w[2], w[3]);
     if (!a.do_v) return;
     const uint4 vw = load_encode8<SRC, KV>(a.v_src, e);
-    uint16_t* dst = a.v + pbase + j;
+    uint16_t* dst = a.v + pbase + v_off(j, 8u * u, a.head_dim);
     const uint32_t vs[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        dst[static_cast<uint64_t>(2 * q) << a.page_shift] = static_cast<uint16_t>(vs[q] & 0xffffu);
-        dst[static_cast<uint64_t>(2 * q + 1) << a.page_shift] = static_cast<uint16_t>(vs[q] >> 16);
+        dst[8 * q] = static_cast<uint16_t>(vs[q] & 0xffffu);
+        dst[8 * q + 4] = static_cast<uint16_t>(vs[q] >> 16);
     }
 }
 
@@ -267,18 +271,11 @@ struct GatherArgs {
     uint32_t heads;  // KV heads per workgroup
 };
 
-// Byte offset in the V tile of dimension d, tile slot jj: rows of `tile`
-// 16-bit slots, and 16 bytes of padding after every 8 rows so that the lanes
-// of one token (consecutive 8-dimension chunks, 8 rows apart) hit distinct
-// LDS banks.
-__device__ inline uint32_t vtile_off(uint32_t d, uint32_t jj, uint32_t tile) {
-    return (d >> 3) * (16u * tile + 16u) + (d & 7u) * 2u * tile + 2u * jj;
-}
-
-// Copies 16 bytes from `src` to `dst` keeping the 16-bit slots of `dst`
-// outside [e0, e1) (a V page group of 8 tokens that the range cuts).
-__device__ inline void merge8(uint16_t* dst, const uint16_t* src, uint32_t e0, uint32_t e1) {
-    if (e0 == 0 && e1 == 8) {
+// Copies a 16-byte V unit (dims d, d + 1 x the 4 slots of a group; element
+// i is slot i % 4 of dim d + i / 4) from `src` to `dst`, keeping the slots
+// of `dst` outside [s0, s1) (a group that a range cuts).
+__device__ inline void merge_v16(uint16_t* dst, const uint16_t* src, uint32_t s0, uint32_t s1) {
+    if (s0 == 0 && s1 >= 4) {
         *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
         return;
     }
@@ -288,11 +285,16 @@ __device__ inline void merge8(uint16_t* dst, const uint16_t* src, uint32_t e0, u
     const uint32_t* nw = reinterpret_cast<const uint32_t*>(&n);
 #pragma unroll
     for (uint32_t e = 0; e < 8; e++) {
-        if (e < e0 || e >= e1) continue;
+        if ((e & 3u) < s0 || (e & 3u) >= s1) continue;
         const uint32_t sh = 16u * (e & 1u), mask = 0xffffu << sh;
         ow[e >> 1] = (ow[e >> 1] & ~mask) | (nw[e >> 1] & mask);
     }
     *reinterpret_cast<uint4*>(dst) = o;
+}
+
+// Copies 16 bytes of K (8 dims of one slot) from `src` to `dst` when keep.
+__device__ inline void copy16_if(uint16_t* dst, const uint16_t* src, bool keep) {
+    if (keep) *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
 }
 
 // 16-byte store with the non-temporal hint (the destination is not read
@@ -312,17 +314,19 @@ struct DivSmall {
 // Gather (TO_FLAT) or scatter (!TO_FLAT) of tokens [t0, t0 + n) of one
 // sequence.  One workgroup per (page of the range, group of `heads` KV
 // heads).  K: a token's 8-dimension chunk is 16 contiguous bytes on both
-// sides.  V: the page's [head_dim][page_len] rows go through an LDS tile of
-// up to 64 tokens per head and are read and written as 16-byte vectors on
-// both sides; a page group of 8 tokens that the range cuts is merged into
-// its 16 bytes by one lane.  A tile's K and V loads are issued together, two
-// of each per lane at a time.
+// sides.  V: a tile of up to 64 slots goes through LDS as [slot][dim]
+// (rows of head_dim + 8 elements, 16-byte aligned); the page side moves as
+// 16-byte units (2 dims x the 4 slots of a group), the flat side as 16-byte
+// (slot, 8 dims) vectors.  A group that the range cuts is merged into its
+// 16 bytes by one lane.  A tile's K and V loads are issued together, two of
+// each per lane at a time.
 template <bool TO_FLAT>
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     extern __shared__ uint4 s_tile[];
-    uint8_t* tile_b = reinterpret_cast<uint8_t*>(s_tile);
     const uint32_t shift = a.page_shift, hd = a.head_dim, cph = hd >> 3, T = a.tile;
-    const uint32_t tile_bytes = cph * (16u * T + 16u);
+    const uint32_t RS = hd + 8;                // LDS row stride (16-bit elements)
+    const uint32_t tile_elems = T * RS;
+    uint16_t* tile16 = reinterpret_cast<uint16_t*>(s_tile);
     const uint32_t pi = (a.t0 >> shift) + blockIdx.x, h0 = blockIdx.y * a.heads;
     const uint32_t p0 = pi << shift;
     const uint32_t ja = max(a.t0, p0) - p0;
@@ -334,20 +338,16 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     auto flat_off = [&](uint32_t hh, uint32_t j, uint32_t c) {
         return (static_cast<uint64_t>(h0 + hh) * a.n + p0 - a.t0 + j) * hd + 8u * c;
     };
-    auto k_paged = [&](uint32_t hh, uint32_t j, uint32_t c) {
-        return a.k + pbase(hh) + (static_cast<uint64_t>(8u * c) << shift) + (j << 3);
-    };
-    auto v_paged = [&](uint32_t hh, uint32_t d, uint32_t j) {
-        return a.v + pbase(hh) + (static_cast<uint64_t>(d) << shift) + j;
-    };
-    const DivSmall by_cph(cph);
+    auto k_paged = [&](uint32_t hh, uint32_t j, uint32_t c) { return a.k + pbase(hh) + k_off(j, 8u * c, hd, shift); };
+    auto v_paged = [&](uint32_t hh, uint32_t j4, uint32_t d) { return a.v + pbase(hh) + v_off(j4, d, hd); };
+    const DivSmall by_cph(cph), by_dp(hd >> 1);
     for (uint32_t tb = ja & ~(T - 1u); tb < jb; tb += T) {
         const uint32_t lo = max(ja, tb), hi = min(jb, tb + T);
-        const uint32_t g_lo = (lo - tb) >> 3, g_hi = (hi - tb + 7u) >> 3;  // groups the range touches
-        const uint32_t ng = g_hi - g_lo;
+        const uint32_t q_lo = (lo - tb) >> 2, q_hi = (hi - tb + 3u) >> 2;  // 4-slot groups the range touches
+        const uint32_t nq = q_hi - q_lo;
         const uint32_t n_tok = (hi - lo) * cph;  // K (and flat V) vectors of the tile, per head
-        const uint32_t n_grp = hd * ng;          // V page vectors of the tile, per head
-        const DivSmall by_ng(ng), by_tok(n_tok), by_grp(n_grp);
+        const uint32_t n_grp = (hd >> 1) * nq;   // V page units of the tile, per head
+        const DivSmall by_tok(n_tok), by_grp(n_grp);
         // vector u of the K (flat) side: head hh, token lo + t, chunk c
         auto split_tok = [&](uint32_t u, uint32_t& hh, uint32_t& t, uint32_t& c) {
             hh = by_tok(u);
@@ -355,12 +355,13 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
             t = by_cph(r);
             c = r - t * cph;
         };
-        // vector u of the V page side: head hh, dimension d, group g
-        auto split_grp = [&](uint32_t u, uint32_t& hh, uint32_t& d, uint32_t& g) {
+        // unit u of the V page side: head hh, group q (slots tb + 4q ..), dims d, d + 1
+        auto split_grp = [&](uint32_t u, uint32_t& hh, uint32_t& q, uint32_t& d) {
             hh = by_grp(u);
             const uint32_t r = u - hh * n_grp;
-            d = by_ng(r);
-            g = g_lo + r - d * ng;
+            const uint32_t qq = by_dp(r);
+            q = q_lo + qq;
+            d = 2u * (r - qq * (hd >> 1));
         };
         const uint32_t NT = a.heads * n_tok, NG = a.heads * n_grp;
         if constexpr (TO_FLAT) {
@@ -369,20 +370,27 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 #pragma unroll
                 for (uint32_t i = 0; i < 2; i++) {
                     const uint32_t u = u0 + 256 * i;
-                    uint32_t hh, t, c, d, g;
+                    uint32_t hh, t, c, q, d;
                     split_tok(u, hh, t, c);
                     if (u < NT) kr[i] = ld_stream16(k_paged(hh, lo + t, c));
-                    split_grp(u, hh, d, g);
-                    if (u < NG) vr[i] = ld_stream16(v_paged(hh, d, tb + 8u * g));
+                    split_grp(u, hh, q, d);
+                    if (u < NG) vr[i] = ld_stream16(v_paged(hh, tb + 4u * q, d));
                 }
 #pragma unroll
                 for (uint32_t i = 0; i < 2; i++) {
                     const uint32_t u = u0 + 256 * i;
-                    uint32_t hh, t, c, d, g;
+                    uint32_t hh, t, c, q, d;
                     split_tok(u, hh, t, c);
                     if (u < NT) st_stream16(a.k_flat + flat_off(hh, lo + t, c), kr[i]);
-                    split_grp(u, hh, d, g);
-                    if (u < NG) *reinterpret_cast<uint4*>(tile_b + hh * tile_bytes + vtile_off(d, 8u * g, T)) = vr[i];
+                    split_grp(u, hh, q, d);
+                    if (u < NG) {
+                        uint16_t* tl = tile16 + hh * tile_elems;
+                        const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+                        for (uint32_t e = 0; e < 8; e++)  // element e: slot e % 4 of dim d + e / 4
+                            tl[(4u * q + (e & 3u)) * RS + d + (e >> 2)] =
+                                static_cast<uint16_t>(w[e >> 1] >> (16u * (e & 1u)));
+                    }
                 }
             }
             __syncthreads();
@@ -390,15 +398,8 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
                 uint32_t hh, t, c;
                 split_tok(u, hh, t, c);
                 const uint32_t jj = lo - tb + t;
-                const uint8_t* tl = tile_b + hh * tile_bytes;
-                uint32_t w[4];
-#pragma unroll
-                for (uint32_t q = 0; q < 4; q++)
-                    w[q] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(tl + vtile_off(8u * c + 2u * q, jj, T))) |
-                           (static_cast<uint32_t>(
-                                *reinterpret_cast<const uint16_t*>(tl + vtile_off(8u * c + 2u * q + 1u, jj, T)))
-                            << 16);
-                st_stream16(a.v_flat + flat_off(hh, tb + jj, c), make_uint4(w[0], w[1], w[2], w[3]));
+                st_stream16(a.v_flat + flat_off(hh, tb + jj, c),
+                            *reinterpret_cast<const uint4*>(tile16 + hh * tile_elems + jj * RS + 8u * c));
             }
         } else {
             for (uint32_t u0 = threadIdx.x; u0 < NT; u0 += 512) {
@@ -420,23 +421,24 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
                     uint32_t hh, t, c;
                     split_tok(u, hh, t, c);
                     st_stream16(k_paged(hh, lo + t, c), kr[i]);
-                    uint8_t* tl = tile_b + hh * tile_bytes;
-                    const uint32_t jj = lo - tb + t;
-                    const uint32_t xw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-#pragma unroll
-                    for (uint32_t e = 0; e < 8; e++)
-                        *reinterpret_cast<uint16_t*>(tl + vtile_off(8u * c + e, jj, T)) =
-                            static_cast<uint16_t>(xw[e >> 1] >> (16u * (e & 1u)));
+                    *reinterpret_cast<uint4*>(tile16 + hh * tile_elems + (lo - tb + t) * RS + 8u * c) = vr[i];
                 }
             }
             __syncthreads();
             for (uint32_t u = threadIdx.x; u < NG; u += 256) {
-                uint32_t hh, d, g;
-                split_grp(u, hh, d, g);
-                const uint32_t j8 = tb + 8u * g;
-                merge8(v_paged(hh, d, j8),
-                       reinterpret_cast<const uint16_t*>(tile_b + hh * tile_bytes + vtile_off(d, 8u * g, T)),
-                       max(lo, j8) - j8, min(hi, j8 + 8u) - j8);
+                uint32_t hh, q, d;
+                split_grp(u, hh, q, d);
+                const uint32_t j4 = tb + 4u * q;
+                const uint16_t* tl = tile16 + hh * tile_elems;
+                uint32_t w[4];
+#pragma unroll
+                for (uint32_t e2 = 0; e2 < 4; e2++) {  // words: (slot 2(e2%2), +1) of dim d + e2 / 2
+                    const uint32_t sl = 4u * q + 2u * (e2 & 1u), dd = d + (e2 >> 1);
+                    w[e2] = static_cast<uint32_t>(tl[sl * RS + dd]) | (static_cast<uint32_t>(tl[(sl + 1u) * RS + dd]) << 16);
+                }
+                const uint4 unit = make_uint4(w[0], w[1], w[2], w[3]);
+                merge_v16(v_paged(hh, j4, d), reinterpret_cast<const uint16_t*>(&unit), max(lo, j4) - j4,
+                          min(hi, j4 + 4u) - j4);
             }
         }
         __syncthreads();
@@ -475,8 +477,8 @@ __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
         dst = a.inl[3 * blockIdx.x + 1];
         ntok = a.inl[3 * blockIdx.x + 2];
     }
-    const uint32_t shift = a.page_shift, P = 1u << shift, gpr = P >> 3;  // V groups per dim row
-    const uint32_t vecs = (L.head_dim << shift) >> 3;                      // 16-byte vectors per page plane
+    const uint32_t shift = a.page_shift, P = 1u << shift, hd = L.head_dim;
+    const uint32_t vecs = (hd << shift) >> 3;  // 16-byte vectors per page plane
     const uint64_t page_elems = static_cast<uint64_t>(L.head_dim) << shift;
     const uint16_t* base = reinterpret_cast<const uint16_t*>(a.mem + (which ? L.v_off : L.k_off)) +
                            static_cast<uint64_t>(h) * a.pool_len * L.head_dim;
@@ -495,12 +497,14 @@ __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
         return;
     }
     for (uint32_t u = threadIdx.x; u < vecs; u += 256) {
-        if (which == 0) {  // K: vector u = chunk row u / P, token u % P
-            if ((u & (P - 1u)) < ntok)
-                *reinterpret_cast<uint4*>(dp + 8u * u) = *reinterpret_cast<const uint4*>(sp + 8u * u);
-        } else {  // V: vector u = dim u / gpr, tokens 8 * (u % gpr) + [0, 8)
-            const uint32_t j8 = 8u * (u & (gpr - 1u));
-            if (j8 < ntok) merge8(dp + 8u * u, sp + 8u * u, 0, min(ntok - j8, 8u));
+        const uint32_t e = 8u * u;
+        if (which == 0) {  // K: element e of group g (32 P elements before it), slot (e - 32 P g) / width
+            const uint32_t g = e / (32u * P);
+            const uint32_t j = (e - 32u * P * g) / k_group_width(hd, 32u * g);
+            copy16_if(dp + e, sp + e, j < ntok);
+        } else {  // V: the unit's 4-slot group q (4 hd elements per group)
+            const uint32_t q = e / (4u * hd);
+            if (4u * q < ntok) merge_v16(dp + e, sp + e, 0, ntok - 4u * q);
         }
     }
 }
@@ -751,14 +755,14 @@ static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t 
         a.head_dim = g.head_dim;
         a.n = n;
         a.t0 = t0;
-        // V tile: up to 64 tokens of every dimension, at most 32 KiB of LDS
-        // per head.  Heads per workgroup: enough for 4 KiB of K per page
+        // V tile: up to 64 slots x (head_dim + 8) elements, at most 32 KiB of
+        // LDS per head.  Heads per workgroup: enough for 4 KiB of K per page
         // (small pages), at most 4, within 64 KiB of LDS.  More heads per
         // workgroup serialise load rounds and measured slower at 4 KiB pages.
         uint32_t tile = std::min(pool->page_len, 64u);
-        while (tile > 8 && (g.head_dim / 8) * (16 * tile + 16) > 32768) tile >>= 1;
+        while (tile > 4 && tile * (g.head_dim + 8) * 2 > 32768) tile >>= 1;
         a.tile = tile;
-        const size_t tile_bytes = static_cast<size_t>(g.head_dim / 8) * (16 * tile + 16);
+        const size_t tile_bytes = static_cast<size_t>(tile) * (g.head_dim + 8) * 2;
         const uint32_t want = std::min<uint32_t>(4, std::max<uint32_t>(1, 2048 / (pool->page_len * g.head_dim)));
         uint32_t heads = 1;
         for (uint32_t hpw = want; hpw > 1; hpw--)

@@ -3,9 +3,10 @@
 // Device layout: one allocation holds, for every layer, K then V, each
 // [kv_heads, pages, <page>] 16-bit words: the elements of the reference's
 // KvPool planes [kv_heads, pool_len, head_dim] (crates/thuban_model/src/
-// pool.rs:131-153) with each page reordered for the attention kernel.  A K
-// page is chunk-major, [head_dim / 8][page_len][8]; a V page is transposed,
-// [head_dim][page_len].  Every plane is aligned to 256 bytes.
+// pool.rs:131-153) with each page reordered for the attention kernel
+// (layout.hpp): K in 32-dimension groups, [head_dim / 32][page_len][32]; V
+// in 4-slot groups, [page_len / 4][head_dim][4].  Every plane is aligned to
+// 256 bytes.
 // The block table [seqs * max_pages] u32 lives in its own allocation and is
 // shared by all layers.
 #include <algorithm>

@@ -218,16 +218,33 @@ class KvPool:
 
     def layer_tensors(self, layer: int):
         """torch views (16-bit words, no copy) of the layer's device planes as
-        stored: K pages chunk-major [kv_heads, pages, head_dim/8, page_len,
-        8], V pages transposed [kv_heads, pages, head_dim, page_len]."""
+        stored, one flat page per row: [kv_heads, pages, page_len * head_dim]
+        (the element order inside a page is page_offsets())."""
         import torch
 
         info = self.layer_info(layer)
         k, v = self.layer_ptrs(layer)
         pages = info.pool_len // info.page_len
-        hd, P = info.head_dim, info.page_len
-        return (_device_view(k, (info.kv_heads, pages, hd // 8, P, 8), torch.int16),
-                _device_view(v, (info.kv_heads, pages, hd, P), torch.int16))
+        n = info.page_len * info.head_dim
+        return (_device_view(k, (info.kv_heads, pages, n), torch.int16),
+                _device_view(v, (info.kv_heads, pages, n), torch.int16))
+
+    @staticmethod
+    def page_offsets(page_len: int, head_dim: int):
+        """Offsets of element (slot j, dim d) inside a K and a V page, as
+        numpy arrays [page_len, head_dim] (THB_PAGE_LAYOUT_MFMA of
+        include/thuban_hip.h): K in 32-dimension groups, group g of width
+        w = min(32, head_dim - 32 g) at 32 P g + w j + d % 32; V in 4-slot
+        groups at (j / 4) 4 head_dim + 4 d + j % 4."""
+        import numpy as np
+
+        j = np.arange(page_len)[:, None]
+        d = np.arange(head_dim)[None, :]
+        g0 = d & ~31
+        w = np.minimum(32, head_dim - g0)
+        k = g0 * page_len + w * j + (d & 31)
+        v = (j >> 2) * (4 * head_dim) + 4 * d + (j & 3)
+        return k.astype(np.int64), v.astype(np.int64)
 
     def read_layer(self, layer: int):
         """Host copies (numpy uint16) of the layer's K and V in the
@@ -238,10 +255,12 @@ class KvPool:
         k, v = self.layer_tensors(layer)
         torch.cuda.synchronize()
         info = self.layer_info(layer)
-        shape = (info.kv_heads, info.pool_len, info.head_dim)
-        kn = k.cpu().numpy().view("uint16").transpose(0, 1, 3, 2, 4).reshape(shape)
-        vn = v.cpu().numpy().view("uint16").transpose(0, 1, 3, 2).reshape(shape)
-        return kn.copy(), vn.copy()
+        P, hd = info.page_len, info.head_dim
+        ko, vo = self.page_offsets(P, hd)
+        shape = (info.kv_heads, info.pool_len, hd)
+        kn = k.cpu().numpy().view("uint16")[..., ko.reshape(-1)].reshape(shape)
+        vn = v.cpu().numpy().view("uint16")[..., vo.reshape(-1)].reshape(shape)
+        return kn, vn
 
     def write_layer(self, layer: int, k_words, v_words) -> None:
         """Uploads K and V words given in the reference layout [kv_heads,
@@ -252,13 +271,12 @@ class KvPool:
         info = self.layer_info(layer)
         k, v = self.layer_tensors(layer)
         pages = info.pool_len // info.page_len
-        hd, P = info.head_dim, info.page_len
-        kw = np.ascontiguousarray(np.asarray(k_words, np.uint16).reshape(
-            info.kv_heads, pages, P, hd // 8, 8).transpose(0, 1, 3, 2, 4))
-        vw = np.ascontiguousarray(np.asarray(v_words, np.uint16).reshape(
-            info.kv_heads, pages, P, hd).transpose(0, 1, 3, 2))
-        k.copy_(torch.from_numpy(kw.view(np.int16)))
-        v.copy_(torch.from_numpy(vw.view(np.int16)))
+        P, hd = info.page_len, info.head_dim
+        ko, vo = self.page_offsets(P, hd)
+        for dev, words, off in ((k, k_words, ko), (v, v_words, vo)):
+            flat = np.empty((info.kv_heads, pages, P * hd), np.uint16)
+            flat[..., off.reshape(-1)] = np.asarray(words, np.uint16).reshape(info.kv_heads, pages, P * hd)
+            dev.copy_(torch.from_numpy(flat.view(np.int16)))
         torch.cuda.synchronize()
 
     def block_table_tensor(self):

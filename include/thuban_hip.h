@@ -54,7 +54,7 @@ extern "C" {
 const char* thb_last_error(void);
 /* ABI revision of this header. */
 uint32_t thb_abi_version(void);
-#define THB_ABI_VERSION 4u
+#define THB_ABI_VERSION 5u
 
 /* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90):
  * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]".  This backend also needs
@@ -116,12 +116,14 @@ int thb_arena_take_copies(thb_arena* arena, uint32_t* triples, size_t cap, uint3
  * reference's KvPool tensors [kv_heads, pages * page_len, head_dim]
  * (pool.rs:131-153) with every page reordered for the attention kernel's
  * matrix-core operands (THB_PAGE_LAYOUT_MFMA).  With P = page_len, page
- * base B = (h * pages + s / P) * head_dim * P and j = s % P, element
- * (head h, slot s, dim d) sits at
- *   K: B + (d / 8) * P * 8 + j * 8 + d % 8   (chunk-major [head_dim/8][P][8])
- *   V: B + d * P + j                           (transposed   [head_dim][P])
- * thb_kv_gather returns both in the reference's token-major layout. */
-#define THB_PAGE_LAYOUT_MFMA 1u
+ * base B = (h * pages + s / P) * head_dim * P, j = s % P, g0 = d - d % 32
+ * and w = min(32, head_dim - g0), element (head h, slot s, dim d) sits at
+ *   K: B + g0 * P + w * j + d % 32               ([head_dim/32][P][32] groups)
+ *   V: B + (j / 4) * 4 * head_dim + 4 * d + j % 4  ([P/4][head_dim][4] groups)
+ * so a token appended to a page dirties head_dim / 32 K and head_dim / 16 V
+ * cache lines.  thb_kv_gather returns both in the reference's token-major
+ * layout. */
+#define THB_PAGE_LAYOUT_MFMA 2u
 typedef struct thb_pool thb_pool;
 
 typedef struct thb_pool_desc {

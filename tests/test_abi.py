@@ -36,7 +36,7 @@ def test_abi_version_and_struct_layouts(tmp_path):
 
     from flint_amd import _lib
 
-    assert _lib.lib().thb_abi_version() == _lib.ABI_VERSION == 4
+    assert _lib.lib().thb_abi_version() == _lib.ABI_VERSION == 5
     structs = {"thb_pool_desc": _lib.PoolDesc, "thb_attn_spec": _lib.AttnSpecC,
                "thb_layer_info": _lib.LayerInfo, "thb_arena_info": _lib.ArenaInfo, "thb_rope": _lib.RopeC,
                "thb_attn_io": _lib.AttnIoC}
@@ -78,3 +78,35 @@ def test_product_does_not_reference_the_oracle():
                 with open(os.path.join(base, fn)) as f:
                     src = f.read()
                 assert "oracle" not in src.lower(), os.path.join(base, fn)
+
+
+def test_page_offsets_match_the_kernels_layout(tmp_path):
+    """KvPool.page_offsets (the host-side conversion used by read_layer /
+    write_layer) and flint_amd/csrc/layout.hpp (what every kernel uses) give
+    the same offset for every (slot, dim) at several page lengths and head
+    dims, and each is a permutation of the page."""
+    import subprocess
+
+    import numpy as np
+
+    from flint_amd.pool import KvPool
+
+    shapes = [(8, 64), (16, 128), (16, 80), (32, 200), (64, 512)]
+    src = tmp_path / "offsets.cpp"
+    src.write_text('#include <cstdio>\n#include "layout.hpp"\nint main() {\n' + "".join(
+        f"for (unsigned j = 0; j < {P}; j++) for (unsigned d = 0; d < {hd}; d++) "
+        f'std::printf("%llu %llu\\n", (unsigned long long)thb::k_off(j, d, {hd}, {P.bit_length() - 1}), '
+        f"(unsigned long long)thb::v_off(j, d, {hd}));\n" for P, hd in shapes) + "return 0; }\n")
+    exe = tmp_path / "offsets"
+    subprocess.run(["g++", "-std=c++17", "-D__host__=", "-D__device__=", "-I",
+                    os.path.join(ROOT, "flint_amd", "csrc"), str(src), "-o", str(exe)], check=True)
+    got = np.array([list(map(int, line.split())) for line in
+                    subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines()])
+    i = 0
+    for P, hd in shapes:
+        k, v = KvPool.page_offsets(P, hd)
+        n = P * hd
+        assert np.array_equal(got[i:i + n, 0], k.reshape(-1)), (P, hd)
+        assert np.array_equal(got[i:i + n, 1], v.reshape(-1)), (P, hd)
+        assert np.array_equal(np.sort(k.reshape(-1)), np.arange(n)) and np.array_equal(np.sort(v.reshape(-1)), np.arange(n))
+        i += n
