@@ -459,9 +459,9 @@ struct CopyArgs {
 // Copy of slots [0, ntok) of one (page, head, K or V) plane of one layer.
 // Grid: (n_triples, layers * 2 * kv_heads), plane fastest.  Every access is
 // a 16-byte vector: a whole page is one contiguous run (4 vectors in flight
-// per lane); of a partial page, a K chunk row moves its first ntok chunks
-// and a V dimension row its first ntok 16-bit slots, the group of 8 that
-// ntok cuts merged by one lane.
+// per lane); of a partial page, each K group moves the 16-byte pieces of its
+// first ntok slots, and V its first ceil(ntok / 4) 4-slot groups, the group
+// that ntok cuts merged slot by slot.
 __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
     const uint32_t planes = 2 * a.kv_heads;
     const uint32_t layer = blockIdx.y / planes, plane = blockIdx.y - layer * planes;
