@@ -441,6 +441,14 @@ def run_secondary(args):
             for layer in range(L):
                 ops.kv_store_attn(k, v, q, pool, layer, y, specs[layer])
         us = _time_steps(torch, step, args.steps, args.warmup) / L
+        for kind, first in (("window", 0), ("global", 1)):
+            def half_step(first=first):
+                for layer in range(first, L, 2):
+                    ops.kv_store_attn(k, v, q, pool, layer, y, specs[layer])
+            lus = _time_steps(torch, half_step, args.steps, args.warmup) / (L // 2)
+            keys = 4096 + 4 if kind == "window" else ctx + 4
+            lb = B * keys * nkv * hd * 2 * 2 + m * nkv * hd * 2 * 2
+            out[f"{kind}_layer"] = {"us": round(lus, 1), "pct_of_peak": round(100 * lb / (lus * 1e3) / PEAK_HBM_GBPS, 1)}
         byts = B * (4096 + ctx + 8) // 2 * nkv * hd * 2 * 2 + m * nkv * hd * 2 * 2
         out["config"] = {"workload": "gemma2-9b C4: B=16 at ctx 8192, 16q/8kv/hd256, soft-cap 50, layers alternate "
                                      "window 4096 / global; step = append 4 drafts + 4-row causal verify (fused), "

@@ -10,7 +10,10 @@
 //    of one sequence x H query heads of one KV head.  Every K/V byte of a
 //    group is loaded once for all of its query vectors (GQA packing).
 //  * A group's key span (from its first key rounded down to the page and tile
-//    size) is cut into n = ceil(span / part_len) equal partitions.  One
+//    size) is cut into n equal partitions, n = ceil(span / part_len) rounded
+//    up to a power of two (so that groups of similar spans tile the 256 CUs
+//    evenly: 3 partitions per group on 128 groups leave half the CUs idle
+//    for the last third of the launch, 4 do not).  One
 //    workgroup of W waves handles one (group, partition, KV head); the waves
 //    split the partition into W contiguous runs of 16-token tiles.  All
 //    boundaries depend only on the group's own key range, so a row's
@@ -1060,14 +1063,16 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
 
     // Partitions of a group (or of a prefill block) start at its first key
     // (rounded down to the page and tile size) and split its span into
-    // n = ceil(span / part_len) equal parts: a function of its own key range
-    // only.
+    // n equal parts, n = ceil(span / part_len) rounded up to a power of two
+    // (then lowered if the aligned part length leaves trailing parts empty):
+    // a function of its own key range only.
     std::vector<uint32_t> groups, items, blocks, bitems;
     const uint32_t PL = pool->part_len;
     const uint32_t align = std::max<uint32_t>(pool->page_len, 16);
     const uint32_t hd_t = template_hd(hd);
     const uint32_t WB = static_cast<uint32_t>(hd_t >= 256 ? 4 : 8);  // waves of attn_prefill
     uint32_t max_parts = 0;
+    uint64_t max_span = 0;
     bool any_split = false;
     auto partition = [&](uint32_t& lo, uint32_t& hi, uint32_t& base, uint32_t& n_parts, uint32_t& plen) {
         base = 0;
@@ -1078,8 +1083,11 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         } else {
             base = lo & ~(align - 1);
             const uint64_t span = uint64_t(hi) - base;
+            max_span = std::max(max_span, span);
             n_parts = static_cast<uint32_t>((span + PL - 1) / PL);
+            if (n_parts > 1) n_parts = 1u << (32 - __builtin_clz(n_parts - 1));
             plen = static_cast<uint32_t>(((span + n_parts - 1) / n_parts + align - 1) / align * align);
+            n_parts = static_cast<uint32_t>((span + plen - 1) / plen);
         }
         max_parts = std::max(max_parts, n_parts);
         any_split = any_split || n_parts > 1;
@@ -1134,8 +1142,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         }
     }
     if (max_parts > kMaxParts)
-        return fail(THB_ERR_CONFIG, "context of " + std::to_string(static_cast<uint64_t>(max_parts) * PL) +
-                                        " tokens exceeds " + std::to_string(kMaxParts) + " partitions of " +
+        return fail(THB_ERR_CONFIG, "key span of " + std::to_string(max_span) + " tokens exceeds " + std::to_string(kMaxParts) + " partitions of " +
                                         std::to_string(PL) + " tokens");
     const uint32_t n_groups = static_cast<uint32_t>(groups.size() / kGroupWords);
     const uint32_t n_blocks = static_cast<uint32_t>(blocks.size() / kBlockWords);
