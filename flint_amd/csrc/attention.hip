@@ -463,22 +463,27 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     };
     uint32_t app_pos = 0, app_d = 0;
     uint64_t app_e = 0;
-    bool app_v = false, app_own = false;
+    bool app_v = false, app_own = false, app_late = false;
+    uint4 app_w = make_uint4(0u, 0u, 0u, 0u);
     const bool rope = FULL && a.rope_on;
-    if (lane < app_items && !rope) {
-        // First item of each lane, stored before the barrier: the barrier's
-        // wait for outstanding memory operations then covers the stores, which
-        // otherwise held up the owning wave's first tile waits (~1 us per
-        // store instruction).  The page comes straight from the block table
-        // (s_page is complete only after the barrier).
-        app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
-        if (app_own) {
-            const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (app_pos >> pshift)];
-            app_store_at(page, app_pos, app_v, app_d,
-                         load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e));
+    // First item of each lane: which lane owns one is known before the
+    // barrier (its position load runs beside the query loads), but its
+    // source is loaded after it, so the barrier's wait does not take a second
+    // round trip.  The source load then completes beside the first tile
+    // loads.  When the token lies beyond the wave's first NB tiles, the store
+    // is issued after those tiles' loads (below): a wave's waits for loads
+    // issued after a store also wait for the store, which is acknowledged
+    // long after it is issued.  Otherwise it is stored before any tile load.
+    if (lane < app_items && !rope) app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
+    __syncthreads();
+    if (app_own) {
+        app_w = load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e);
+        app_late = app_pos >= ws + 16u * NB;
+        if (!app_late) {
+            app_store(app_pos, app_v, app_d, app_w);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         }
     }
-    __syncthreads();
     if (rope) {
         if (app_items != 0) {
             // Rotary append: the key head of each row this wave owns, one chunk
@@ -510,9 +515,11 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
         }
     } else if (app_items > 64) {
         for (uint32_t t = lane + 64; t < app_items; t += 64) {
-            if (app_decode(t, app_pos, app_v, app_d, app_e))
-                app_store(app_pos, app_v, app_d,
-                          load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e));
+            uint32_t pos2, d2;
+            uint64_t e2;
+            bool v2;
+            if (app_decode(t, pos2, v2, d2, e2))
+                app_store(pos2, v2, d2, load_encode8_rt<KVE>(a.src_dtype, v2 ? a.v_src : a.k_src, e2));
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
@@ -602,6 +609,12 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 #pragma unroll
         for (int b = 0; b < NB; b++)
             if (ws + 16u * b < we) load(ws + 16u * b, kr[b], vr[b]);
+        // The token lies at or beyond tile NB of this wave: no load issued so
+        // far reads it, and every later load of it follows this store.
+        if (app_late) {
+            app_store(app_pos, app_v, app_d, app_w);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        }
         for (uint32_t t0 = ws; t0 < we; t0 += 16u * NB) {
 #pragma unroll
             for (int b = 0; b < NB; b++) {
