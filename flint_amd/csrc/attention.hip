@@ -40,6 +40,7 @@
 //    partitions writes (m, l, o) per partition and a second kernel merges
 //    them in partition order; there are no device-wide fences or atomics.
 #include <algorithm>
+#include <cmath>
 #include <string>
 
 #include "codec.hpp"
@@ -163,6 +164,11 @@ struct Ops<true> {
     __device__ static f32x4 pv(const u32x2& v, const in4& p, f32x4 acc) {
         return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(in4, v), p, acc, 0, 0, 0);
     }
+    // PV over 32 tokens: 8 tokens of one dimension (A) against 8 probabilities
+    // of one column (B).
+    __device__ static f32x4 pv32(const u32x4& v, const in8& p, f32x4 acc) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(in8, v), p, acc, 0, 0, 0);
+    }
     __device__ static void split4(const float* p, in4& h, in4& l) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -196,6 +202,9 @@ struct Ops<false> {
     }
     __device__ static f32x4 pv(const u32x2& v, const in4& p, f32x4 acc) {
         return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(in4, v), p, acc, 0, 0, 0);
+    }
+    __device__ static f32x4 pv32(const u32x4& v, const in8& p, f32x4 acc) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(in8, v), p, acc, 0, 0, 0);
     }
     __device__ static void split4(const float* p, in4& h, in4& l) {
 #pragma unroll
@@ -270,15 +279,17 @@ __device__ inline void store_y(const AttnArgs& a, uint32_t row, uint32_t head, u
 }
 
 // Q^T operand of a lane: column (row, head), dims 32j + 8 a4 .. + 8 of k-step
-// j, split into high and low halves.  The raw query is split and the f32
-// scores are scaled afterwards, so the low half stays out of the f16
-// subnormal range.  In the FULL kernels: query heads q_stride apart and,
+// j, split into high and low halves.  The decode kernels split the raw query
+// and scale the f32 scores afterwards, so the low half stays out of the f16
+// subnormal range; the prefill kernel passes pre = the score scale instead
+// (|pre| <= 1), which moves one multiply per score out of its inner loop at a
+// cost of ~1e-7 in the scores.  In the FULL kernels: query heads q_stride apart and,
 // with rope on, the query head is first normalised (q_norm; the four lanes
 // of the column add their sums of squares) and rotated at the row's
 // position.  Every lane must call it (column sums).
 template <int KS, class O, bool FULL>
 __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_t head, uint32_t a4,
-                              typename O::in8 (&qh)[KS], typename O::in8 (&ql)[KS]) {
+                              typename O::in8 (&qh)[KS], typename O::in8 (&ql)[KS], float pre = 1.0f) {
     const uint32_t hd = a.head_dim;
     const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * (FULL ? a.q_stride : hd);
     const bool rope = FULL && a.rope_on;
@@ -293,6 +304,8 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
 #pragma unroll
                 for (int e = 0; e < 8; e++) x[e] = 0.0f;
             }
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] *= pre;
             O::split8(x, qh[j], ql[j]);
         }
         return;
@@ -353,7 +366,11 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
         }
     }
 #pragma unroll
-    for (int j = 0; j < KS; j++) O::split8(x[j], qh[j], ql[j]);
+    for (int j = 0; j < KS; j++) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[j][e] *= pre;
+        O::split8(x[j], qh[j], ql[j]);
+    }
 }
 
 // One (group, partition, KV head) per workgroup of W waves.  NB tiles of
@@ -941,6 +958,359 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
     }
 }
 
+// Chunked prefill at head_dim <= 128 (attn_prefill serves wider heads).  One
+// workgroup of W waves handles a block of up to 2W consecutive groups of one
+// chunk, for one KV head and one partition of the block's key span.  Wave w
+// owns groups g0 + 2w and g0 + 2w + 1 (32 query columns), so every K and V
+// operand read from LDS feeds four matrix-core products (two column groups,
+// high and low halves).  Keys advance 32 at a time:
+//  * QK^T: two 16-token products per column group (S^T[16 tok x 16 col],
+//    v_mfma_f32_16x16x32), which leave lane (a, c) with tokens 4a..4a+3 of
+//    each half;
+//  * PV: one v_mfma_f32_16x16x32 per 16 dims over all 32 tokens.  Its B
+//    operand (8 probabilities of one column) is the lane's two score
+//    quadruples, so its k index runs over tokens {4a..4a+3, 16+4a..16+4a+3};
+//    the A operand (V^T) is read from LDS in that same token order.
+// K and V tiles of 64 tokens are double-buffered in LDS and shared by all
+// waves; the next tile's global loads are in flight during the compute.
+// They are ordinary cached loads: the blocks of a chunk read the same keys
+// (one KV head's blocks run on one XCD, whose L2 keeps them), where the
+// streaming hint of the decode kernels sent every tile to HBM.
+//   K tile: [4 slices of 16][HD/8 chunks][16 tokens] x 16 bytes (as attn_prefill).
+//   V tile: [2 steps of 32][HD dims][4 lane groups] x 16 bytes.  Entry
+//     (s, d, a) holds dim d of tokens 32s + 4a..+3 and 32s + 16 + 4a..+3; the
+//     lane-group index is XOR-ed with (d / 4) % 4, so the 16 lanes of an
+//     operand read hit distinct banks.
+#ifndef THB_PREFILL_TILE
+#define THB_PREFILL_TILE 64
+#endif
+template <int HD, bool F16, int W, bool FULL, bool CAP>
+__global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
+    using O = Ops<F16>;
+    typedef typename O::in8 in8;
+    constexpr int KS = HD / 32;
+    constexpr int MT = HD / 16;
+    constexpr int NCG = 2;                 // column groups per wave
+    // Probabilities with an f16 KV: one f16 operand (relative error <= 2^-12,
+    // so each output moves by at most 2^-12 max|v - y|).  With bf16 (8 bits)
+    // they keep the high + low split of the decode kernels.
+    constexpr bool PLO = !F16;
+    constexpr int TT = THB_PREFILL_TILE;   // tokens per tile
+    constexpr int NS = TT / 32;            // 32-token steps per tile
+    constexpr int CPH = HD / 8;            // 8-dim chunks of a key
+    constexpr int KU = TT * HD / 8;        // 16-byte K units per tile
+    constexpr int VE = NS * HD * 4;        // 16-byte V entries per tile
+    constexpr int VP = NS * 4 * (HD / 2);  // V load units (step, lane group, dim pair): two loads each
+    constexpr int NT = 64 * W;
+    constexpr int KPT = (KU + NT - 1) / NT;
+    constexpr int VPT = (VP + NT - 1) / NT;
+
+    __shared__ u32x4 s_k[2][KU];
+    __shared__ u32x4 s_v[2][VE];
+    __shared__ uint32_t s_page[kMaxPartPages];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t a4 = lane >> 4, c = lane & 15u;
+    const uint32_t bitem = blockIdx.x / a.n_kvh, kvh = blockIdx.x - bitem * a.n_kvh;
+
+    const uint32_t* Bk = a.blocks + a.bitems[bitem] * kBlockWords;
+    const uint32_t g0 = Bk[0], ng = Bk[1], seq = Bk[2], blo = Bk[3], bhi = Bk[4];
+    const uint32_t n_parts = Bk[5], bbase = Bk[6], P = Bk[7], bitem0 = Bk[8];
+    const uint32_t part = bitem - bitem0;
+    const uint32_t pbeg = bbase + part * P;
+    const uint32_t tb = max(blo, pbeg), te = min(bhi, pbeg + P);
+    const uint32_t hd = a.head_dim;
+    const uint32_t pshift = a.page_shift;
+    const uint32_t pmask = (1u << pshift) - 1u;
+    const uint32_t last = te > 0 ? te - 1 : 0;
+
+    {
+        const uint32_t npg = P >> pshift;
+        const uint32_t lp0 = pbeg >> pshift;
+        const uint32_t* trow = a.table + static_cast<uint64_t>(seq) * a.max_pages;
+        for (uint32_t i = tid; i < npg; i += NT) {
+            const uint32_t lp = lp0 + i;
+            const bool used = tb < te && (lp << pshift) < te && ((lp + 1) << pshift) > tb;
+            s_page[i] = used ? trow[lp] : 0u;
+        }
+    }
+
+    // This wave's two column groups; [wlo, whi) spans both groups' keys.
+    bool con[NCG];
+    uint32_t row[NCG], head[NCG], clo[NCG], chi[NCG], cspan[NCG], item0[NCG];
+    uint32_t wlo = 0xFFFFFFFFu, whi = 0;
+#pragma unroll
+    for (int g = 0; g < NCG; g++) {
+        const uint32_t gi = NCG * wave + g;
+        const bool gon = gi < ng;
+        const uint32_t* G = a.groups + (g0 + (gon ? gi : 0u)) * kGroupWords;
+        const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3];
+        item0[g] = G[10];
+        const uint32_t ncols = gon ? R * H : 0u;
+        con[g] = c < ncols;
+        const uint32_t rr = con[g] ? c / H : 0u;
+        row[g] = r0 + rr;
+        head[g] = kvh * a.nq_per_kv + h0 + (con[g] ? c - rr * H : 0u);
+        clo[g] = chi[g] = 0;
+        if (con[g]) {
+            clo[g] = max(a.ranges[2 * row[g]], tb);
+            chi[g] = min(a.ranges[2 * row[g] + 1], te);
+        }
+        cspan[g] = chi[g] > clo[g] ? chi[g] - clo[g] : 0u;  // key t is read iff t - clo < cspan
+        if (gon) {
+            const uint32_t glo = max(G[5], tb), ghi = min(G[6], te);
+            if (glo < ghi) {
+                wlo = min(wlo, glo);
+                whi = max(whi, ghi);
+            }
+        }
+    }
+    // Per group, the keys every column reads: a 32-key step inside
+    // [lomax, himin) needs no mask.
+    uint32_t lomax[NCG], himin[NCG];
+#pragma unroll
+    for (int g = 0; g < NCG; g++) {
+        uint32_t lo = con[g] ? clo[g] : 0u, hi = con[g] ? chi[g] : 0xFFFFFFFFu;
+#pragma unroll
+        for (int sh = 1; sh < 64; sh <<= 1) {
+            lo = max(lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo), sh)));
+            hi = min(hi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi), sh)));
+        }
+        lomax[g] = __builtin_amdgcn_readfirstlane(lo);
+        himin[g] = __builtin_amdgcn_readfirstlane(hi);
+    }
+    in8 qh[NCG][KS], ql[NCG][KS];
+
+    const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
+    const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
+
+    // Global -> registers for one tile; tokens outside [tb, te) are clamped
+    // into it (their scores are masked).
+    auto load = [&](uint32_t t0, u32x4 (&kr)[KPT], u32x4 (&vr)[VPT][2]) {
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const uint32_t u = tid + k * NT;
+            const uint32_t st = u / (16 * CPH), rem = u - st * (16 * CPH);
+            const uint32_t ch = rem >> 4, tok = rem & 15u;
+            const uint32_t t = min(max(t0 + 16u * st + tok, tb), last);
+            const uint32_t page = s_page[(t - pbeg) >> pshift];
+            const bool ok = u < static_cast<uint32_t>(KU) && 8u * ch < hd;
+            kr[k] = ok ? *(reinterpret_cast<const u32x4*>(
+                             kplane + ((static_cast<uint64_t>(page) * hd) << pshift) + k_off(t & pmask, 8u * ch, hd, pshift)))
+                       : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const uint32_t u = tid + k * NT;
+            const uint32_t st = u / (4 * (HD / 2)), rem = u - st * (4 * (HD / 2));
+            const uint32_t ag = rem / (HD / 2), d = 2u * (rem - ag * (HD / 2));
+            const bool ok = u < static_cast<uint32_t>(VP) && d < hd;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t t = min(max(t0 + 32u * st + 16u * h + 4u * ag, tb & ~3u), last & ~3u);
+                const uint32_t page = s_page[(t - pbeg) >> pshift];
+                vr[k][h] = ok ? *(reinterpret_cast<const u32x4*>(
+                                    vplane + ((static_cast<uint64_t>(page) * hd) << pshift) + v_off(t & pmask, d, hd)))
+                              : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto store = [&](int buf, const u32x4 (&kr)[KPT], const u32x4 (&vr)[VPT][2]) {
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const uint32_t u = tid + k * NT;
+            if (u < static_cast<uint32_t>(KU)) s_k[buf][u] = kr[k];
+        }
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const uint32_t u = tid + k * NT;
+            if (u >= static_cast<uint32_t>(VP)) continue;
+            const uint32_t st = u / (4 * (HD / 2)), rem = u - st * (4 * (HD / 2));
+            const uint32_t ag = rem / (HD / 2), d = 2u * (rem - ag * (HD / 2));
+            const uint32_t sw = ag ^ ((d >> 2) & 3u);  // the same for d and d + 1
+            s_v[buf][(st * HD + d) * 4 + sw] = u32x4{vr[k][0].x, vr[k][0].y, vr[k][1].x, vr[k][1].y};
+            s_v[buf][(st * HD + d + 1u) * 4 + sw] = u32x4{vr[k][0].z, vr[k][0].w, vr[k][1].z, vr[k][1].w};
+        }
+    };
+
+    // The softmax denominators come from the matrix cores: lsum[g] is a PV
+    // product against a row of ones, so every element holds the column's sum
+    // of probabilities (all 32 keys of a step, all four lane groups).
+    float m[NCG];
+    f32x4 o[NCG][MT], lsum[NCG];
+#pragma unroll
+    for (int g = 0; g < NCG; g++) {
+        m[g] = kFloor;
+        lsum[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < MT; i++) o[g][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    u32x4 ones;  // eight 1.0 in the KV type
+    {
+        const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;
+        ones = u32x4{one2, one2, one2, one2};
+    }
+
+    // 32-key steps, software-pipelined: the QK^T products of step s + 1 are
+    // issued before the softmax of step s, so the matrix cores work on them
+    // while the vector ALU computes the probabilities.  Products are ordered
+    // so that an accumulator is reused only every fourth MFMA (two column
+    // groups x two halves), which covers the matrix pipeline's latency; the
+    // mask is one unsigned range compare per score, and steps inside every
+    // column's keys skip it.
+    auto qk_step = [&](int buf, int st, f32x4 (&sc)[NCG][2]) {
+#pragma unroll
+        for (int g = 0; g < NCG; g++) sc[g][0] = sc[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            u32x4 kv[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) kv[h] = s_k[buf][((2 * st + h) * CPH + 4 * j + a4) * 16u + c];
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int g = 0; g < NCG; g++) sc[g][h] = O::qk(kv[h], qh[g][j], sc[g][h]);
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int g = 0; g < NCG; g++) sc[g][h] = O::qk(kv[h], ql[g][j], sc[g][h]);
+        }
+    };
+    auto softmax_pv = [&](int buf, int st, uint32_t ts, const f32x4 (&sc)[NCG][2]) {
+        in8 ph[NCG], pl[NCG];
+#pragma unroll
+        for (int g = 0; g < NCG; g++) {
+            float x[8];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float v = sc[g][h][e];  // the query carries the scale
+                    if constexpr (CAP) v = a.cap2 * tanh_approx(v);
+                    x[4 * h + e] = v;
+                }
+            }
+            if (!(ts >= lomax[g] && ts + 32u <= himin[g])) {  // wave-uniform
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t t = ts + 16u * (e >> 2) + 4u * a4 + (e & 3);
+                    x[e] = t - clo[g] < cspan[g] ? x[e] : -INFINITY;
+                }
+            }
+            // The column max (two cross-lane steps) is needed only when some
+            // score beats its column's running max by more than kTau; without
+            // one, no column rescales, exactly as if the max had been taken.
+            float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+            if (__builtin_amdgcn_ballot_w64(mx > m[g] + kTau) != 0) {  // wave-uniform
+                mx = col_max(mx);
+                if (mx > m[g] + kTau) {
+                    const float alpha = fast_exp2(m[g] - mx);
+                    lsum[g] *= alpha;
+#pragma unroll
+                    for (int i = 0; i < MT; i++) o[g][i] *= alpha;
+                    m[g] = mx;
+                }
+            }
+            float p[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) p[e] = fast_exp2(x[e] - m[g]);
+            if constexpr (PLO) {
+                O::split8(p, ph[g], pl[g]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) ph[g][e] = static_cast<_Float16>(p[e]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MT; i += 2) {
+            u32x4 vv[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t d = 16u * (i + u) + c;
+                vv[u] = s_v[buf][(st * HD + d) * 4 + (a4 ^ ((d >> 2) & 3u))];
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int g = 0; g < NCG; g++) o[g][i + u] = O::pv32(vv[u], ph[g], o[g][i + u]);
+            if constexpr (PLO) {
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+#pragma unroll
+                    for (int g = 0; g < NCG; g++) o[g][i + u] = O::pv32(vv[u], pl[g], o[g][i + u]);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < NCG; g++) lsum[g] = O::pv32(ones, ph[g], lsum[g]);
+        if constexpr (PLO) {
+#pragma unroll
+            for (int g = 0; g < NCG; g++) lsum[g] = O::pv32(ones, pl[g], lsum[g]);
+        }
+    };
+    auto compute = [&](int buf, uint32_t t0) {
+        bool act[NS];
+#pragma unroll
+        for (int st = 0; st < NS; st++) {
+            const uint32_t ts = t0 + 32u * st;
+            act[st] = !(ts >= whi || ts + 32u <= wlo);  // inside this wave's keys
+        }
+        f32x4 scA[NCG][2], scB[NCG][2];
+        if (act[0]) qk_step(buf, 0, scA);
+#pragma unroll
+        for (int st = 0; st < NS; st++) {
+            if (st + 1 < NS && act[st + 1]) qk_step(buf, st + 1, (st & 1) ? scA : scB);
+            if (act[st]) softmax_pv(buf, st, t0 + 32u * st, (st & 1) ? scB : scA);
+        }
+    };
+
+    const uint32_t t_first = tb & ~31u;
+    const uint32_t n_tiles = te > t_first ? (te - t_first + TT - 1) / TT : 0u;
+    __syncthreads();  // s_page complete
+    {
+        u32x4 kr[KPT], vr[VPT][2];
+        // The first tile's loads are in flight while the queries are loaded.
+        if (n_tiles) load(t_first, kr, vr);
+#pragma unroll
+        for (int g = 0; g < NCG; g++) load_q<KS, O, FULL>(a, con[g], row[g], head[g], a4, qh[g], ql[g], a.qscale);
+        if (n_tiles) store(0, kr, vr);
+        __syncthreads();
+        for (uint32_t i = 0; i < n_tiles; i++) {
+            const uint32_t t0 = t_first + i * TT;
+            const bool more = i + 1 < n_tiles;
+            if (more) load(t0 + TT, kr, vr);
+            compute(static_cast<int>(i & 1u), t0);
+            if (more) store(static_cast<int>((i + 1) & 1u), kr, vr);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < NCG; g++) {
+        const float lg = lsum[g][0];
+        if (!con[g]) continue;
+        if (n_parts == 1) {
+            const float inv = 1.0f / lg;
+#pragma unroll
+            for (int i = 0; i < MT; i++) {
+                const uint32_t d = 16u * i + 4u * a4;
+                if (d >= hd) continue;
+                const f32x4 yv = o[g][i] * inv;
+                const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
+                store_y<4, FULL>(a, row[g], head[g], d, v4);
+            }
+            continue;
+        }
+        const uint64_t pb = (static_cast<uint64_t>(item0[g] + part) * a.n_kvh + kvh) * kCols + c;
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+            *reinterpret_cast<f32x4*>(a.part_o + pb * HD + 16u * i + 4u * a4) = o[g][i];
+        if (a4 == 0) {
+            a.part_ml[2 * pb] = m[g];
+            a.part_ml[2 * pb + 1] = lg;
+        }
+    }
+}
+
 // ------------------------------------------------------------ host side
 uint32_t template_hd(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : hd <= 256 ? 256 : 512; }
 
@@ -975,21 +1345,56 @@ void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s
     }
 }
 
+// Waves of attn_prefill_wide (head_dim <= 128; two query groups per wave).
+#ifndef THB_PREFILL_WAVES
+#define THB_PREFILL_WAVES 8
+#endif
+// Query groups per prefill block: 2 per wave of attn_prefill_wide, 1 per wave
+// of attn_prefill (wider heads).
+constexpr uint32_t block_groups(bool wide, uint32_t hd_t) {
+    return wide ? 2 * THB_PREFILL_WAVES : static_cast<uint32_t>(hd_t <= 128 ? THB_ATTN_WAVES : waves_for(256));
+}
+
+// Score scale applied to the query (log2 units, or 1 / softcap).
+float q_scale(const thb_attn_spec& sp) {
+    return sp.softcap > 0.0f ? sp.scale / sp.softcap : sp.scale * 1.4426950408889634f;
+}
+
+// attn_prefill_wide serves head_dim <= 128 when the score scale can be folded
+// into the query (|scale| <= 1 keeps the scaled query in range); other calls
+// use attn_prefill.
+bool prefill_wide(uint32_t hd_t, const thb_attn_spec& sp) { return hd_t <= 128 && std::fabs(q_scale(sp)) <= 1.0f; }
+
 template <int HD, bool F16>
-void launch_prefill_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
-    constexpr int W = waves_for(HD);
+void launch_prefill_hd(bool wide, dim3 grid, const AttnArgs& a, hipStream_t s) {
+    if constexpr (HD <= 128) {
+        if (wide) {
+            constexpr int W = THB_PREFILL_WAVES;
+            const bool cap = a.cap2 != 0.0f;
+            if (a.full && cap)
+                hipLaunchKernelGGL((attn_prefill_wide<HD, F16, W, true, true>), grid, dim3(64 * W), 0, s, a);
+            else if (a.full)
+                hipLaunchKernelGGL((attn_prefill_wide<HD, F16, W, true, false>), grid, dim3(64 * W), 0, s, a);
+            else if (cap)
+                hipLaunchKernelGGL((attn_prefill_wide<HD, F16, W, false, true>), grid, dim3(64 * W), 0, s, a);
+            else
+                hipLaunchKernelGGL((attn_prefill_wide<HD, F16, W, false, false>), grid, dim3(64 * W), 0, s, a);
+            return;
+        }
+    }
+    constexpr int W = HD <= 128 ? THB_ATTN_WAVES : waves_for(HD);
     if (a.full)
         hipLaunchKernelGGL((attn_prefill<HD, F16, W, true>), grid, dim3(64 * W), 0, s, a);
     else
         hipLaunchKernelGGL((attn_prefill<HD, F16, W, false>), grid, dim3(64 * W), 0, s, a);
 }
 
-void launch_prefill(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
+void launch_prefill(uint32_t hd_t, bool wide, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
     switch (hd_t) {
-        case 64: f16 ? launch_prefill_hd<64, true>(grid, a, s) : launch_prefill_hd<64, false>(grid, a, s); break;
-        case 128: f16 ? launch_prefill_hd<128, true>(grid, a, s) : launch_prefill_hd<128, false>(grid, a, s); break;
-        case 256: f16 ? launch_prefill_hd<256, true>(grid, a, s) : launch_prefill_hd<256, false>(grid, a, s); break;
-        default: f16 ? launch_prefill_hd<512, true>(grid, a, s) : launch_prefill_hd<512, false>(grid, a, s); break;
+        case 64: f16 ? launch_prefill_hd<64, true>(wide, grid, a, s) : launch_prefill_hd<64, false>(wide, grid, a, s); break;
+        case 128: f16 ? launch_prefill_hd<128, true>(wide, grid, a, s) : launch_prefill_hd<128, false>(wide, grid, a, s); break;
+        case 256: f16 ? launch_prefill_hd<256, true>(wide, grid, a, s) : launch_prefill_hd<256, false>(wide, grid, a, s); break;
+        default: f16 ? launch_prefill_hd<512, true>(wide, grid, a, s) : launch_prefill_hd<512, false>(wide, grid, a, s); break;
     }
 }
 
@@ -1083,7 +1488,8 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     const uint32_t PL = pool->part_len;
     const uint32_t align = std::max<uint32_t>(pool->page_len, 16);
     const uint32_t hd_t = template_hd(hd);
-    const uint32_t WB = static_cast<uint32_t>(hd_t >= 256 ? 4 : 8);  // waves of attn_prefill
+    const bool wide = prefill_wide(hd_t, sp);
+    const uint32_t WB = block_groups(wide, hd_t);  // query groups per prefill block
     uint32_t max_parts = 0;
     uint64_t max_span = 0;
     bool any_split = false;
@@ -1215,6 +1621,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     plan.n_slots = n_slots;
     plan.split = any_split;
     plan.hd_t = hd_t;
+    plan.wide = wide;
 
     // The append can run inside the attention launch when no query reads a
     // token that another workgroup appends: the call is causal, every row's
@@ -1274,7 +1681,7 @@ int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint
     for (auto& p : pool->plans)
         if (p.rows == rows && p.rows_version == rows->version && p.arena_version == av && p.row_off == sp.row_off &&
             p.m == sp.m && p.seq == sp.seq && p.causal == sp.causal && p.window == sp.window &&
-            p.q_heads == sp.q_heads && p.head_dim == hd) {
+            p.q_heads == sp.q_heads && p.head_dim == hd && p.wide == prefill_wide(p.hd_t, sp)) {
             p.last_use = ++pool->plan_clock;
             *out = &p;
             return THB_OK;
@@ -1342,14 +1749,8 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.head_dim = hd;
     a.part_len = pool->part_len;
     a.n_kvh = pool->kv_heads;
-    const float log2e = 1.4426950408889634f;
-    if (sp.softcap > 0.0f) {
-        a.qscale = sp.scale / sp.softcap;
-        a.cap2 = sp.softcap * log2e;
-    } else {
-        a.qscale = sp.scale * log2e;
-        a.cap2 = 0.0f;
-    }
+    a.qscale = q_scale(sp);
+    a.cap2 = sp.softcap > 0.0f ? sp.softcap * 1.4426950408889634f : 0.0f;
     a.q_dt = sp.q_dtype;
     a.y_dt = sp.y_dtype;
     a.q_stride = io.q_stride ? io.q_stride : hd;
@@ -1375,7 +1776,7 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
         THB_HIP(hipGetLastError());
     }
     if (n_pwg) {
-        launch_prefill(hd_t, f16, dim3(static_cast<uint32_t>(n_pwg)), a, s);
+        launch_prefill(hd_t, plan.wide, f16, dim3(static_cast<uint32_t>(n_pwg)), a, s);
         THB_HIP(hipGetLastError());
     }
     if (plan.split) {
