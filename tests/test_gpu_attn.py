@@ -328,6 +328,11 @@ PREFILL_CASES = [
     ("qwen2-page8-bf16", 14, 2, 64, 8, "bf16", 100, 150, 0, 0.0),
     ("hd512-page32", 8, 2, 512, 32, "f16", 333, 70, 0, 0.0),
     ("mqa32-head-split", 32, 1, 128, 32, "f16", 700, 64, 0, 0.0),
+    # the head_dim <= 128 kernel with soft-cap and a window, and with bf16 probabilities split in two
+    ("hd128-window-softcap", 32, 8, 128, 16, "f16", 3000, 200, 1024, 30.0),
+    ("hd64-bf16-softcap-split", 8, 2, 64, 16, "bf16", 6000, 130, 0, 20.0),
+    # a score scale above 1 / log2(e): the query cannot carry it, the other prefill kernel runs
+    ("hd128-scale-above-one", 32, 8, 128, 16, "f16", 500, 100, 0, 0.0, 1.0),
 ]
 
 
@@ -340,7 +345,7 @@ def test_chunked_prefill_parity(torch_cuda, case):
     from flint_amd import ops
     from flint_amd.pool import RowMeta
 
-    name, nq, nkv, hd, pl, kv, prefix, chunk, window, cap = case
+    name, nq, nkv, hd, pl, kv, prefix, chunk, window, cap = case[:10]
     say("prefill", name)
     rng = random.Random(zlib.crc32(name.encode()))
     lens = [prefix + chunk, 777]
@@ -356,7 +361,7 @@ def test_chunked_prefill_parity(torch_cuda, case):
     k = torch.randn(m, nkv, hd, device="cuda", generator=g)
     v = torch.randn(m, nkv, hd, device="cuda", generator=g)
     q = torch.randn(m, nq, hd, device="cuda", generator=g) * (2.0 if cap else 1.0)
-    scale = 1.0 / math.sqrt(hd)
+    scale = case[10] if len(case) > 10 else 1.0 / math.sqrt(hd)
     rows.write(positions, seqs, m)
     y = torch.empty_like(q)
     spec = ops.AttnSpec(q_heads=nq, window=window, scale=scale, m=m, causal=True, seq=None, args=rows,
