@@ -58,6 +58,10 @@ constexpr uint32_t kMaxPartPages = 1024;
 constexpr uint32_t kMaxParts = 512;   // partitions of one group the merge kernel takes
 constexpr uint32_t kCols = 16;        // query vectors per group (MFMA N)
 constexpr uint32_t kBlockWords = 9;   // g0, ng, seq, lo, hi, n_parts, base, plen, bitem0
+// Work-item records carry their group's (or block's) words and the
+// partition index, so a workgroup finds its work in one dependent load.
+constexpr uint32_t kItemWords = kGroupWords + 1;
+constexpr uint32_t kBItemWords = kBlockWords + 1;
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -69,10 +73,9 @@ struct AttnArgs {
     const void* q;
     void* y;
     const uint32_t* groups;
-    const uint32_t* items;   // work item -> group
+    const uint32_t* items;   // decode work items: group words + partition (kItemWords each)
     const uint32_t* ranges;  // [m][2]: lo, hi
-    const uint32_t* blocks;  // prefill blocks of consecutive groups
-    const uint32_t* bitems;  // prefill work item -> block
+    const uint32_t* bitems;  // prefill work items: block words + partition (kBItemWords each)
     const uint32_t* table;
     uint16_t* k;
     uint16_t* v;
@@ -397,10 +400,10 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     // and items are ordered longest first (the host sorts them).
     const uint32_t item = blockIdx.x / a.n_kvh, kvh = blockIdx.x - item * a.n_kvh;
 
-    const uint32_t* G = a.groups + a.items[item] * kGroupWords;
+    const uint32_t* G = a.items + static_cast<uint64_t>(item) * kItemWords;
     const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3], seq = G[4];
-    const uint32_t glo = G[5], ghi = G[6], n_parts = G[7], gbase = G[8], P = G[9], item0 = G[10];
-    const uint32_t pbeg = gbase + (item - item0) * P;
+    const uint32_t glo = G[5], ghi = G[6], n_parts = G[7], gbase = G[8], P = G[9];
+    const uint32_t pbeg = gbase + G[kGroupWords] * P;
     const uint32_t tb = max(glo, pbeg), te = min(ghi, pbeg + P);
     const uint32_t hd = a.head_dim;
     const uint32_t pshift = a.page_shift;
@@ -770,10 +773,10 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
     const uint32_t a4 = lane >> 4, c = lane & 15u;
     const uint32_t bitem = blockIdx.x / a.n_kvh, kvh = blockIdx.x - bitem * a.n_kvh;
 
-    const uint32_t* Bk = a.blocks + a.bitems[bitem] * kBlockWords;
+    const uint32_t* Bk = a.bitems + static_cast<uint64_t>(bitem) * kBItemWords;
     const uint32_t g0 = Bk[0], ng = Bk[1], seq = Bk[2], blo = Bk[3], bhi = Bk[4];
-    const uint32_t n_parts = Bk[5], bbase = Bk[6], P = Bk[7], bitem0 = Bk[8];
-    const uint32_t part = bitem - bitem0;
+    const uint32_t n_parts = Bk[5], bbase = Bk[6], P = Bk[7];
+    const uint32_t part = Bk[kBlockWords];
     const uint32_t pbeg = bbase + part * P;
     const uint32_t tb = max(blo, pbeg), te = min(bhi, pbeg + P);
     const uint32_t hd = a.head_dim;
@@ -1014,10 +1017,10 @@ __global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
     const uint32_t a4 = lane >> 4, c = lane & 15u;
     const uint32_t bitem = blockIdx.x / a.n_kvh, kvh = blockIdx.x - bitem * a.n_kvh;
 
-    const uint32_t* Bk = a.blocks + a.bitems[bitem] * kBlockWords;
+    const uint32_t* Bk = a.bitems + static_cast<uint64_t>(bitem) * kBItemWords;
     const uint32_t g0 = Bk[0], ng = Bk[1], seq = Bk[2], blo = Bk[3], bhi = Bk[4];
-    const uint32_t n_parts = Bk[5], bbase = Bk[6], P = Bk[7], bitem0 = Bk[8];
-    const uint32_t part = bitem - bitem0;
+    const uint32_t n_parts = Bk[5], bbase = Bk[6], P = Bk[7];
+    const uint32_t part = Bk[kBlockWords];
     const uint32_t pbeg = bbase + part * P;
     const uint32_t tb = max(blo, pbeg), te = min(bhi, pbeg + P);
     const uint32_t hd = a.head_dim;
@@ -1266,13 +1269,13 @@ __global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
 
     const uint32_t t_first = tb & ~31u;
     const uint32_t n_tiles = te > t_first ? (te - t_first + TT - 1) / TT : 0u;
+    // The queries are loaded and split while the page table fills s_page.
+#pragma unroll
+    for (int g = 0; g < NCG; g++) load_q<KS, O, FULL>(a, con[g], row[g], head[g], a4, qh[g], ql[g], a.qscale);
     __syncthreads();  // s_page complete
     {
         u32x4 kr[KPT], vr[VPT][2];
-        // The first tile's loads are in flight while the queries are loaded.
         if (n_tiles) load(t_first, kr, vr);
-#pragma unroll
-        for (int g = 0; g < NCG; g++) load_q<KS, O, FULL>(a, con[g], row[g], head[g], a4, qh[g], ql[g], a.qscale);
         if (n_tiles) store(0, kr, vr);
         __syncthreads();
         for (uint32_t i = 0; i < n_tiles; i++) {
@@ -1603,15 +1606,22 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     if (n_items > 0x7FFFFFFFu || n_groups > 0x7FFFFFFFu) return fail(THB_ERR_CONFIG, "attention call too large");
 
     std::vector<uint32_t> blob;
-    blob.reserve(groups.size() + items.size() + 2 * m + blocks.size() + bitems.size());
+    blob.reserve(groups.size() + n_items * kItemWords + 2 * m + n_bitems * kBItemWords);
     blob.insert(blob.end(), groups.begin(), groups.end());
-    blob.insert(blob.end(), items.begin(), items.end());
+    for (uint32_t i = 0; i < n_items; i++) {  // group words + partition index
+        const uint32_t* gr = &groups[static_cast<size_t>(items[i]) * kGroupWords];
+        blob.insert(blob.end(), gr, gr + kGroupWords);
+        blob.push_back(i - gr[10]);
+    }
     for (uint32_t r = 0; r < m; r++) {
         blob.push_back(rp.lo[r]);
         blob.push_back(rp.hi[r]);
     }
-    blob.insert(blob.end(), blocks.begin(), blocks.end());
-    blob.insert(blob.end(), bitems.begin(), bitems.end());
+    for (uint32_t i = 0; i < n_bitems; i++) {  // block words + partition index
+        const uint32_t* bk = &blocks[static_cast<size_t>(bitems[i]) * kBlockWords];
+        blob.insert(blob.end(), bk, bk + kBlockWords);
+        blob.push_back(i - bk[8]);
+    }
     void* dev = plan.dev.reserve(blob.size() * 4, false);
     pool->stager.upload(dev, blob.data(), blob.size() * 4, stream);
     plan.n_groups = n_groups;
@@ -1730,9 +1740,8 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.y = io.y_dev;
     a.groups = blob;
     a.items = blob + static_cast<size_t>(plan.n_groups) * kGroupWords;
-    a.ranges = a.items + plan.n_items;
-    a.blocks = a.ranges + 2 * static_cast<size_t>(sp.m);
-    a.bitems = a.blocks + static_cast<size_t>(plan.n_blocks) * kBlockWords;
+    a.ranges = a.items + static_cast<size_t>(plan.n_items) * kItemWords;
+    a.bitems = a.ranges + 2 * static_cast<size_t>(sp.m);
     a.table = pool->table_dev;
     a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
     a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
