@@ -93,8 +93,9 @@ struct AttnArgs {
     const void* gate;          // sigmoid gate of the output (q_dt), or null
     uint32_t gate_stride;      // elements from one gate head to the next
     // full = 1 selects the kernels with the extensions of thb_attn_io (query
-    // stride, gate, bf16 query/output, rope); the others take f32/f16 q and
-    // y only and are the lean path of the common call.
+    // stride, gate, bf16 query/output, rope) and the logit soft-cap; the
+    // others take f32/f16 q and y only and are the lean path of the common
+    // call.
     uint32_t full;
     // Rotary position embedding (FULL kernels): the query is normalised and
     // rotated as it is loaded, the fused append rotates the key.
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     __shared__ float s_l[HALF][64];
 
     const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t a4 = lane >> 4, c = lane & 15u;
     // 1-D grid, KV head fastest: consecutive workgroups share a work item,
     // and items are ordered longest first (the host sorts them).
@@ -432,6 +433,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
         clo = max(a.ranges[2 * row], tb);
         chi = min(a.ranges[2 * row + 1], te);
     }
+    const uint32_t cspan = chi > clo ? chi - clo : 0u;  // key t is read iff t - clo < cspan
 
     // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8], split hi/lo.
     in8 qh[KS], ql[KS];
@@ -594,19 +596,24 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             float x = s[e] * a.qscale;
-            if (a.cap2 != 0.0f) x = a.cap2 * tanh_approx(x);
+            if (FULL && a.cap2 != 0.0f) x = a.cap2 * tanh_approx(x);  // soft-cap: FULL kernels only
             const uint32_t t = t0 + 4u * a4 + e;
-            x = (t >= clo && t < chi) ? x : -INFINITY;
+            x = t - clo < cspan ? x : -INFINITY;
             sv[e] = x;
             mx = fmaxf(mx, x);
         }
-        mx = col_max(mx);
-        if (mx > m + kTau) {
-            const float alpha = fast_exp2(m - mx);
-            l *= alpha;
+        // The column max (two cross-lane steps) is taken only when some score
+        // beats its column's running max by more than kTau; without one, no
+        // column rescales, exactly as if the max had been taken.
+        if (__builtin_amdgcn_ballot_w64(mx > m + kTau) != 0) {
+            mx = col_max(mx);
+            if (mx > m + kTau) {
+                const float alpha = fast_exp2(m - mx);
+                l *= alpha;
 #pragma unroll
-            for (int i = 0; i < MT; i++) o[i] *= alpha;
-            m = mx;
+                for (int i = 0; i < MT; i++) o[i] *= alpha;
+                m = mx;
+            }
         }
         float p[4];
 #pragma unroll
@@ -1767,7 +1774,7 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.gate_stride = io.gate_stride ? io.gate_stride : hd;
     a.rope_on = rope != nullptr;
     a.full = rope != nullptr || io.gate_dev != nullptr || a.q_stride != hd || sp.q_dtype == THB_DT_BF16 ||
-             sp.y_dtype == THB_DT_BF16;
+             sp.y_dtype == THB_DT_BF16 || sp.softcap > 0.0f;
     a.meta = meta;
     a.qrope = rope ? rope_dev(*rope, true) : RopeDev{};
     a.krope = rope ? rope_dev(*rope, false) : RopeDev{};
