@@ -1325,17 +1325,19 @@ __global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
 uint32_t template_hd(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : hd <= 256 ? 256 : 512; }
 
 // Waves per workgroup and tiles in flight per wave of each head_dim
-// template: up to head_dim 128, 8 waves (2 per SIMD, 256 registers each);
-// above, 4 waves (512 registers each), because the query, output and load
-// registers grow with head_dim.
+// template: up to head_dim 256, 8 waves (2 per SIMD, 256 registers each),
+// with two tiles in flight up to 128 and one at 256 (the query, output and
+// load registers grow with head_dim; at 256 the second wave per SIMD hides
+// more than a second tile, 1.5% on Gemma-2 layers); at 512, 4 waves (512
+// registers each) with one tile.
 #ifndef THB_ATTN_WAVES
 #define THB_ATTN_WAVES 8
 #endif
 #ifndef THB_ATTN_RING
 #define THB_ATTN_RING 2
 #endif
-constexpr int waves_for(int hd) { return hd >= 256 ? 4 : THB_ATTN_WAVES; }
-constexpr int ring_for(int hd) { return hd >= 512 ? 1 : hd >= 256 ? 2 : THB_ATTN_RING; }
+constexpr int waves_for(int hd) { return hd >= 512 ? 4 : THB_ATTN_WAVES; }
+constexpr int ring_for(int hd) { return hd >= 256 ? 1 : THB_ATTN_RING; }
 
 template <int HD, bool F16>
 void launch_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
@@ -1362,7 +1364,7 @@ void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s
 // Query groups per prefill block: 2 per wave of attn_prefill_wide, 1 per wave
 // of attn_prefill (wider heads).
 constexpr uint32_t block_groups(bool wide, uint32_t hd_t) {
-    return wide ? 2 * THB_PREFILL_WAVES : static_cast<uint32_t>(hd_t <= 128 ? THB_ATTN_WAVES : waves_for(256));
+    return wide ? 2 * THB_PREFILL_WAVES : static_cast<uint32_t>(waves_for(static_cast<int>(hd_t)));
 }
 
 // Score scale applied to the query (log2 units, or 1 / softcap).
@@ -1392,7 +1394,7 @@ void launch_prefill_hd(bool wide, dim3 grid, const AttnArgs& a, hipStream_t s) {
             return;
         }
     }
-    constexpr int W = HD <= 128 ? THB_ATTN_WAVES : waves_for(HD);
+    constexpr int W = waves_for(HD);  // one group per wave: block_groups(false, HD)
     if (a.full)
         hipLaunchKernelGGL((attn_prefill<HD, F16, W, true>), grid, dim3(64 * W), 0, s, a);
     else
