@@ -63,6 +63,21 @@ constexpr uint32_t kBlockWords = 9;   // g0, ng, seq, lo, hi, n_parts, base, ple
 constexpr uint32_t kItemWords = kGroupWords + 1;
 constexpr uint32_t kBItemWords = kBlockWords + 1;
 
+// Waves per workgroup and tiles in flight per wave of each head_dim
+// template: up to head_dim 256, 8 waves (2 per SIMD, 256 registers each),
+// with two tiles in flight up to 128 and one at 256 (the query, output and
+// load registers grow with head_dim; at 256 the second wave per SIMD hides
+// more than a second tile, 1.5% on Gemma-2 layers); at 512, 4 waves (512
+// registers each) with one tile.
+#ifndef THB_ATTN_WAVES
+#define THB_ATTN_WAVES 8
+#endif
+#ifndef THB_ATTN_RING
+#define THB_ATTN_RING 2
+#endif
+constexpr int waves_for(int hd) { return hd >= 512 ? 4 : THB_ATTN_WAVES; }
+constexpr int ring_for(int hd) { return hd >= 256 ? 1 : THB_ATTN_RING; }
+
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -76,6 +91,7 @@ struct AttnArgs {
     const uint32_t* items;   // decode work items: group words + partition (kItemWords each)
     const uint32_t* ranges;  // [m][2]: lo, hi
     const uint32_t* bitems;  // prefill work items: block words + partition (kBItemWords each)
+    const uint32_t* order;   // attn_mixed: launch order of decode items and prefill blocks (bit 31)
     const uint32_t* table;
     uint16_t* k;
     uint16_t* v;
@@ -381,7 +397,7 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
 // loads are kept in flight per wave: tile i + NB is requested as soon as
 // tile i has been consumed.
 template <int HD, bool F16, int W, int NB, bool FULL>
-__global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
+__device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
     typedef typename O::in4 in4;
@@ -399,7 +415,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     const uint32_t a4 = lane >> 4, c = lane & 15u;
     // 1-D grid, KV head fastest: consecutive workgroups share a work item,
     // and items are ordered longest first (the host sorts them).
-    const uint32_t item = blockIdx.x / a.n_kvh, kvh = blockIdx.x - item * a.n_kvh;
+    const uint32_t item = bid / a.n_kvh, kvh = bid - item * a.n_kvh;
 
     const uint32_t* G = a.items + static_cast<uint64_t>(item) * kItemWords;
     const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3], seq = G[4];
@@ -702,6 +718,11 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     }
 }
 
+template <int HD, bool F16, int W, int NB, bool FULL>
+__global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
+    decode_wg<HD, F16, W, NB, FULL>(a, blockIdx.x);
+}
+
 // Merges the partitions of every group that has more than one, in
 // partition order.  One workgroup per (group, KV head).
 template <int HD, bool FULL>
@@ -995,7 +1016,7 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
 #define THB_PREFILL_TILE 64
 #endif
 template <int HD, bool F16, int W, bool FULL, bool CAP>
-__global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
+__device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
     constexpr int KS = HD / 32;
@@ -1022,7 +1043,7 @@ __global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t a4 = lane >> 4, c = lane & 15u;
-    const uint32_t bitem = blockIdx.x / a.n_kvh, kvh = blockIdx.x - bitem * a.n_kvh;
+    const uint32_t bitem = bid / a.n_kvh, kvh = bid - bitem * a.n_kvh;
 
     const uint32_t* Bk = a.bitems + static_cast<uint64_t>(bitem) * kBItemWords;
     const uint32_t g0 = Bk[0], ng = Bk[1], seq = Bk[2], blo = Bk[3], bhi = Bk[4];
@@ -1321,23 +1342,32 @@ __global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
     }
 }
 
+template <int HD, bool F16, int W, bool FULL, bool CAP>
+__global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
+    prefill_wide_wg<HD, F16, W, FULL, CAP>(a, blockIdx.x);
+}
+
+// A call with decode items and prefill blocks (a continuous batch) as one
+// launch: record r of the launch order is a decode item or a prefill block
+// (bit 31), and its KV heads are the workgroups r * n_kvh .. + n_kvh - 1.
+// The host interleaves the two kinds, so that workgroups streaming KV from
+// HBM and workgroups busy on the matrix cores run side by side on different
+// CUs instead of one kernel after the other.  Each workgroup runs exactly
+// the code (and arithmetic) of its own kernel.
+template <int HD, bool F16, int W, bool FULL, bool CAP>
+__global__ __launch_bounds__(64 * W, 2) void attn_mixed(AttnArgs a) {
+    const uint32_t rec = blockIdx.x / a.n_kvh, kvh = blockIdx.x - rec * a.n_kvh;
+    const uint32_t w = a.order[rec];
+    const uint32_t bid = (w & 0x7FFFFFFFu) * a.n_kvh + kvh;
+    if (w >> 31)
+        prefill_wide_wg<HD, F16, W, FULL, CAP>(a, bid);
+    else
+        decode_wg<HD, F16, W, ring_for(HD), FULL>(a, bid);
+}
+
 // ------------------------------------------------------------ host side
 uint32_t template_hd(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : hd <= 256 ? 256 : 512; }
 
-// Waves per workgroup and tiles in flight per wave of each head_dim
-// template: up to head_dim 256, 8 waves (2 per SIMD, 256 registers each),
-// with two tiles in flight up to 128 and one at 256 (the query, output and
-// load registers grow with head_dim; at 256 the second wave per SIMD hides
-// more than a second tile, 1.5% on Gemma-2 layers); at 512, 4 waves (512
-// registers each) with one tile.
-#ifndef THB_ATTN_WAVES
-#define THB_ATTN_WAVES 8
-#endif
-#ifndef THB_ATTN_RING
-#define THB_ATTN_RING 2
-#endif
-constexpr int waves_for(int hd) { return hd >= 512 ? 4 : THB_ATTN_WAVES; }
-constexpr int ring_for(int hd) { return hd >= 256 ? 1 : THB_ATTN_RING; }
 
 template <int HD, bool F16>
 void launch_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
@@ -1408,6 +1438,29 @@ void launch_prefill(uint32_t hd_t, bool wide, bool f16, dim3 grid, const AttnArg
         case 256: f16 ? launch_prefill_hd<256, true>(wide, grid, a, s) : launch_prefill_hd<256, false>(wide, grid, a, s); break;
         default: f16 ? launch_prefill_hd<512, true>(wide, grid, a, s) : launch_prefill_hd<512, false>(wide, grid, a, s); break;
     }
+}
+
+template <int HD, bool F16>
+void launch_mixed_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
+    constexpr int W = THB_PREFILL_WAVES;
+    static_assert(HD > 128 || THB_ATTN_WAVES != THB_PREFILL_WAVES || W == waves_for(HD), "mixed launch waves");
+    const bool cap = a.cap2 != 0.0f;
+    if (a.full && cap)
+        hipLaunchKernelGGL((attn_mixed<HD, F16, W, true, true>), grid, dim3(64 * W), 0, s, a);
+    else if (a.full)
+        hipLaunchKernelGGL((attn_mixed<HD, F16, W, true, false>), grid, dim3(64 * W), 0, s, a);
+    else if (cap)
+        hipLaunchKernelGGL((attn_mixed<HD, F16, W, false, true>), grid, dim3(64 * W), 0, s, a);
+    else
+        hipLaunchKernelGGL((attn_mixed<HD, F16, W, false, false>), grid, dim3(64 * W), 0, s, a);
+}
+
+// Mixed launches exist at head_dim <= 128 (where attn_prefill_wide runs).
+void launch_mixed(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
+    if (hd_t == 64)
+        f16 ? launch_mixed_hd<64, true>(grid, a, s) : launch_mixed_hd<64, false>(grid, a, s);
+    else
+        f16 ? launch_mixed_hd<128, true>(grid, a, s) : launch_mixed_hd<128, false>(grid, a, s);
 }
 
 template <int HD>
@@ -1631,6 +1684,32 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         blob.insert(blob.end(), bk, bk + kBlockWords);
         blob.push_back(i - bk[8]);
     }
+    // A call with both kinds of work runs them in one launch (attn_mixed),
+    // interleaved longest first by an estimate of each workgroup's time: a
+    // decode partition streams 4 * head_dim bytes per key at ~24 GB/s per
+    // CU; a prefill block pays ~6 us before its first 64-key tile and
+    // ~3.2 us per tile (head_dim 128, measured).  The order changes no row's
+    // arithmetic.
+    const bool mixed = n_items > 0 && n_bitems > 0 && wide && THB_ATTN_WAVES == THB_PREFILL_WAVES;
+    if (mixed) {
+        std::vector<std::pair<float, uint32_t>> est;
+        est.reserve(n_items + n_bitems);
+        for (uint32_t i = 0; i < n_items; i++) {
+            const uint32_t* gr = &groups[static_cast<size_t>(items[i]) * kGroupWords];
+            const uint64_t p0 = uint64_t(gr[8]) + uint64_t(i - gr[10]) * gr[9];
+            const uint64_t keys = gr[6] > p0 ? std::min<uint64_t>(gr[9], gr[6] - p0) : 0;
+            est.push_back({1.0f + static_cast<float>(keys) * 4.0f * hd / 24000.0f, i});
+        }
+        for (uint32_t i = 0; i < n_bitems; i++) {
+            const uint32_t* bk = &blocks[static_cast<size_t>(bitems[i]) * kBlockWords];
+            const uint64_t p0 = uint64_t(bk[6]) + uint64_t(i - bk[8]) * bk[7];
+            const uint64_t keys = bk[4] > p0 ? std::min<uint64_t>(bk[7], bk[4] - p0) : 0;
+            est.push_back({6.0f + static_cast<float>((keys + 63) / 64) * 3.2f * hd_t / 128.0f, 0x80000000u | i});
+        }
+        std::stable_sort(est.begin(), est.end(),
+                         [](const std::pair<float, uint32_t>& x, const std::pair<float, uint32_t>& y) { return x.first > y.first; });
+        for (auto& e : est) blob.push_back(e.second);
+    }
     void* dev = plan.dev.reserve(blob.size() * 4, false);
     pool->stager.upload(dev, blob.data(), blob.size() * 4, stream);
     plan.n_groups = n_groups;
@@ -1641,6 +1720,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     plan.split = any_split;
     plan.hd_t = hd_t;
     plan.wide = wide;
+    plan.mixed = mixed;
 
     // The append can run inside the attention launch when no query reads a
     // token that another workgroup appends: the call is causal, every row's
@@ -1751,6 +1831,7 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.items = blob + static_cast<size_t>(plan.n_groups) * kGroupWords;
     a.ranges = a.items + static_cast<size_t>(plan.n_items) * kItemWords;
     a.bitems = a.ranges + 2 * static_cast<size_t>(sp.m);
+    a.order = a.bitems + static_cast<size_t>(plan.n_bitems) * kBItemWords;
     a.table = pool->table_dev;
     a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
     a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
@@ -1785,15 +1866,18 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     const uint64_t n_pwg = static_cast<uint64_t>(plan.n_bitems) * pool->kv_heads;
     if (n_wg > 0x7FFFFFFFull || n_pwg > 0x7FFFFFFFull)
         throw HipError{hipErrorInvalidConfiguration, "attention grid too large"};
-    // A mixed call runs the decode items, then the prefill blocks, on the
-    // caller's stream.  (Running the prefill kernel concurrently on a second
-    // stream measured slower once the prefill kernel ran two workgroups per
-    // CU: 262 vs 248 us per C3 layer.)
-    if (n_wg) {
+    // A call with decode items and attn_prefill_wide blocks runs them in one
+    // interleaved launch; otherwise the decode items, then the prefill
+    // blocks, on the caller's stream.  (Running the prefill kernel on a
+    // second stream measured slower: 262 vs 248 us per C3 layer.)
+    if (plan.mixed) {
+        launch_mixed(hd_t, f16, dim3(static_cast<uint32_t>(n_wg + n_pwg)), a, s);
+        THB_HIP(hipGetLastError());
+    } else if (n_wg) {
         launch(hd_t, f16, dim3(static_cast<uint32_t>(n_wg)), a, s);
         THB_HIP(hipGetLastError());
     }
-    if (n_pwg) {
+    if (n_pwg && !plan.mixed) {
         launch_prefill(hd_t, plan.wide, f16, dim3(static_cast<uint32_t>(n_pwg)), a, s);
         THB_HIP(hipGetLastError());
     }
