@@ -509,9 +509,10 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     // source is loaded after it, so the barrier's wait does not take a second
     // round trip.  The source load then completes beside the first tile
     // loads.  When the token lies beyond the wave's first NB tiles, the store
-    // is issued after those tiles' loads (below): a wave's waits for loads
-    // issued after a store also wait for the store, which is acknowledged
-    // long after it is issued.  Otherwise it is stored before any tile load.
+    // is issued in the tile loop, right before the load of the token's tile:
+    // a wave's waits for loads issued after a store also wait for the store,
+    // which is acknowledged long after it is issued.  Otherwise it is stored
+    // before any tile load.
     if (lane < app_items && !rope) app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
     __syncthreads();
     if (app_own) {
@@ -652,19 +653,24 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
 #pragma unroll
         for (int b = 0; b < NB; b++)
             if (ws + 16u * b < we) load(ws + 16u * b, kr[b], vr[b]);
-        // The token lies at or beyond tile NB of this wave: no load issued so
-        // far reads it, and every later load of it follows this store.
-        if (app_late) {
-            app_store(app_pos, app_v, app_d, app_w);
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        }
         for (uint32_t t0 = ws; t0 < we; t0 += 16u * NB) {
 #pragma unroll
             for (int b = 0; b < NB; b++) {
                 const uint32_t t = t0 + 16u * b;
                 if (t < we) {
                     compute(t, kr[b], vr[b]);
-                    if (t + 16u * NB < we) load(t + 16u * NB, kr[b], vr[b]);
+                    const uint32_t tn = t + 16u * NB;
+                    if (tn < we) {
+                        // The token lies beyond tile NB of this wave: it is
+                        // stored just before the load of its own tile, so
+                        // only the waits for that tile (whose load latency
+                        // covers the store's) also wait for the store.
+                        if (app_late && app_pos - tn < 16u) {
+                            app_store(app_pos, app_v, app_d, app_w);
+                            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                        }
+                        load(tn, kr[b], vr[b]);
+                    }
                 }
             }
         }
