@@ -1021,13 +1021,16 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
 #ifndef THB_PREFILL_TILE
 #define THB_PREFILL_TILE 64
 #endif
+#ifndef THB_PREFILL_NCG
+#define THB_PREFILL_NCG 2
+#endif
 template <int HD, bool F16, int W, bool FULL, bool CAP>
 __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
     constexpr int KS = HD / 32;
     constexpr int MT = HD / 16;
-    constexpr int NCG = 2;                 // column groups per wave
+    constexpr int NCG = THB_PREFILL_NCG;   // column groups per wave
     // Probabilities with an f16 KV: one f16 operand (relative error <= 2^-12,
     // so each output moves by at most 2^-12 max|v - y|).  With bf16 (8 bits)
     // they keep the high + low split of the decode kernels.
@@ -1349,7 +1352,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
 }
 
 template <int HD, bool F16, int W, bool FULL, bool CAP>
-__global__ __launch_bounds__(64 * W, 2) void attn_prefill_wide(AttnArgs a) {
+__global__ __launch_bounds__(64 * W, W >= 8 ? W / 4 : 1) void attn_prefill_wide(AttnArgs a) {
     prefill_wide_wg<HD, F16, W, FULL, CAP>(a, blockIdx.x);
 }
 
@@ -1400,7 +1403,7 @@ void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s
 // Query groups per prefill block: 2 per wave of attn_prefill_wide, 1 per wave
 // of attn_prefill (wider heads).
 constexpr uint32_t block_groups(bool wide, uint32_t hd_t) {
-    return wide ? 2 * THB_PREFILL_WAVES : static_cast<uint32_t>(waves_for(static_cast<int>(hd_t)));
+    return wide ? THB_PREFILL_NCG * THB_PREFILL_WAVES : static_cast<uint32_t>(waves_for(static_cast<int>(hd_t)));
 }
 
 // Score scale applied to the query (log2 units, or 1 / softcap).
