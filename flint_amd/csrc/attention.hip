@@ -995,12 +995,14 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
     }
 }
 
-// Chunked prefill at head_dim <= 128 (attn_prefill serves wider heads).  One
-// workgroup of W waves handles a block of up to 2W consecutive groups of one
-// chunk, for one KV head and one partition of the block's key span.  Wave w
-// owns groups g0 + 2w and g0 + 2w + 1 (32 query columns), so every K and V
-// operand read from LDS feeds four matrix-core products (two column groups,
-// high and low halves).  Keys advance 32 at a time:
+// Chunked prefill at head_dim <= 128 (attn_prefill serves wider heads and
+// scales above one), as the workgroup body of attn_prefill_wide and
+// attn_mixed.  One workgroup of W waves handles a block of up to NCG * W
+// consecutive groups of one chunk, for one KV head and one partition of the
+// block's key span.  Wave w owns groups g0 + NCG w .. + NCG - 1 (16 NCG query
+// columns), so every K and V operand read from LDS feeds a product for each
+// of its groups (two for the query's high and low halves in QK^T).  Keys
+// advance 32 at a time:
 //  * QK^T: two 16-token products per column group (S^T[16 tok x 16 col],
 //    v_mfma_f32_16x16x32), which leave lane (a, c) with tokens 4a..4a+3 of
 //    each half;
