@@ -36,7 +36,7 @@ struct AttnPlan {
     uint32_t n_blocks = 0, n_bitems = 0;    // prefill blocks and their work items
     uint32_t n_slots = 0;                   // partial-result slots (all groups' partitions)
     uint32_t hd_t = 0;   // head_dim template of the kernel
-    bool wide = false;   // prefill blocks run attn_prefill_wide (part of the key: it fixes the block size)
+    bool wide = false;   // prefill blocks run attn_prefill_wide (head_dim <= 128)
     bool mixed = false;  // decode items and prefill blocks run as one launch (attn_mixed)
     bool split = false;  // some group spans several partitions: merge kernel runs
     bool fusable = false;  // an append of the call's rows can run inside the launch

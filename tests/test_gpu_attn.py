@@ -331,7 +331,7 @@ PREFILL_CASES = [
     # the head_dim <= 128 kernel with soft-cap and a window, and with bf16 probabilities split in two
     ("hd128-window-softcap", 32, 8, 128, 16, "f16", 3000, 200, 1024, 30.0),
     ("hd64-bf16-softcap-split", 8, 2, 64, 16, "bf16", 6000, 130, 0, 20.0),
-    # a score scale above 1 / log2(e): the query cannot carry it, the other prefill kernel runs
+    # a score scale above 1 / log2(e): the query carries it times 2^-1
     ("hd128-scale-above-one", 32, 8, 128, 16, "f16", 500, 100, 0, 0.0, 1.0),
 ]
 

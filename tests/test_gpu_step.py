@@ -141,3 +141,94 @@ def test_attn_step_errors(torch_cuda):
     ops.attn_step(pool, 0, spec, q, y, q_stride=128, gate=q[..., 64:], gate_stride=128)
     torch.cuda.synchronize()
     assert torch.allclose(y, torch.zeros_like(y))  # zero V: y = 0 whatever the gate
+
+
+MIXED_CASES = [
+    # name, rope + q/k norm + gate, softcap, window
+    ("mixed-rope-gate", True, 0.0, 0),
+    ("mixed-softcap-window", False, 30.0, 1000),
+]
+
+
+@pytest.mark.parametrize("case", MIXED_CASES, ids=[c[0] for c in MIXED_CASES])
+def test_mixed_decode_and_prefill_one_call(torch_cuda, case):
+    """Decode rows (one spanning several partitions) and a prefill chunk in
+    ONE call run as one interleaved launch: against the oracle within 2e-3,
+    and bit-identical to the decode rows and the chunk called on their own."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+    from flint_amd.rope import Rope, rope_tables
+
+    name, use_rope, cap, window = case
+    say("mixed step", name)
+    nq, nkv, hd, chunk = 16, 4, 128, 64
+    lens = [9000, 700, 300]
+    budget = [lens[0] + 1, lens[1] + 1, lens[2] + chunk]
+    seed = zlib.crc32(name.encode())
+    pool = make_pool(budget, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype="f16", extra_pages=3)
+    scattered_alloc(pool, budget, random.Random(seed), 16)
+    rows = RowMeta(512)
+    fill(torch, pool, rows, lens, seed=7, scale=2.0 if cap else 1.0)
+    positions = [lens[0], lens[1]] + list(range(lens[2], lens[2] + chunk))
+    seqs = [0, 1] + [2] * chunk
+    m = len(seqs)
+    rng = np.random.default_rng(seed)
+    rope = cos = sin = qn = kn = None
+    if use_rope:
+        cos, sin = rope_tables(max(budget) + 1, hd, hd, 1e6)
+        qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+        kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+        rope = Rope(cos, sin, hd, q_norm=qn, k_norm=kn, eps=1e-6)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed & 0xFFFF)
+    qg = torch.randn(m, nq, 2 * hd, device="cuda", generator=g) * (2.0 if cap else 1.0)
+    k_new = torch.randn(m, nkv, hd, device="cuda", generator=g)
+    v_new = torch.randn(m, nkv, hd, device="cuda", generator=g)
+    rows.write(positions, seqs, m)
+    ref = oracle_layer(torch, pool)
+    kr = k_new.cpu().numpy()
+    q = np.ascontiguousarray(qg[..., :hd].cpu().numpy())
+    gate = qg[..., hd:].cpu().numpy()
+    if use_rope:
+        kr = oracle.rope_rows(kr, positions, hd, cos, sin, w=kn)
+        q = oracle.rope_rows(q, positions, hd, cos, sin, w=qn)
+    meta = oracle.row_meta(positions, seqs)
+    ref.kv_store(np.ascontiguousarray(kr), v_new.cpu().numpy(), meta, m, oracle.SRC_F32)
+    scale = 1 / math.sqrt(hd)
+    want = ref.attn(q, meta, m, nq, scale, window=window, softcap=cap)
+    if use_rope:
+        want = want * _sigmoid(gate)
+
+    def spec_for(rw, n):
+        return ops.AttnSpec(q_heads=nq, window=window, scale=scale, m=n, causal=True, seq=None, args=rw,
+                            softcap=cap)
+
+    def step(rw, idx, y, append):
+        qq = qg[idx].contiguous() if idx is not None else qg
+        kw = dict(q_stride=2 * hd, rope=rope)
+        if use_rope:
+            kw.update(gate=qq[..., hd:], gate_stride=2 * hd)
+        if append:
+            kw.update(k_src=k_new, v_src=v_new)
+        ops.attn_step(pool, 0, spec_for(rw, qq.shape[0]), qq, y, **kw)
+
+    y = torch.empty(m, nq, hd, device="cuda")
+    step(rows, None, y, True)
+    torch.cuda.synchronize()
+    k2, v2 = pool.read_layer(0)
+    assert np.array_equal(k2, ref.k) and np.array_equal(v2, ref.v), name
+    diff = np.abs(y.cpu().numpy() - want)
+    err = float(np.max(diff))
+    say("mixed step", name, "max abs err", err, "worst row", int(np.argmax(diff.reshape(m, -1).max(axis=1))),
+        "decode rows", float(diff[:2].max()))
+    assert err <= TOL, name
+    # the decode rows alone, then the chunk alone (keys already appended)
+    rows_solo = RowMeta(512)
+    for idx in ([0, 1], list(range(2, m))):
+        rows_solo.write([positions[i] for i in idx], [seqs[i] for i in idx], len(idx))
+        ys = torch.empty(len(idx), nq, hd, device="cuda")
+        step(rows_solo, idx, ys, False)
+        torch.cuda.synchronize()
+        assert torch.equal(ys, y[idx]), (name, "batch == solo", idx[0])
+    pool.close()
