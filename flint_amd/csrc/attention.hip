@@ -107,7 +107,7 @@ struct AttnArgs {
     // attn_prefill_wide: the query carries qpre = the sign of qscale (an exact
     // multiply), and qpost = |qscale| scales its products inside the
     // exponent's fma.  (Splitting q * qscale into f16 halves instead measured
-    // ~100x larger errors against the oracle, 2.6e-5 vs 3e-7.)
+    // ~100x larger errors against an exact softmax, 2.6e-5 vs 3e-7.)
     float qpre, qpost;
     uint32_t q_dt, y_dt;       // THB_DT_* of the query (and gate) and of the output
     uint32_t q_stride;         // elements from one query head to the next
@@ -1268,7 +1268,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
             for (int e = 0; e < 8; e++) p[e] = fast_exp2(CAP ? x[e] - m[g] : __builtin_fmaf(x[e], a.qpost, -m[g]));
             // High and low halves, as in the decode kernels: one f16 operand
             // alone (relative error 2^-12) measured 1e-4 .. 5e-4 against the
-            // oracle on N(0,1) .. N(0,4) data, both halves 3e-7.
+            // exact softmax on N(0,1) .. N(0,4) data, both halves 3e-7.
             O::split8(p, ph[g], pl[g]);
         }
 #pragma unroll
