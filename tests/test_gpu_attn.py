@@ -50,6 +50,8 @@ def check_parity(torch, pool, rows, q, positions, seqs, label, **kw):
     say(label, "max abs err", err)
     assert np.all(np.isfinite(got)), label
     assert err <= TOL, (label, err)
+    if y.dtype == torch.float32:
+        assert err <= TIGHT, (label, "precision regression", err)
     return y
 
 
@@ -148,6 +150,8 @@ def test_reference_mode_chunk(torch_cuda, causal):
     err = float(np.max(np.abs(y.cpu().numpy() - want)))
     say("reference-mode chunk causal", causal, err)
     assert err <= TOL
+    if y.dtype == torch.float32:
+        assert err <= TIGHT, ("reference-mode chunk", "precision regression", err)
 
 
 def test_reference_anchor_through_gpu(torch_cuda, golden):
@@ -242,6 +246,8 @@ def test_llama3_full_shape_sampled(torch_cuda):
         err = float(np.max(np.abs(y[s:s + 1].cpu().numpy() - want)))
         say("llama3 full seq", s, err)
         assert err <= TOL
+        if y.dtype == torch.float32:
+            assert err <= TIGHT, ("llama3 full seq", s, "precision regression", err)
 
 
 def test_attn_errors(torch_cuda):
@@ -324,6 +330,8 @@ def test_fused_append_matches_separate_calls(torch_cuda, case):
     err = float(np.max(np.abs(yb.cpu().numpy() - want)))
     say("fused append", name, "max abs err", err)
     assert err <= TOL
+    if yb.dtype == torch.float32:
+        assert err <= TIGHT, (name, "precision regression", err)
 
 
 PREFILL_CASES = [
