@@ -752,16 +752,37 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
     const uint32_t ncols = R * H;
     const uint32_t hd = a.head_dim;
     const uint64_t base = static_cast<uint64_t>(item0) * a.n_kvh + kvh;  // partition pi: base + pi * n_kvh
+    // Partitions are read eight at a time, all eight loads issued before the
+    // first is used (one round trip per eight partitions, not one each); the
+    // sums still run in partition order.
+    constexpr uint32_t U = 8;
     if (tid < ncols) {
+        const uint64_t mstep = 2 * static_cast<uint64_t>(a.n_kvh) * kCols;
+        const float* ml = a.part_ml + 2 * (base * kCols + tid);
         float M = kFloor;
-        for (uint32_t pi = 0; pi < n_parts; pi++)
-            M = fmaxf(M, a.part_ml[2 * ((base + static_cast<uint64_t>(pi) * a.n_kvh) * kCols + tid)]);
+        for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
+            float mv[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; u++) mv[u] = p0 + u < n_parts ? ml[(p0 + u) * mstep] : kFloor;
+#pragma unroll
+            for (uint32_t u = 0; u < U; u++) M = fmaxf(M, mv[u]);
+        }
         float L = 0.0f;
-        for (uint32_t pi = 0; pi < n_parts; pi++) {
-            const uint64_t b = 2 * ((base + static_cast<uint64_t>(pi) * a.n_kvh) * kCols + tid);
-            const float w = fast_exp2(a.part_ml[b] - M);
-            s_w[pi * kCols + tid] = w;
-            L += w * a.part_ml[b + 1];
+        for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
+            float mv[U], lv[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; u++) {
+                const bool in = p0 + u < n_parts;
+                mv[u] = in ? ml[(p0 + u) * mstep] : kFloor;
+                lv[u] = in ? ml[(p0 + u) * mstep + 1] : 0.0f;
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < U; u++) {
+                if (p0 + u >= n_parts) break;
+                const float w = fast_exp2(mv[u] - M);
+                s_w[(p0 + u) * kCols + tid] = w;
+                L += w * lv[u];
+            }
         }
         s_inv[tid] = 1.0f / L;
     }
@@ -771,7 +792,16 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
         const uint32_t c = idx / hd, d = idx - c * hd;
         const float* src = a.part_o + (base * kCols + c) * HD + d;
         float acc = 0.0f;
-        for (uint32_t pi = 0; pi < n_parts; pi++) acc += s_w[pi * kCols + c] * src[pi * step];
+        for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
+            float ov[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; u++) ov[u] = p0 + u < n_parts ? src[(p0 + u) * step] : 0.0f;
+#pragma unroll
+            for (uint32_t u = 0; u < U; u++) {
+                if (p0 + u >= n_parts) break;
+                acc += s_w[(p0 + u) * kCols + c] * ov[u];
+            }
+        }
         const float yv[1] = {acc * s_inv[c]};
         const uint32_t rr = c / H, hh = c - rr * H;
         store_y<1, FULL>(a, r0 + rr, kvh * a.nq_per_kv + h0 + hh, d, yv);
