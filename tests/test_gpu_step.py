@@ -150,9 +150,10 @@ def test_attn_step_errors(torch_cuda):
 
 
 MIXED_CASES = [
-    # name, rope + q/k norm + gate, softcap, window
-    ("mixed-rope-gate", True, 0.0, 0),
-    ("mixed-softcap-window", False, 30.0, 1000),
+    # name, rope + q/k norm + gate, softcap, window, (q heads, KV heads, head_dim, KV type)
+    ("mixed-rope-gate", True, 0.0, 0, (16, 4, 128, "f16")),
+    ("mixed-softcap-window", False, 30.0, 1000, (16, 4, 128, "f16")),
+    ("mixed-qwen2-hd64-bf16", False, 0.0, 0, (14, 2, 64, "bf16")),
 ]
 
 
@@ -166,13 +167,13 @@ def test_mixed_decode_and_prefill_one_call(torch_cuda, case):
     from flint_amd.pool import RowMeta
     from flint_amd.rope import Rope, rope_tables
 
-    name, use_rope, cap, window = case
+    name, use_rope, cap, window, (nq, nkv, hd, kv) = case
     say("mixed step", name)
-    nq, nkv, hd, chunk = 16, 4, 128, 64
+    chunk = 64
     lens = [9000, 700, 300]
     budget = [lens[0] + 1, lens[1] + 1, lens[2] + chunk]
     seed = zlib.crc32(name.encode())
-    pool = make_pool(budget, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype="f16", extra_pages=3)
+    pool = make_pool(budget, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype=kv, extra_pages=3)
     scattered_alloc(pool, budget, random.Random(seed), 16)
     rows = RowMeta(512)
     fill(torch, pool, rows, lens, seed=7, scale=2.0 if cap else 1.0)
