@@ -311,15 +311,65 @@ struct DivSmall {
     __device__ uint32_t operator()(uint32_t u) const { return static_cast<uint32_t>((u * m) >> 32); }
 };
 
+// Lane l of a quad holds row l of a 4 x 4 matrix of words in a[0..3] and
+// ends with column l (a[k] = the old a[l] of quad lane k): two exchanges of
+// two words each, with lane l ^ 2 and then with lane l ^ 1 (DPP quad
+// permutations; all 4 lanes of the quad must be active).
+template <int CTRL>
+__device__ inline uint32_t quad_perm(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), CTRL, 0xF, 0xF, false));
+}
+__device__ inline void quad_transpose(uint32_t (&a)[4], uint32_t l) {
+    const bool b1 = (l & 2u) != 0, b0 = (l & 1u) != 0;
+    {
+        const uint32_t r0 = quad_perm<0x4E>(b1 ? a[0] : a[2]), r1 = quad_perm<0x4E>(b1 ? a[1] : a[3]);
+        a[0] = b1 ? r0 : a[0];
+        a[1] = b1 ? r1 : a[1];
+        a[2] = b1 ? a[2] : r0;
+        a[3] = b1 ? a[3] : r1;
+    }
+    {
+        const uint32_t r0 = quad_perm<0xB1>(b0 ? a[0] : a[1]), r1 = quad_perm<0xB1>(b0 ? a[2] : a[3]);
+        a[0] = b0 ? r0 : a[0];
+        a[2] = b0 ? r1 : a[2];
+        a[1] = b0 ? a[1] : r0;
+        a[3] = b0 ? a[3] : r1;
+    }
+}
+
+// The 4 lanes of a quad hold the V page units of dims 8c .. 8c + 7 of one
+// 4-slot group (lane l: dims 8c + 2l and 8c + 2l + 1; element i of the unit
+// is slot i % 4 of dim 8c + 2l + i / 4).  Returns slot l's 8 dims in order:
+// lane l's row of the flat layout.
+__device__ inline uint4 v_units_to_row(const uint4& w, uint32_t l) {
+    // a[s]: (dim 8c + 2l, dim 8c + 2l + 1) of slot s
+    uint32_t a[4] = {(w.x & 0xffffu) | (w.z << 16), (w.x >> 16) | (w.z & 0xffff0000u), (w.y & 0xffffu) | (w.w << 16),
+                     (w.y >> 16) | (w.w & 0xffff0000u)};
+    quad_transpose(a, l);  // a[k]: (dim 8c + 2k, dim 8c + 2k + 1) of slot l
+    return make_uint4(a[0], a[1], a[2], a[3]);
+}
+
+// Inverse of v_units_to_row: lane l holds slot l's dims 8c .. 8c + 7 and
+// gets the page unit of dims 8c + 2l, 8c + 2l + 1 over the group's 4 slots.
+__device__ inline uint4 v_row_to_units(const uint4& r, uint32_t l) {
+    uint32_t a[4] = {r.x, r.y, r.z, r.w};
+    quad_transpose(a, l);  // a[s]: (dim 8c + 2l, dim 8c + 2l + 1) of slot s
+    return make_uint4((a[0] & 0xffffu) | (a[1] << 16), (a[2] & 0xffffu) | (a[3] << 16),
+                      (a[0] >> 16) | (a[1] & 0xffff0000u), (a[2] >> 16) | (a[3] & 0xffff0000u));
+}
+
 // Gather (TO_FLAT) or scatter (!TO_FLAT) of tokens [t0, t0 + n) of one
 // sequence.  One workgroup per (page of the range, group of `heads` KV
 // heads).  K: a token's 8-dimension chunk is 16 contiguous bytes on both
-// sides.  V: a tile of up to 64 slots goes through LDS as [slot][dim]
-// (rows of head_dim + 8 elements, 16-byte aligned); the page side moves as
-// 16-byte units (2 dims x the 4 slots of a group), the flat side as 16-byte
-// (slot, 8 dims) vectors.  A group that the range cuts is merged into its
-// 16 bytes by one lane.  A tile's K and V loads are issued together, two of
-// each per lane at a time.
+// sides.  V, page side: 16-byte units (2 dims x the 4 slots of a group);
+// flat side: 16-byte (slot, 8 dims) vectors.
+// * A page the range covers whole: every lane moves one K vector (flat
+//   order) and one V unit (page order) per round, two rounds in flight; the
+//   4 lanes of a quad hold the 4 units of one group's 8 dims and trade them
+//   into 4 flat rows in registers (no LDS, no barrier).
+// * A page the range cuts: a tile of up to 64 slots of V goes through LDS as
+//   [slot][dim] (rows of head_dim + 8 elements, 16-byte aligned), and a group
+//   that the range cuts is merged into its 16 bytes by one lane.
 template <bool TO_FLAT>
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     extern __shared__ uint4 s_tile[];
@@ -341,6 +391,46 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     auto k_paged = [&](uint32_t hh, uint32_t j, uint32_t c) { return a.k + pbase(hh) + k_off(j, 8u * c, hd, shift); };
     auto v_paged = [&](uint32_t hh, uint32_t j4, uint32_t d) { return a.v + pbase(hh) + v_off(j4, d, hd); };
     const DivSmall by_cph(cph), by_dp(hd >> 1);
+    if (ja == 0 && jb == (1u << shift)) {
+        // vectors per head plane: hd * page_len / 8, a multiple of 8, so the
+        // bound below keeps whole quads active
+        const uint32_t vecs = (hd << shift) >> 3, NV = a.heads * vecs, l = threadIdx.x & 3u;
+        const DivSmall by_vecs(vecs);
+        for (uint32_t u0 = threadIdx.x; u0 < NV; u0 += 512) {
+            uint4 kr[2], vr[2];
+#pragma unroll
+            for (uint32_t i = 0; i < 2; i++) {
+                const uint32_t u = u0 + 256 * i;
+                if (u >= NV) continue;
+                const uint32_t hh = by_vecs(u), r = u - hh * vecs;
+                const uint32_t t = by_cph(r), c = r - t * cph;  // K: token t, chunk c
+                const uint32_t q = by_dp(r), c8 = (r - q * (hd >> 1)) >> 2;  // V unit r: group q, dims 8 c8 + 2 l
+                if constexpr (TO_FLAT) {
+                    kr[i] = ld_stream16(k_paged(hh, t, c));
+                    vr[i] = ld_stream16(a.v + pbase(hh) + 8u * r);
+                } else {
+                    kr[i] = ld_stream16(a.k_flat + flat_off(hh, t, c));
+                    vr[i] = ld_stream16(a.v_flat + flat_off(hh, 4u * q + l, c8));
+                }
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 2; i++) {
+                const uint32_t u = u0 + 256 * i;
+                if (u >= NV) continue;
+                const uint32_t hh = by_vecs(u), r = u - hh * vecs;
+                const uint32_t t = by_cph(r), c = r - t * cph;
+                const uint32_t q = by_dp(r), c8 = (r - q * (hd >> 1)) >> 2;
+                if constexpr (TO_FLAT) {
+                    st_stream16(a.k_flat + flat_off(hh, t, c), kr[i]);
+                    st_stream16(a.v_flat + flat_off(hh, 4u * q + l, c8), v_units_to_row(vr[i], l));
+                } else {
+                    st_stream16(k_paged(hh, t, c), kr[i]);
+                    st_stream16(a.v + pbase(hh) + 8u * r, v_row_to_units(vr[i], l));
+                }
+            }
+        }
+        return;
+    }
     for (uint32_t tb = ja & ~(T - 1u); tb < jb; tb += T) {
         const uint32_t lo = max(ja, tb), hi = min(jb, tb + T);
         const uint32_t q_lo = (lo - tb) >> 2, q_hi = (hi - tb + 3u) >> 2;  // 4-slot groups the range touches

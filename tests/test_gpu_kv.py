@@ -109,37 +109,50 @@ def test_kv_store_reference_lcg_vector(torch_cuda, golden):
     assert np.array_equal(got_v, np.array(case["expect_v"], np.uint16))
 
 
-@pytest.mark.parametrize("hd", [64, 128, 256])
-def test_gather_scatter_round_trip(torch_cuda, hd):
+@pytest.mark.parametrize("hd,pl", [(64, 16), (128, 16), (256, 16), (80, 8), (128, 32), (96, 64)])
+def test_gather_scatter_round_trip(torch_cuda, hd, pl):
+    """Gather and scatter over ranges that cut a page at both ends and cover
+    whole pages between (the whole pages take the register-transpose path,
+    the cut ones the LDS path); head_dim 80 and 96 end K in a group narrower
+    than 32 dims, head_dim 64 at page 16 and 80 at page 8 put several KV
+    heads in one workgroup."""
     torch = torch_cuda
     from flint_amd import ops
     from flint_amd.pool import RowMeta
 
-    say("gather/scatter", hd)
-    rng = random.Random(hd)
-    lens = [100, 47]
-    pool = make_pool(lens, kv_heads=2, head_dim=hd, page_len=16, kv_dtype="f16", layers=2, extra_pages=4)
-    scattered_alloc(pool, lens, rng, 16)
+    say("gather/scatter", hd, pl)
+    rng = random.Random(hd * 1000 + pl)
+    lens = [6 * pl + 4, 3 * pl + 4]
+    pool = make_pool(lens, kv_heads=2, head_dim=hd, page_len=pl, kv_dtype="f16", layers=2, extra_pages=4)
+    scattered_alloc(pool, lens, rng, pl)
     rows = RowMeta(128)
     fill(torch, pool, rows, lens, layer=1, seed=3)
     ref = oracle_layer(torch, pool, layer=1)
-    kd = torch.empty(2, 61, hd, dtype=torch.int16, device="cuda")
+    g0, gn = pl + 3, 4 * pl + 4  # pages 1 (cut), 2..4 (whole), 5 (cut)
+    kd = torch.empty(2, gn, hd, dtype=torch.int16, device="cuda")
     vd = torch.empty_like(kd)
-    ops.kv_gather(pool, 1, 0, 30, 61, kd, vd)
+    ops.kv_gather(pool, 1, 0, g0, gn, kd, vd)
     torch.cuda.synchronize()
-    rk, rv = ref.gather(0, 30, 61)
+    rk, rv = ref.gather(0, g0, gn)
     assert np.array_equal(kd.cpu().numpy().view(np.uint16), rk)
     assert np.array_equal(vd.cpu().numpy().view(np.uint16), rv)
-    # scatter new words into seq 1 tokens [5, 40), gather back
-    nk = torch.randint(-30000, 30000, (2, 35, hd), dtype=torch.int16, device="cuda")
-    nv = torch.randint(-30000, 30000, (2, 35, hd), dtype=torch.int16, device="cuda")
-    ops.kv_scatter(pool, 1, 1, 5, 35, nk, nv)
-    ops.kv_gather(pool, 1, 1, 5, 35, kd[:, :35].contiguous(), vd[:, :35].contiguous())
-    k2 = torch.empty(2, 35, hd, dtype=torch.int16, device="cuda")
+    # scatter new words into seq 1 tokens [5, 2 pl + 8): pages 0 (cut), 1 (whole), 2 (cut)
+    s0, sn = 5, 2 * pl + 3
+    nk = torch.randint(-30000, 30000, (2, sn, hd), dtype=torch.int16, device="cuda")
+    nv = torch.randint(-30000, 30000, (2, sn, hd), dtype=torch.int16, device="cuda")
+    ops.kv_scatter(pool, 1, 1, s0, sn, nk, nv)
+    k2 = torch.empty(2, sn, hd, dtype=torch.int16, device="cuda")
     v2 = torch.empty_like(k2)
-    ops.kv_gather(pool, 1, 1, 5, 35, k2, v2)
+    ops.kv_gather(pool, 1, 1, s0, sn, k2, v2)
     torch.cuda.synchronize()
     assert torch.equal(k2, nk) and torch.equal(v2, nv)
+    # the scatter left every other token of the layer as it was
+    after = oracle_layer(torch, pool, layer=1)
+    table = pool.arena.table_of(1)
+    slots = [table[t // pl] * pl + t % pl for t in range(s0, s0 + sn)]
+    ref.k[:, slots, :] = nk.cpu().numpy().view(np.uint16)
+    ref.v[:, slots, :] = nv.cpu().numpy().view(np.uint16)
+    assert np.array_equal(after.k, ref.k) and np.array_equal(after.v, ref.v)
     # layer 0 untouched by layer-1 traffic
     k0, _ = pool.layer_tensors(0)
     assert int(k0.abs().sum()) == 0
