@@ -74,59 +74,120 @@ struct RunArgs {
 
 // Tokens per run.  A 4096-row prefill call at head_dim 128 (8 KV heads) took
 // 11.1 / 9.8 / 8.2 / 9.8 us with runs of 64 / 32 / 16 / 8 tokens: 16 gives
-// 2048 workgroups, enough to keep every CU's loads in flight.
+// 2048 workgroups, enough to keep every CU's loads in flight.  Runs after a
+// chunk's first start at multiples of kRunTokens positions, so only a
+// chunk's first and last runs can cut a 4-slot V group.
 constexpr uint32_t kRunTokens = 16;
-constexpr uint32_t kMaxRunPages = kRunTokens / 8 + 1;  // pages a run touches (page_len >= 8)
+
+// Lane l of a quad holds row l of a 4 x 4 matrix of words in a[0..3] and
+// ends with column l (a[k] = the old a[l] of quad lane k): two exchanges of
+// two words each, with lane l ^ 2 and then with lane l ^ 1 (DPP quad
+// permutations; all 4 lanes of the quad must be active).
+template <int CTRL>
+__device__ inline uint32_t quad_perm(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), CTRL, 0xF, 0xF, false));
+}
+__device__ inline void quad_transpose(uint32_t (&a)[4], uint32_t l) {
+    const bool b1 = (l & 2u) != 0, b0 = (l & 1u) != 0;
+    {
+        const uint32_t r0 = quad_perm<0x4E>(b1 ? a[0] : a[2]), r1 = quad_perm<0x4E>(b1 ? a[1] : a[3]);
+        a[0] = b1 ? r0 : a[0];
+        a[1] = b1 ? r1 : a[1];
+        a[2] = b1 ? a[2] : r0;
+        a[3] = b1 ? a[3] : r1;
+    }
+    {
+        const uint32_t r0 = quad_perm<0xB1>(b0 ? a[0] : a[1]), r1 = quad_perm<0xB1>(b0 ? a[2] : a[3]);
+        a[0] = b0 ? r0 : a[0];
+        a[2] = b0 ? r1 : a[2];
+        a[1] = b0 ? a[1] : r0;
+        a[3] = b0 ? a[3] : r1;
+    }
+}
+
+// The 4 lanes of a quad hold the V page units of dims 8c .. 8c + 7 of one
+// 4-slot group (lane l: dims 8c + 2l and 8c + 2l + 1; element i of the unit
+// is slot i % 4 of dim 8c + 2l + i / 4).  Returns slot l's 8 dims in order:
+// lane l's row of the flat layout.
+__device__ inline uint4 v_units_to_row(const uint4& w, uint32_t l) {
+    // a[s]: (dim 8c + 2l, dim 8c + 2l + 1) of slot s
+    uint32_t a[4] = {(w.x & 0xffffu) | (w.z << 16), (w.x >> 16) | (w.z & 0xffff0000u), (w.y & 0xffffu) | (w.w << 16),
+                     (w.y >> 16) | (w.w & 0xffff0000u)};
+    quad_transpose(a, l);  // a[k]: (dim 8c + 2k, dim 8c + 2k + 1) of slot l
+    return make_uint4(a[0], a[1], a[2], a[3]);
+}
+
+// Inverse of v_units_to_row: lane l holds slot l's dims 8c .. 8c + 7 and
+// gets the page unit of dims 8c + 2l, 8c + 2l + 1 over the group's 4 slots.
+__device__ inline uint4 v_row_to_units(const uint4& r, uint32_t l) {
+    uint32_t a[4] = {r.x, r.y, r.z, r.w};
+    quad_transpose(a, l);  // a[s]: (dim 8c + 2l, dim 8c + 2l + 1) of slot s
+    return make_uint4((a[0] & 0xffffu) | (a[1] << 16), (a[2] & 0xffffu) | (a[3] << 16),
+                      (a[0] >> 16) | (a[1] & 0xffff0000u), (a[2] >> 16) | (a[3] & 0xffff0000u));
+}
 
 // Append of runs: consecutive rows of one sequence whose positions are
 // consecutive (a prefill chunk), up to kRunTokens tokens, across pages.  One
-// workgroup per (run, KV head).  K: one 16-byte store per (token, 8 dims).
-// V: the encoded rows are staged in LDS as [token][dim] and written as the
-// pages' 4-slot groups, 16 bytes (2 dims x 4 slots) per store where a whole
-// group lies inside the run, 2 bytes at its ends.
+// workgroup per (run, KV head); lane u moves (token u % len, 8-dimension
+// chunk u / len).  The run record is the only load ahead of the others:
+// every lane issues its source loads and its page's block-table entry
+// together.  K: one 16-byte store per (token, chunk).  V:
+// * a run of whole 4-slot groups (position and length multiples of 4): the
+//   4 lanes of a quad hold one group's 4 tokens and trade their rows into the
+//   group's 4 page units in registers, one 16-byte store each;
+// * otherwise the encoded rows are staged in LDS as [token][dim] and written
+//   as the pages' 4-slot groups, 16 bytes (2 dims x 4 slots) per store where
+//   a whole group lies inside the run, 2 bytes at its ends.
 template <uint32_t SRC, uint32_t KV>
 __global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
     extern __shared__ uint32_t s_run[];  // [len][head_dim + 2] 16-bit V slots
-    __shared__ uint32_t s_pg[kMaxRunPages];
     const uint32_t run = blockIdx.x / a.kv_heads, h = blockIdx.x - run * a.kv_heads;
     const uint32_t* R = a.runs + 4 * run;
     const uint32_t row0 = R[0], len = R[1], seq = R[2], pos0 = R[3];
     const uint32_t shift = a.page_shift, hd = a.head_dim, cph = hd >> 3, mask = (1u << shift) - 1u;
-    const uint32_t lp0 = pos0 >> shift, np = ((pos0 + len - 1) >> shift) - lp0 + 1;
-    if (threadIdx.x < np) s_pg[threadIdx.x] = a.table[static_cast<uint64_t>(seq) * a.max_pages + lp0 + threadIdx.x];
-    __syncthreads();
+    const uint32_t* trow = a.table + static_cast<uint64_t>(seq) * a.max_pages;
     const uint64_t hbase = static_cast<uint64_t>(h) * a.plane;
-    auto page_base = [&](uint32_t pos) {
-        return hbase + ((static_cast<uint64_t>(s_pg[(pos >> shift) - lp0]) * hd) << shift);
-    };
+    auto page_base = [&](uint32_t page) { return hbase + ((static_cast<uint64_t>(page) * hd) << shift); };
+    const bool whole_groups = ((pos0 | len) & 3u) == 0;  // then len * cph is a multiple of 4: whole quads
     const uint32_t rs = (hd + 2) >> 1;  // LDS row stride in 32-bit words
-    // Four (token, chunk) units per lane at a time: all their source loads are
-    // issued before the first store.
+    // Up to two (token, chunk) units per lane at a time (71 VGPRs with four,
+    // 7 waves per SIMD): all their loads are issued before the first store.
     const uint32_t units = len * cph;
-    for (uint32_t u0 = threadIdx.x; u0 < units; u0 += 4 * 256) {
-        uint4 kw[4], vw[4];
+    for (uint32_t u0 = threadIdx.x; u0 < units; u0 += 2 * 256) {
+        uint4 kw[2], vw[2];
+        uint32_t pg[2];
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
+        for (uint32_t i = 0; i < 2; i++) {
             const uint32_t u = u0 + 256 * i;
             if (u >= units) continue;
             const uint32_t ch = u / len, t = u - ch * len;
             const uint64_t e = ((static_cast<uint64_t>(row0 + t)) * a.kv_heads + h) * hd + 8u * ch;
             if (a.do_k) kw[i] = load_encode8<SRC, KV>(a.k_src, e);
             vw[i] = load_encode8<SRC, KV>(a.v_src, e);
+            pg[i] = trow[(pos0 + t) >> shift];
         }
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
+        for (uint32_t i = 0; i < 2; i++) {
             const uint32_t u = u0 + 256 * i;
             if (u >= units) continue;
             const uint32_t ch = u / len, t = u - ch * len, pos = pos0 + t;
-            if (a.do_k) *reinterpret_cast<uint4*>(a.k + page_base(pos) + k_off(pos & mask, 8u * ch, hd, shift)) = kw[i];
-            uint32_t* dst = s_run + t * rs + 4u * ch;
-            dst[0] = vw[i].x;
-            dst[1] = vw[i].y;
-            dst[2] = vw[i].z;
-            dst[3] = vw[i].w;
+            const uint64_t pb = page_base(pg[i]);
+            if (a.do_k) *reinterpret_cast<uint4*>(a.k + pb + k_off(pos & mask, 8u * ch, hd, shift)) = kw[i];
+            if (whole_groups) {
+                // a group never spans two pages (page_len is a multiple of 4)
+                const uint32_t l = t & 3u;
+                *reinterpret_cast<uint4*>(a.v + pb + v_off((pos & mask) & ~3u, 8u * ch + 2u * l, hd)) =
+                    v_row_to_units(vw[i], l);
+            } else {
+                uint32_t* dst = s_run + t * rs + 4u * ch;
+                dst[0] = vw[i].x;
+                dst[1] = vw[i].y;
+                dst[2] = vw[i].z;
+                dst[3] = vw[i].w;
+            }
         }
     }
+    if (whole_groups) return;
     __syncthreads();
     const uint16_t* sv = reinterpret_cast<const uint16_t*>(s_run);
     const uint32_t S = hd + 2;                                               // LDS row stride (16-bit)
@@ -136,7 +197,7 @@ __global__ __launch_bounds__(256) void kv_store_runs_kernel(RunArgs a) {
     // consecutive lanes write consecutive units.
     for (uint32_t u = threadIdx.x; u < dpairs * nq; u += 256) {
         const uint32_t q = u / dpairs, d = 2u * (u - q * dpairs), p4 = (Q0 + q) << 2;
-        uint16_t* dst = a.v + page_base(p4) + v_off(p4 & mask, d, hd);
+        uint16_t* dst = a.v + page_base(trow[p4 >> shift]) + v_off(p4 & mask, d, hd);
         if (p4 >= pos0 && p4 + 4 <= pos0 + len) {
             const uint32_t t = p4 - pos0;
             uint32_t w[4];
@@ -310,53 +371,6 @@ struct DivSmall {
     __device__ explicit DivSmall(uint32_t d) : m(0xFFFFFFFFull / d + 1u) {}
     __device__ uint32_t operator()(uint32_t u) const { return static_cast<uint32_t>((u * m) >> 32); }
 };
-
-// Lane l of a quad holds row l of a 4 x 4 matrix of words in a[0..3] and
-// ends with column l (a[k] = the old a[l] of quad lane k): two exchanges of
-// two words each, with lane l ^ 2 and then with lane l ^ 1 (DPP quad
-// permutations; all 4 lanes of the quad must be active).
-template <int CTRL>
-__device__ inline uint32_t quad_perm(uint32_t x) {
-    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), CTRL, 0xF, 0xF, false));
-}
-__device__ inline void quad_transpose(uint32_t (&a)[4], uint32_t l) {
-    const bool b1 = (l & 2u) != 0, b0 = (l & 1u) != 0;
-    {
-        const uint32_t r0 = quad_perm<0x4E>(b1 ? a[0] : a[2]), r1 = quad_perm<0x4E>(b1 ? a[1] : a[3]);
-        a[0] = b1 ? r0 : a[0];
-        a[1] = b1 ? r1 : a[1];
-        a[2] = b1 ? a[2] : r0;
-        a[3] = b1 ? a[3] : r1;
-    }
-    {
-        const uint32_t r0 = quad_perm<0xB1>(b0 ? a[0] : a[1]), r1 = quad_perm<0xB1>(b0 ? a[2] : a[3]);
-        a[0] = b0 ? r0 : a[0];
-        a[2] = b0 ? r1 : a[2];
-        a[1] = b0 ? a[1] : r0;
-        a[3] = b0 ? a[3] : r1;
-    }
-}
-
-// The 4 lanes of a quad hold the V page units of dims 8c .. 8c + 7 of one
-// 4-slot group (lane l: dims 8c + 2l and 8c + 2l + 1; element i of the unit
-// is slot i % 4 of dim 8c + 2l + i / 4).  Returns slot l's 8 dims in order:
-// lane l's row of the flat layout.
-__device__ inline uint4 v_units_to_row(const uint4& w, uint32_t l) {
-    // a[s]: (dim 8c + 2l, dim 8c + 2l + 1) of slot s
-    uint32_t a[4] = {(w.x & 0xffffu) | (w.z << 16), (w.x >> 16) | (w.z & 0xffff0000u), (w.y & 0xffffu) | (w.w << 16),
-                     (w.y >> 16) | (w.w & 0xffff0000u)};
-    quad_transpose(a, l);  // a[k]: (dim 8c + 2k, dim 8c + 2k + 1) of slot l
-    return make_uint4(a[0], a[1], a[2], a[3]);
-}
-
-// Inverse of v_units_to_row: lane l holds slot l's dims 8c .. 8c + 7 and
-// gets the page unit of dims 8c + 2l, 8c + 2l + 1 over the group's 4 slots.
-__device__ inline uint4 v_row_to_units(const uint4& r, uint32_t l) {
-    uint32_t a[4] = {r.x, r.y, r.z, r.w};
-    quad_transpose(a, l);  // a[s]: (dim 8c + 2l, dim 8c + 2l + 1) of slot s
-    return make_uint4((a[0] & 0xffffu) | (a[1] << 16), (a[2] & 0xffffu) | (a[3] << 16),
-                      (a[0] >> 16) | (a[1] & 0xffff0000u), (a[2] >> 16) | (a[3] & 0xffff0000u));
-}
 
 // Gather (TO_FLAT) or scatter (!TO_FLAT) of tokens [t0, t0 + n) of one
 // sequence.  One workgroup per (page of the range, group of `heads` KV
@@ -616,19 +630,23 @@ void launch_runs(uint32_t kv, dim3 grid, const RunArgs& a, hipStream_t s) {
         hipLaunchKernelGGL((kv_store_runs_kernel<SRC, THB_KV_BF16_TRUNC>), grid, dim3(256), lds, s, a);
 }
 
-// Cuts rows [0, m) of the call into runs (consecutive rows of one sequence,
-// consecutive positions, at most max_run tokens).  Returns the number of
-// rows in runs of 8 or more tokens.
+// Cuts rows [0, m) of the call into runs: chunks of consecutive rows of one
+// sequence at consecutive positions, cut where a position is a multiple of
+// max_run (so every run but a chunk's first and last covers whole 4-slot
+// groups).  Returns the number of rows in chunks of 8 or more tokens.
 uint32_t make_runs(const uint32_t* meta, uint32_t m, uint32_t max_run, std::vector<uint32_t>& runs) {
     uint32_t long_rows = 0;
     uint32_t r = 0;
     while (r < m) {
         const uint32_t seq = meta[8 * r + 1], pos0 = meta[8 * r];
         uint32_t len = 1;
-        while (r + len < m && len < max_run && meta[8 * (r + len) + 1] == seq && meta[8 * (r + len)] == pos0 + len)
-            len++;
-        runs.insert(runs.end(), {r, len, seq, pos0});
+        while (r + len < m && meta[8 * (r + len) + 1] == seq && meta[8 * (r + len)] == pos0 + len) len++;
         if (len >= 8) long_rows += len;
+        for (uint32_t t = 0; t < len;) {
+            const uint32_t n = std::min(len - t, max_run - (pos0 + t) % max_run);
+            runs.insert(runs.end(), {r + t, n, seq, pos0 + t});
+            t += n;
+        }
         r += len;
     }
     return long_rows;
