@@ -20,13 +20,21 @@ from .pool import KvPool, RowMeta, _ptr, _stream_ptr
 _DTYPES = {"f32": _lib.DT_F32, "f16": _lib.DT_F16, "bf16": _lib.DT_BF16}
 
 
+_DTYPE_OF = {}  # dtype object -> code, filled on first use
+
+
 def _dtype_code(x, default="f32") -> int:
     if x is None:
         return _DTYPES[default]
+    code = _DTYPE_OF.get(x)
+    if code is not None:
+        return code
     if isinstance(x, str):
         return _DTYPES[x]
     name = str(x).replace("torch.", "")
-    return {"float32": _lib.DT_F32, "float16": _lib.DT_F16, "bfloat16": _lib.DT_BF16}[name]
+    code = {"float32": _lib.DT_F32, "float16": _lib.DT_F16, "bfloat16": _lib.DT_BF16}[name]
+    _DTYPE_OF[x] = code
+    return code
 
 
 @dataclass

@@ -21,16 +21,34 @@ from . import _lib
 from ._lib import check, lib
 
 
-def _stream_ptr(stream) -> Optional[int]:
-    if stream is None:
+_current_stream = None  # callable: address of torch's current HIP stream, or None without a GPU
+
+
+def _current_stream_fn():
+    """Resolved once.  torch's raw-stream accessor returns the address
+    without building a Stream object (~0.3 us against ~3 us per call)."""
+    global _current_stream
+    if _current_stream is None:
         try:
             import torch
 
-            if torch.cuda.is_available():
-                return torch.cuda.current_stream().cuda_stream
+            if not torch.cuda.is_available():
+                _current_stream = lambda: None
+            else:
+                get_dev = getattr(torch._C, "_cuda_getDevice", None)
+                get_raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+                if get_dev is not None and get_raw is not None:
+                    _current_stream = lambda: get_raw(get_dev())
+                else:
+                    _current_stream = lambda: torch.cuda.current_stream().cuda_stream
         except ImportError:
-            pass
-        return None
+            _current_stream = lambda: None
+    return _current_stream
+
+
+def _stream_ptr(stream) -> Optional[int]:
+    if stream is None:
+        return _current_stream_fn()()
     if isinstance(stream, int):
         return stream
     return stream.cuda_stream
