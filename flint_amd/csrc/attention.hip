@@ -1065,7 +1065,7 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
 #ifndef THB_PREFILL_NCG
 #define THB_PREFILL_NCG 2
 #endif
-template <int HD, bool F16, int W, bool FULL, bool CAP>
+template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
 __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
@@ -1249,10 +1249,14 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int g = 0; g < NCG; g++) sc[g][h] = O::qk(kv[h], qh[g][j], sc[g][h]);
+            // The query's low half is exactly zero (QLO false: an f16 query
+            // against f16 keys): its products would add zeros.
+            if constexpr (QLO) {
 #pragma unroll
-            for (int h = 0; h < 2; h++)
+                for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int g = 0; g < NCG; g++) sc[g][h] = O::qk(kv[h], ql[g][j], sc[g][h]);
+                    for (int g = 0; g < NCG; g++) sc[g][h] = O::qk(kv[h], ql[g][j], sc[g][h]);
+            }
         }
     };
     auto softmax_pv = [&](int buf, int st, uint32_t ts, const f32x4 (&sc)[NCG][2]) {
@@ -1386,9 +1390,9 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
     }
 }
 
-template <int HD, bool F16, int W, bool FULL, bool CAP>
+template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
 __global__ __launch_bounds__(64 * W, W >= 8 ? W / 4 : 1) void attn_prefill_wide(AttnArgs a) {
-    prefill_wide_wg<HD, F16, W, FULL, CAP>(a, blockIdx.x);
+    prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, blockIdx.x);
 }
 
 // A call with decode items and prefill blocks (a continuous batch) as one
@@ -1398,13 +1402,13 @@ __global__ __launch_bounds__(64 * W, W >= 8 ? W / 4 : 1) void attn_prefill_wide(
 // HBM and workgroups busy on the matrix cores run side by side on different
 // CUs instead of one kernel after the other.  Each workgroup runs exactly
 // the code (and arithmetic) of its own kernel.
-template <int HD, bool F16, int W, bool FULL, bool CAP>
+template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
 __global__ __launch_bounds__(64 * W, 2) void attn_mixed(AttnArgs a) {
     const uint32_t rec = blockIdx.x / a.n_kvh, kvh = blockIdx.x - rec * a.n_kvh;
     const uint32_t w = a.order[rec];
     const uint32_t bid = (w & 0x7FFFFFFFu) * a.n_kvh + kvh;
     if (w >> 31)
-        prefill_wide_wg<HD, F16, W, FULL, CAP>(a, bid);
+        prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, bid);
     else
         decode_wg<HD, F16, W, ring_for(HD), FULL>(a, bid);
 }
@@ -1449,6 +1453,11 @@ float q_scale(const thb_attn_spec& sp) {
 // attn_prefill_wide serves head_dim <= 128; attn_prefill the wider heads.
 bool prefill_wide(uint32_t hd_t) { return hd_t <= 128; }
 
+// An f16 query read as it is (the lean kernels: no rotation, no norm)
+// against f16 keys: its low half after the split is exactly zero, and the
+// lean prefill kernel skips those products.
+bool query_exact(const AttnArgs& a, bool f16_kv) { return f16_kv && !a.full && a.q_dt == THB_DT_F16; }
+
 template <int HD, bool F16>
 void launch_prefill_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
     if constexpr (HD <= 128) {
@@ -1460,6 +1469,8 @@ void launch_prefill_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
             hipLaunchKernelGGL((attn_prefill_wide<HD, F16, W, true, false>), grid, dim3(64 * W), 0, s, a);
         else if (cap)
             hipLaunchKernelGGL((attn_prefill_wide<HD, F16, W, false, true>), grid, dim3(64 * W), 0, s, a);
+        else if (query_exact(a, F16))
+            hipLaunchKernelGGL((attn_prefill_wide<HD, true, W, false, false, false>), grid, dim3(64 * W), 0, s, a);
         else
             hipLaunchKernelGGL((attn_prefill_wide<HD, F16, W, false, false>), grid, dim3(64 * W), 0, s, a);
     } else {
@@ -1491,6 +1502,8 @@ void launch_mixed_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
         hipLaunchKernelGGL((attn_mixed<HD, F16, W, true, false>), grid, dim3(64 * W), 0, s, a);
     else if (cap)
         hipLaunchKernelGGL((attn_mixed<HD, F16, W, false, true>), grid, dim3(64 * W), 0, s, a);
+    else if (query_exact(a, F16))
+        hipLaunchKernelGGL((attn_mixed<HD, true, W, false, false, false>), grid, dim3(64 * W), 0, s, a);
     else
         hipLaunchKernelGGL((attn_mixed<HD, F16, W, false, false>), grid, dim3(64 * W), 0, s, a);
 }

@@ -334,6 +334,47 @@ def test_fused_append_matches_separate_calls(torch_cuda, case):
         assert err <= TIGHT, (name, "precision regression", err)
 
 
+@pytest.mark.parametrize("hd,nq,nkv", [(128, 32, 8), (64, 14, 2)])
+def test_prefill_f16_query_bit_identical_to_f32(torch_cuda, hd, nq, nkv):
+    """An f16 query against f16 keys takes the prefill kernels that skip the
+    products of the query's low half (exactly zero after the split).  The
+    output must equal, bit for bit, the same call with the query widened to
+    f32 (the kernels that compute those products): a call mixing decode rows
+    with a prefill chunk (one launch), and the chunk alone."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    say("f16 query == f32 query", hd)
+    rng = random.Random(hd)
+    lens = [1400, 777, 2100]
+    pool = make_pool(lens, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype="f16", extra_pages=3)
+    scattered_alloc(pool, lens, rng, 16)
+    rows = RowMeta(256)
+    fill(torch, pool, rows, lens, seed=hd)
+    ref = oracle_layer(torch, pool)
+    positions = list(range(1200, 1400)) + [776, 2099]
+    seqs = [0] * 200 + [1, 2]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(hd)
+    q16 = torch.randn(len(seqs), nq, hd, device="cuda", generator=g).half()
+    scale = 1.0 / math.sqrt(hd)
+    for m in (len(seqs), 200):  # mixed call, then the chunk alone
+        rows.write(positions[:m], seqs[:m], m)
+        spec = ops.AttnSpec(q_heads=nq, window=0, scale=scale, m=m, causal=True, seq=None, args=rows)
+        y16 = torch.empty(m, nq, hd, device="cuda")
+        y32 = torch.empty_like(y16)
+        ops.attn(q16[:m].contiguous(), pool, 0, y16, spec)
+        ops.attn(q16[:m].float().contiguous(), pool, 0, y32, spec)
+        torch.cuda.synchronize()
+        assert torch.equal(y16, y32), (hd, m)
+        want = ref.attn(q16[:m].float().cpu().numpy(), oracle.row_meta(positions[:m], seqs[:m]), m, nq, scale)
+        sample = [0, 1, 63, 64, 150, 199] + list(range(200, m))
+        err = float(np.max(np.abs(y16.cpu().numpy()[sample] - want[sample])))
+        say("f16 query", hd, m, "max abs err", err)
+        assert err <= TIGHT
+
+
 PREFILL_CASES = [
     # name, nq, nkv, hd, page_len, kv, prefix tokens, chunk rows, window, softcap
     ("llama-long-prefix", 32, 8, 128, 16, "f16", 9000, 300, 0, 0.0),
