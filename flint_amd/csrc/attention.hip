@@ -41,6 +41,7 @@
 //    them in partition order; there are no device-wide fences or atomics.
 #include <algorithm>
 #include <cmath>
+#include <queue>
 #include <string>
 
 #include "codec.hpp"
@@ -1737,31 +1738,84 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         blob.insert(blob.end(), bk, bk + kBlockWords);
         blob.push_back(i - bk[8]);
     }
-    // A call with both kinds of work runs them in one launch (attn_mixed),
-    // interleaved longest first by an estimate of each workgroup's time: a
-    // decode partition streams 4 * head_dim bytes per key at ~24 GB/s per
-    // CU; a prefill block pays ~6 us before its first 64-key tile and
-    // ~3.2 us per tile (head_dim 128, measured).  The order changes no row's
+    // A call with both kinds of work runs them in one launch (attn_mixed).
+    // Its order comes from a list schedule over record slots (CUs / KV
+    // heads; a record is a decode item or a prefill block over all its KV
+    // heads): at most dmax decode records run at once and the prefill blocks
+    // fill the other slots (longest first within each kind), so that HBM
+    // streams decode while the matrix cores run prefill.  The host simulates
+    // up to ~32 values of dmax and keeps the order with the shortest
+    // simulated makespan.
+    // Model (measured per workgroup): a decode workgroup streams its bytes at
+    // min(kCuBytesPerUs, kHbmBytesPerUs / decode workgroups running when it
+    // starts); a prefill block costs ~10 us plus ~4.5 us per 64-key tile
+    // (head_dim 128, beside streaming decode).  The order changes no row's
     // arithmetic.
     const bool mixed = n_items > 0 && n_bitems > 0 && wide && THB_ATTN_WAVES == THB_PREFILL_WAVES;
     if (mixed) {
-        std::vector<std::pair<float, uint32_t>> est;
-        est.reserve(n_items + n_bitems);
+        constexpr double kHbmBytesPerUs = 6.2e6, kCuBytesPerUs = 3.7e4;
+        const uint32_t n_kvh = pool->kv_heads;
+        std::vector<std::pair<double, uint32_t>> dec, pre;  // (bytes per workgroup | us, record)
+        dec.reserve(n_items);
+        pre.reserve(n_bitems);
         for (uint32_t i = 0; i < n_items; i++) {
             const uint32_t* gr = &groups[static_cast<size_t>(items[i]) * kGroupWords];
             const uint64_t p0 = uint64_t(gr[8]) + uint64_t(i - gr[10]) * gr[9];
             const uint64_t keys = gr[6] > p0 ? std::min<uint64_t>(gr[9], gr[6] - p0) : 0;
-            est.push_back({1.0f + static_cast<float>(keys) * 4.0f * hd / 24000.0f, i});
+            dec.push_back({static_cast<double>(keys) * 4.0 * hd, i});
         }
         for (uint32_t i = 0; i < n_bitems; i++) {
             const uint32_t* bk = &blocks[static_cast<size_t>(bitems[i]) * kBlockWords];
             const uint64_t p0 = uint64_t(bk[6]) + uint64_t(i - bk[8]) * bk[7];
             const uint64_t keys = bk[4] > p0 ? std::min<uint64_t>(bk[7], bk[4] - p0) : 0;
-            est.push_back({6.0f + static_cast<float>((keys + 63) / 64) * 3.2f * hd_t / 128.0f, 0x80000000u | i});
+            pre.push_back({10.0 + static_cast<double>((keys + 63) / 64) * 4.5 * hd_t / 128.0, 0x80000000u | i});
         }
-        std::stable_sort(est.begin(), est.end(),
-                         [](const std::pair<float, uint32_t>& x, const std::pair<float, uint32_t>& y) { return x.first > y.first; });
-        for (auto& e : est) blob.push_back(e.second);
+        auto longest_first = [](const std::pair<double, uint32_t>& x, const std::pair<double, uint32_t>& y) {
+            return x.first > y.first;
+        };
+        std::stable_sort(dec.begin(), dec.end(), longest_first);
+        std::stable_sort(pre.begin(), pre.end(), longest_first);
+        const uint32_t slots = std::max<uint32_t>(2, pool->cus / n_kvh);
+        std::vector<uint32_t> order, best;
+        double best_t = INFINITY;
+        const uint32_t step = std::max<uint32_t>(1, slots / 32);  // at most ~32 simulations
+        for (uint32_t dmax = 1; dmax < slots; dmax += step) {
+            std::priority_queue<std::pair<double, bool>, std::vector<std::pair<double, bool>>,
+                                std::greater<std::pair<double, bool>>>
+                running;  // (end time, decode)
+            uint32_t free_slots = slots, n_dec = 0;
+            size_t di = 0, pi = 0;
+            double t = 0.0, end = 0.0;  // dispatch time of the next record, makespan
+            order.clear();
+            while (di < dec.size() || pi < pre.size()) {
+                while (free_slots == 0) {
+                    const auto e = running.top();
+                    running.pop();
+                    t = e.first;
+                    free_slots++;
+                    if (e.second) n_dec--;
+                }
+                double done;
+                if (di < dec.size() && (n_dec < dmax || pi == pre.size())) {
+                    n_dec++;  // rate from the decode workgroups running once this one starts
+                    done = t + dec[di].first / std::min(kCuBytesPerUs,
+                                                        kHbmBytesPerUs / (static_cast<double>(n_dec) * n_kvh));
+                    running.push({done, true});
+                    order.push_back(dec[di++].second);
+                } else {
+                    done = t + pre[pi].first;
+                    running.push({done, false});
+                    order.push_back(pre[pi++].second);
+                }
+                end = std::max(end, done);
+                free_slots--;
+            }
+            if (end < best_t) {
+                best_t = end;
+                best.swap(order);
+            }
+        }
+        blob.insert(blob.end(), best.begin(), best.end());
     }
     void* dev = plan.dev.reserve(blob.size() * 4, false);
     pool->stager.upload(dev, blob.data(), blob.size() * 4, stream);

@@ -308,6 +308,9 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
         }
         p->mem_bytes = off;
         THB_HIP(hipGetDevice(&p->device));
+        int cus = 0;
+        THB_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device));
+        if (cus > 0) p->cus = static_cast<uint32_t>(cus);
         if (d->arena_dev) {
             if (d->arena_bytes < off)
                 return fail(THB_ERR_CONFIG, "external arena holds " + std::to_string(d->arena_bytes) +

@@ -81,6 +81,7 @@ struct thb_pool {
     std::array<thb::AttnPlan, 4> plans;
     uint64_t plan_clock = 0;
     int device = 0;
+    uint32_t cus = 256;  // compute units of the device (orders mixed launches)
 };
 
 namespace thb {
