@@ -68,8 +68,9 @@ constexpr uint32_t kBItemWords = kBlockWords + 1;
 // template: up to head_dim 256, 8 waves (2 per SIMD, 256 registers each),
 // with two tiles in flight up to 128 and one at 256 (the query, output and
 // load registers grow with head_dim; at 256 the second wave per SIMD hides
-// more than a second tile, 1.5% on Gemma-2 layers); at 512, 4 waves (512
-// registers each) with one tile.
+// more than a second tile, 1.5% on Gemma-2 layers, and a second tile with
+// the query halves in LDS measured 2% slower); at 512, 4 waves with one
+// tile and the query halves in LDS.
 #ifndef THB_ATTN_WAVES
 #define THB_ATTN_WAVES 8
 #endif
@@ -78,6 +79,9 @@ constexpr uint32_t kBItemWords = kBlockWords + 1;
 #endif
 constexpr int waves_for(int hd) { return hd >= 512 ? 4 : THB_ATTN_WAVES; }
 constexpr int ring_for(int hd) { return hd >= 256 ? 1 : THB_ATTN_RING; }
+// Decode keeps the query's high and low halves in LDS (one copy for the
+// workgroup's waves, which share the query group) instead of registers.
+constexpr bool q_in_lds(int hd) { return hd >= 512; }
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -461,9 +465,24 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     }
     const uint32_t cspan = chi > clo ? chi - clo : 0u;  // key t is read iff t - clo < cspan
 
-    // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8], split hi/lo.
-    in8 qh[KS], ql[KS];
-    load_q<KS, O, FULL>(a, con, row, head, a4, qh, ql);
+    // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8], split hi/lo; at
+    // head_dim 512 in LDS (wave 0 writes it before the barrier below).
+    constexpr bool QLDS = q_in_lds(HD);
+    __shared__ in8 s_q[QLDS ? KS : 1][2][64];
+    [[maybe_unused]] in8 qh[QLDS ? 1 : KS], ql[QLDS ? 1 : KS];
+    if constexpr (QLDS) {
+        if (wave == 0) {
+            in8 th[KS], tl[KS];
+            load_q<KS, O, FULL>(a, con, row, head, a4, th, tl);
+#pragma unroll
+            for (int j = 0; j < KS; j++) {
+                s_q[j][0][lane] = th[j];
+                s_q[j][1][lane] = tl[j];
+            }
+        }
+    } else {
+        load_q<KS, O, FULL>(a, con, row, head, a4, qh, ql);
+    }
 
 
     // This wave's run of 16-token tiles inside [tb, te).
@@ -615,8 +634,13 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < KS; j++) {
-            s = O::qk(kr[j], qh[j], s);
-            s = O::qk(kr[j], ql[j], s);
+            if constexpr (QLDS) {
+                s = O::qk(kr[j], s_q[j][0][lane], s);
+                s = O::qk(kr[j], s_q[j][1][lane], s);
+            } else {
+                s = O::qk(kr[j], qh[j], s);
+                s = O::qk(kr[j], ql[j], s);
+            }
         }
         float sv[4];
         float mx = -INFINITY;
