@@ -417,12 +417,16 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     typedef typename O::in4 in4;
     constexpr int KS = HD / 32;  // QK k-steps of 32 dimensions
     constexpr int MT = HD / 16;  // PV tiles of 16 dimensions
-    constexpr int HALF = W / 2 > 0 ? W / 2 : 1;
+    // The W waves' states are merged in one step (every state in LDS, each
+    // wave merging and storing its own 16-dimension tiles) where they fit
+    // beside the prefill body of attn_mixed; wider heads use a fixed tree.
+    constexpr bool FLAT = HD <= 128;
+    constexpr int NSTATE = FLAT ? W : (W / 2 > 0 ? W / 2 : 1);
 
     __shared__ uint32_t s_page[kMaxPartPages];
-    __shared__ f32x4 s_o[HALF][MT][64];
-    __shared__ float s_m[HALF][64];
-    __shared__ float s_l[HALF][64];
+    __shared__ f32x4 s_o[NSTATE][MT][64];
+    __shared__ float s_m[NSTATE][64];
+    __shared__ float s_l[NSTATE][64];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -710,6 +714,47 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
         }
     }
     l = col_sum(l);
+
+    if constexpr (FLAT) {
+        // ---- merge the W waves' states in one step ----------------------
+#pragma unroll
+        for (int i = 0; i < MT; i++) s_o[wave][i][lane] = o[i];
+        s_m[wave][lane] = m;
+        s_l[wave][lane] = l;
+        __syncthreads();
+        float M = s_m[0][lane];
+#pragma unroll
+        for (int w = 1; w < W; w++) M = fmaxf(M, s_m[w][lane]);
+        float f[W];
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            f[w] = fast_exp2(s_m[w][lane] - M);
+            L += s_l[w][lane] * f[w];
+        }
+        const uint64_t pb = (static_cast<uint64_t>(item) * a.n_kvh + kvh) * kCols + c;
+        for (uint32_t i = wave; i < static_cast<uint32_t>(MT); i += W) {  // this wave's tiles
+            f32x4 acc = s_o[0][i][lane] * f[0];
+#pragma unroll
+            for (int w = 1; w < W; w++) acc += s_o[w][i][lane] * f[w];
+            const uint32_t d = 16u * i + 4u * a4;
+            if (!con || d >= hd) continue;
+            if (n_parts == 1) {
+                const f32x4 yv = acc * (1.0f / L);
+                const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
+                store_y<4, FULL>(a, row, head, d, v4);
+            } else {
+                // several partitions: publish this one's (m, l, o); the
+                // merge kernel combines them after this kernel has finished
+                *reinterpret_cast<f32x4*>(a.part_o + pb * HD + d) = acc;
+            }
+        }
+        if (n_parts > 1 && wave == 0 && con && a4 == 0) {
+            a.part_ml[2 * pb] = M;
+            a.part_ml[2 * pb + 1] = L;
+        }
+        return;
+    }
 
     // ---- merge the W waves' states through LDS (fixed tree) -------------
     for (uint32_t half = W / 2; half >= 1; half >>= 1) {
