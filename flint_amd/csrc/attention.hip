@@ -97,6 +97,7 @@ struct AttnArgs {
     const uint32_t* ranges;  // [m][2]: lo, hi
     const uint32_t* bitems;  // prefill work items: block words + partition (kBItemWords each)
     const uint32_t* order;   // attn_mixed: launch order of decode items and prefill blocks (bit 31)
+    const uint32_t* merge_groups;  // attn_merge: the groups that span several partitions
     const uint32_t* table;
     uint16_t* k;
     uint16_t* v;
@@ -809,12 +810,14 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 }
 
 // Merges the partitions of every group that has more than one, in
-// partition order.  One workgroup per (group, KV head).
+// partition order.  One workgroup per (such group, KV head): the plan lists
+// them, so a call of many single-partition groups launches no idle
+// workgroups.
 template <int HD, bool FULL>
 __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
     __shared__ float s_w[kMaxParts * kCols];
     __shared__ float s_inv[kCols];
-    const uint32_t g = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const uint32_t g = a.merge_groups[blockIdx.x], kvh = blockIdx.y, tid = threadIdx.x;
     const uint32_t* G = a.groups + g * kGroupWords;
     const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3];
     const uint32_t n_parts = G[7], item0 = G[10];
@@ -1886,6 +1889,11 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         }
         blob.insert(blob.end(), best.begin(), best.end());
     }
+    // The groups the merge kernel combines (more than one partition).
+    const size_t merge_off = blob.size();
+    for (uint32_t gi = 0; gi < n_groups; gi++)
+        if (groups[static_cast<size_t>(gi) * kGroupWords + 7] > 1) blob.push_back(gi);
+    const uint32_t n_merge = static_cast<uint32_t>(blob.size() - merge_off);
     void* dev = plan.dev.reserve(blob.size() * 4, false);
     pool->stager.upload(dev, blob.data(), blob.size() * 4, stream);
     plan.n_groups = n_groups;
@@ -1894,6 +1902,8 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     plan.n_bitems = n_bitems;
     plan.n_slots = n_slots;
     plan.split = any_split;
+    plan.n_merge = n_merge;
+    plan.merge_off = static_cast<uint32_t>(merge_off);
     plan.hd_t = hd_t;
     plan.wide = wide;
     plan.mixed = mixed;
@@ -2008,6 +2018,7 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.ranges = a.items + static_cast<size_t>(plan.n_items) * kItemWords;
     a.bitems = a.ranges + 2 * static_cast<size_t>(sp.m);
     a.order = a.bitems + static_cast<size_t>(plan.n_bitems) * kBItemWords;
+    a.merge_groups = blob + plan.merge_off;
     a.table = pool->table_dev;
     a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
     a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
@@ -2060,7 +2071,7 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
         THB_HIP(hipGetLastError());
     }
     if (plan.split) {
-        launch_merge(hd_t, dim3(plan.n_groups, pool->kv_heads), a, s);
+        launch_merge(hd_t, dim3(plan.n_merge, pool->kv_heads), a, s);
         THB_HIP(hipGetLastError());
     }
 }

@@ -39,6 +39,7 @@ struct AttnPlan {
     bool wide = false;   // prefill blocks run attn_prefill_wide (head_dim <= 128)
     bool mixed = false;  // decode items and prefill blocks run as one launch (attn_mixed)
     bool split = false;  // some group spans several partitions: merge kernel runs
+    uint32_t n_merge = 0, merge_off = 0;  // groups of several partitions: count, blob offset (words)
     bool fusable = false;  // an append of the call's rows can run inside the launch
     DevBuf dev;  // [groups | items | row ranges]
     uint64_t last_use = 0;
