@@ -419,9 +419,10 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     constexpr int KS = HD / 32;  // QK k-steps of 32 dimensions
     constexpr int MT = HD / 16;  // PV tiles of 16 dimensions
     // The W waves' states are merged in one step (every state in LDS, each
-    // wave merging and storing its own 16-dimension tiles) where they fit
-    // beside the prefill body of attn_mixed; wider heads use a fixed tree.
-    constexpr bool FLAT = HD <= 128;
+    // wave merging and storing its own 16-dimension tiles) where they fit:
+    // up to head_dim 128 beside the prefill body of attn_mixed, at 256 (128
+    // KiB, never in attn_mixed) alone; head_dim 512 uses a fixed tree.
+    constexpr bool FLAT = HD <= 256;
     constexpr int NSTATE = FLAT ? W : (W / 2 > 0 ? W / 2 : 1);
 
     __shared__ uint32_t s_page[kMaxPartPages];
