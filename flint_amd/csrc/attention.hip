@@ -1419,13 +1419,14 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
 
     const uint32_t t_first = tb & ~31u;
     const uint32_t n_tiles = te > t_first ? (te - t_first + TT - 1) / TT : 0u;
-    // The queries are loaded and split while the page table fills s_page.
-#pragma unroll
-    for (int g = 0; g < NCG; g++) load_q<KS, O, FULL>(a, con[g], row[g], head[g], a4, qh[g], ql[g], a.qpre);
     __syncthreads();  // s_page complete
     {
         u32x4 kr[KPT], vr[VPT][2];
         if (n_tiles) load(t_first, kr, vr);
+        // The queries are loaded and split while the first tile's loads are
+        // in flight (their round trips overlap).
+#pragma unroll
+        for (int g = 0; g < NCG; g++) load_q<KS, O, FULL>(a, con[g], row[g], head[g], a4, qh[g], ql[g], a.qpre);
         if (n_tiles) store(0, kr, vr);
         __syncthreads();
         for (uint32_t i = 0; i < n_tiles; i++) {
