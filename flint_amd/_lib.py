@@ -12,7 +12,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libthuban_hip.so")
 
-ABI_VERSION = 5  # THB_ABI_VERSION of include/thuban_hip.h
+ABI_VERSION = 6  # THB_ABI_VERSION of include/thuban_hip.h
 
 THB_OK = 0
 THB_ERR_MODEL = -1
@@ -120,6 +120,7 @@ SIGNATURES = [
     ("thb_last_error", ctypes.c_char_p, []),
     ("thb_abi_version", _u32, []),
     ("thb_check_head_dim", _int, [_u32]),
+    ("thb_backend_head_dim", _int, [_u32]),
     ("thb_arena_create", _int, [_pu32, _u32, _i64, _u32, ctypes.POINTER(_vp)]),
     ("thb_arena_destroy", None, [_vp]),
     ("thb_arena_alloc", _int, [_vp, _u32, _u32, _u32]),
@@ -132,6 +133,8 @@ SIGNATURES = [
     ("thb_arena_seq_len", _int, [_vp, _u32, _pu32]),
     ("thb_arena_info_get", _int, [_vp, ctypes.POINTER(ArenaInfo)]),
     ("thb_arena_take_copies", _int, [_vp, _pu32, _sz, _pu32]),
+    ("thb_arena_free_list", _int, [_vp, _pu32, _sz, _pu32]),
+    ("thb_arena_refs", _int, [_vp, _pu32, _sz]),
     ("thb_pool_create", _int, [ctypes.POINTER(PoolDesc), ctypes.POINTER(_vp)]),
     ("thb_pool_destroy", None, [_vp]),
     ("thb_pool_alloc", _int, [_vp, _u32, _u32, _u32]),
@@ -139,6 +142,10 @@ SIGNATURES = [
     ("thb_pool_truncate", _int, [_vp, _u32, _u32]),
     ("thb_pool_fork", _int, [_vp, _u32, _u32, _u32]),
     ("thb_pool_sync", _int, [_vp, _vp]),
+    ("thb_pool_alloc_rows", _int, [_vp, _vp, _u32, _u32, _vp]),
+    ("thb_pool_status", _int, [_vp, _vp]),
+    ("thb_pool_read_state", _int, [_vp, _vp, _pu32, _sz, _pu32, _pu32, _sz, _pu32, _sz]),
+    ("thb_pool_pull", _int, [_vp, _vp]),
     ("thb_pool_arena", _vp, [_vp]),
     ("thb_pool_layer", _int, [_vp, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(LayerInfo)]),
     ("thb_pool_block_table", _int, [_vp, ctypes.POINTER(_vp)]),

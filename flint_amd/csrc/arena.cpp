@@ -136,6 +136,18 @@ std::string Arena::fork(uint32_t src, uint32_t dst, uint32_t tokens) {
     return {};
 }
 
+void Arena::load_state(const uint32_t* free_stack, uint32_t n_free, const uint32_t* refs, const uint32_t* npages,
+                       const uint32_t* table) {
+    free_.assign(free_stack, free_stack + n_free);
+    refs_.assign(refs, refs + pages_);
+    for (size_t s = 0; s < tables_.size(); s++) {
+        const uint32_t* row = table + s * max_pages_;
+        tables_[s].assign(row, row + std::min(npages[s], max_pages_));
+        touch(static_cast<uint32_t>(s));
+    }
+    copies_.clear();
+}
+
 void Arena::table(uint32_t* out) const {
     std::fill(out, out + static_cast<size_t>(tables_.size()) * max_pages_, 0xFFFFFFFFu);
     for (size_t s = 0; s < tables_.size(); s++)

@@ -38,6 +38,15 @@ public:
     uint32_t page_len() const { return page_len_; }
     uint32_t seq_len(uint32_t seq) const { return seq_lens_[seq]; }
 
+    // Free stack (back() is the next page handed out) and reference counts.
+    const std::vector<uint32_t>& free_list() const { return free_; }
+    const std::vector<uint32_t>& refs() const { return refs_; }
+    // Replaces the allocator state with a device allocator's: free stack
+    // [n_free], reference counts [pages], page counts [seqs] and the
+    // flattened table [seqs * max_pages].  Pending copies are dropped.
+    void load_state(const uint32_t* free_stack, uint32_t n_free, const uint32_t* refs, const uint32_t* npages,
+                    const uint32_t* table);
+
     // Copies recorded by fork / copy-on-write, not yet executed on a device.
     std::vector<PageCopy>& copies() { return copies_; }
     // Rows of the flattened table changed since the last clear_dirty().

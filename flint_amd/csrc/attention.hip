@@ -1650,8 +1650,7 @@ RowPlan plan_rows(const uint32_t* args, uint32_t m, uint32_t seq_fixed, bool cau
     return rp;
 }
 
-int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint32_t hd, AttnPlan& plan,
-               hipStream_t stream) {
+int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint32_t hd, AttnPlan& plan) {
     const Arena& arena = pool->arena.a;
     const uint32_t m = sp.m;
     const uint32_t* args = rows->host.data() + 8 * static_cast<size_t>(sp.row_off);
@@ -1896,8 +1895,8 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     for (uint32_t gi = 0; gi < n_groups; gi++)
         if (groups[static_cast<size_t>(gi) * kGroupWords + 7] > 1) blob.push_back(gi);
     const uint32_t n_merge = static_cast<uint32_t>(blob.size() - merge_off);
-    void* dev = plan.dev.reserve(blob.size() * 4, false);
-    pool->stager.upload(dev, blob.data(), blob.size() * 4, stream);
+    plan.blob.swap(blob);
+    plan.uploaded = false;
     plan.n_groups = n_groups;
     plan.n_items = n_items;
     plan.n_blocks = n_blocks;
@@ -1960,9 +1959,18 @@ int check_attn_call(thb_pool* pool, uint32_t layer, const void* q, void* y, cons
     return THB_OK;
 }
 
+// Copies a plan's blob to its own device buffer (once per plan).
+void upload_plan(thb_pool* pool, AttnPlan& plan, hipStream_t s) {
+    if (plan.uploaded) return;
+    void* dev = plan.dev.reserve(plan.blob.size() * 4, false);
+    pool->stager.upload(dev, plan.blob.data(), plan.blob.size() * 4, s);
+    plan.uploaded = true;
+}
+
 // Finds or builds the launch plan of this call (cached per rows write, call
-// shape and allocator state).  Runs inside guarded().
-int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint32_t hd, hipStream_t s,
+// shape and allocator state); with `upload`, its blob is on the device in
+// plan->dev.  Runs inside guarded().
+int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint32_t hd, hipStream_t s, bool upload,
              AttnPlan** out) {
     const uint64_t av = pool->arena.a.version();
     for (auto& p : pool->plans)
@@ -1970,6 +1978,7 @@ int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint
             p.m == sp.m && p.seq == sp.seq && p.causal == sp.causal && p.window == sp.window &&
             p.q_heads == sp.q_heads && p.head_dim == hd) {
             p.last_use = ++pool->plan_clock;
+            if (upload) upload_plan(pool, p, s);
             *out = &p;
             return THB_OK;
         }
@@ -1977,7 +1986,8 @@ int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint
     for (auto& p : pool->plans)
         if (p.last_use < plan->last_use) plan = &p;
     plan->rows = nullptr;
-    if (int rc = build_plan(pool, rows, sp, hd, *plan, s)) return rc;
+    if (int rc = build_plan(pool, rows, sp, hd, *plan)) return rc;
+    if (upload) upload_plan(pool, *plan, s);
     plan->rows = rows;
     plan->rows_version = rows->version;
     plan->arena_version = av;
@@ -1993,24 +2003,36 @@ int get_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, uint
     return THB_OK;
 }
 
-// Launches attention (and, when app is set, the fused append) for a plan.
-// With rope set, the query is rotated as it is loaded (and the fused append
-// rotates the key); meta is the row meta of the call's first row.
+// Bytes of split-K partial results a plan needs (0 without a split) and,
+// in *o_bytes, the size of the partial outputs that come first.
+uint64_t partial_bytes(const thb_pool* pool, const AttnPlan& plan, uint64_t* o_bytes) {
+    if (!plan.split) {
+        *o_bytes = 0;
+        return 0;
+    }
+    const uint64_t n_part = static_cast<uint64_t>(plan.n_slots) * pool->kv_heads * kCols;
+    *o_bytes = (n_part * plan.hd_t * 4 + 255) & ~uint64_t(255);
+    return *o_bytes + n_part * 8;
+}
+
+// Launches attention (and, when app is set, the fused append) for a plan
+// whose blob is at `blob` on the device, with the split-K partial results
+// (when the plan splits) at `part`.  With rope set, the query is rotated as
+// it is loaded (and the fused append rotates the key); meta is the row meta
+// of the call's first row.
 void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const thb_attn_spec& sp, const AttnPlan& plan,
-                 bool fused_append, const uint32_t* meta, hipStream_t s) {
+                 bool fused_append, const uint32_t* meta, const uint32_t* blob, uint8_t* part, hipStream_t s) {
     const thb_rope* rope = io.rope;
     const uint32_t hd = pool->geom[layer].head_dim;
     const uint32_t hd_t = plan.hd_t;
     float* part_o = nullptr;
     float* part_ml = nullptr;
     if (plan.split) {
-        const uint64_t n_part = static_cast<uint64_t>(plan.n_slots) * pool->kv_heads * kCols;
-        const uint64_t o_bytes = (n_part * hd_t * 4 + 255) & ~uint64_t(255), ml_bytes = n_part * 8;
-        uint8_t* part = static_cast<uint8_t*>(pool->partials.reserve(o_bytes + ml_bytes, false));
+        uint64_t o_bytes = 0;
+        partial_bytes(pool, plan, &o_bytes);
         part_o = reinterpret_cast<float*>(part);
         part_ml = reinterpret_cast<float*>(part + o_bytes);
     }
-    const uint32_t* blob = static_cast<const uint32_t*>(plan.dev.get());
     const LayerGeom& g = pool->geom[layer];
     AttnArgs a;
     a.q = io.q_dev;
@@ -2131,10 +2153,14 @@ int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_a
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
         AttnPlan* plan = nullptr;
-        if (int rc = get_plan(pool, rows, *spec, hd, s, &plan)) return rc;
+        if (int rc = get_plan(pool, rows, *spec, hd, s, true, &plan)) return rc;
         const uint32_t* meta = rows->dev + 8 * static_cast<size_t>(spec->row_off);
+        const uint32_t* blob = static_cast<const uint32_t*>(plan->dev.get());
+        uint64_t o_bytes = 0;
+        const uint64_t pb = partial_bytes(pool, *plan, &o_bytes);
+        uint8_t* part = pb ? static_cast<uint8_t*>(pool->partials.reserve(pb, false)) : nullptr;
         if (!append) {
-            launch_plan(pool, layer, *io, *spec, *plan, false, meta, s);
+            launch_plan(pool, layer, *io, *spec, *plan, false, meta, blob, part, s);
             return THB_OK;
         }
         // The row meta's sequence must be the one the append uses: a fixed
@@ -2144,7 +2170,7 @@ int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_a
             for (uint32_t r = spec->row_off; r < spec->row_off + spec->m && fuse; r++)
                 fuse = rows->host[8 * r + 1] == spec->seq;
         if (fuse) {
-            launch_plan(pool, layer, *io, *spec, *plan, true, meta, s);
+            launch_plan(pool, layer, *io, *spec, *plan, true, meta, blob, part, s);
             return THB_OK;
         }
         const int rc = rope ? thb_kv_store_rope(pool, layer, io->k_src_dev, io->v_src_dev, io->src_dtype, rope, rows,
@@ -2152,7 +2178,7 @@ int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_a
                             : thb_kv_store(pool, layer, io->k_src_dev, io->v_src_dev, io->src_dtype, rows,
                                            spec->row_off, spec->m, stream);
         if (rc) return rc;
-        launch_plan(pool, layer, *io, *spec, *plan, false, meta, s);
+        launch_plan(pool, layer, *io, *spec, *plan, false, meta, blob, part, s);
         return THB_OK;
     });
 }

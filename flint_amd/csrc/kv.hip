@@ -728,24 +728,23 @@ int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint3
     return THB_OK;
 }
 
-void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_t max_tokens, hipStream_t stream) {
-    if (n == 0 || max_tokens == 0) return;
+namespace {
+// Copy arguments of pool p; the triples are set by the caller.
+CopyArgs copy_args(const thb_pool* p) {
     CopyArgs a{};
     a.mem = p->mem;
     a.layers = static_cast<const DevLayer*>(p->geom_buf.get());
     a.pool_len = static_cast<uint64_t>(p->arena.a.pages()) * p->page_len;
     a.kv_heads = p->kv_heads;
     a.page_shift = p->page_shift;
-    const uint64_t planes = static_cast<uint64_t>(p->layers) * 2 * p->kv_heads;
+    return a;
+}
+
+// Launches block_copy_kernel over n triples (a.triples on the device, or
+// a.inl), one workgroup per (triple, plane).
+void launch_copy_grid(const CopyArgs& a, uint32_t n, uint32_t layers, hipStream_t stream) {
+    const uint64_t planes = static_cast<uint64_t>(layers) * 2 * a.kv_heads;
     if (planes > kMaxGridY) throw HipError{hipErrorInvalidConfiguration, "block copy: layers*2*kv_heads > 65535"};
-    if (n <= kInlineCopies) {  // a fork's or rollback's few copies: no upload
-        std::copy(triples, triples + 3 * static_cast<size_t>(n), a.inl);
-        a.triples = nullptr;
-    } else {
-        void* dev = p->copy_buf.reserve(static_cast<size_t>(n) * 12, false);
-        p->stager.upload(dev, triples, static_cast<size_t>(n) * 12, stream);
-        a.triples = static_cast<const uint32_t*>(dev);
-    }
     constexpr uint32_t kMaxGridX = 1u << 30;
     for (uint32_t i0 = 0; i0 < n; i0 += kMaxGridX) {
         CopyArgs b = a;
@@ -754,6 +753,29 @@ void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_
                            dim3(256), 0, stream, b);
         THB_HIP(hipGetLastError());
     }
+}
+}  // namespace
+
+void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_t max_tokens, hipStream_t stream) {
+    if (n == 0 || max_tokens == 0) return;
+    CopyArgs a = copy_args(p);
+    if (n <= kInlineCopies) {  // a fork's or rollback's few copies: no upload
+        std::copy(triples, triples + 3 * static_cast<size_t>(n), a.inl);
+        a.triples = nullptr;
+    } else {
+        void* dev = p->copy_buf.reserve(static_cast<size_t>(n) * 12, false);
+        p->stager.upload(dev, triples, static_cast<size_t>(n) * 12, stream);
+        a.triples = static_cast<const uint32_t*>(dev);
+    }
+    launch_copy_grid(a, n, p->layers, stream);
+}
+
+void launch_block_copy_dev(thb_pool* p, const uint32_t* triples_dev, uint32_t n, uint32_t max_tokens,
+                           hipStream_t stream) {
+    if (n == 0 || max_tokens == 0) return;
+    CopyArgs a = copy_args(p);
+    a.triples = triples_dev;
+    launch_copy_grid(a, n, p->layers, stream);
 }
 
 }  // namespace thb
@@ -848,6 +870,18 @@ static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t 
     if (!k || !v) return fail(THB_ERR_INVALID, "null buffer");
     if (!aligned16(k) || !aligned16(v)) return fail(THB_ERR_INVALID, "buffers must be 16-byte aligned");
     if (int rc = check_cover(pool, seq, static_cast<uint64_t>(t0) + n)) return rc;
+    if (!to_flat) {
+        // A scatter writes in place: a page another sequence also holds (a
+        // fork's shared prefix) would change under it.
+        const Arena& ar = pool->arena.a;
+        const auto& tbl = ar.table_of(seq);
+        const uint32_t p0 = t0 >> pool->page_shift;
+        const uint32_t p1 = static_cast<uint32_t>((static_cast<uint64_t>(t0) + n - 1) >> pool->page_shift);
+        for (uint32_t i = p0; i <= p1; i++)
+            if (ar.refs()[tbl[i]] > 1)
+                return fail(THB_ERR_MODEL, "scatter into page " + std::to_string(tbl[i]) + " of sequence " +
+                                               std::to_string(seq) + ", which is shared with another sequence");
+    }
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
@@ -908,7 +942,7 @@ int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* st
     if (!triples) return fail(THB_ERR_INVALID, "triples is null");
     const uint32_t pages = pool->arena.a.pages();
     uint32_t max_tok = 0;
-    std::vector<uint32_t> seen;
+    std::vector<uint32_t> srcs, dsts;
     for (uint32_t i = 0; i < n; i++) {
         uint32_t s = triples[3 * i], d = triples[3 * i + 1], t = triples[3 * i + 2];
         if (s >= pages || d >= pages)
@@ -918,14 +952,19 @@ int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* st
             return fail(THB_ERR_INVALID, "page copy of " + std::to_string(t) + " tokens exceeds page_len " +
                                              std::to_string(pool->page_len));
         max_tok = std::max(max_tok, t);
-        seen.push_back(s);
-        seen.push_back(d);
+        srcs.push_back(s);
+        dsts.push_back(d);
     }
-    std::vector<uint32_t> sorted = seen;
-    std::sort(sorted.begin(), sorted.end());
-    for (size_t i = 1; i < sorted.size(); i++)
-        if (sorted[i] == sorted[i - 1])
-            return fail(THB_ERR_INVALID, "page " + std::to_string(sorted[i]) + " appears twice in one block copy");
+    // The copies run in parallel: a destination written twice, or a page
+    // both read and written, would race.  One source may feed many copies.
+    std::sort(srcs.begin(), srcs.end());
+    std::sort(dsts.begin(), dsts.end());
+    for (size_t i = 1; i < dsts.size(); i++)
+        if (dsts[i] == dsts[i - 1])
+            return fail(THB_ERR_INVALID, "page " + std::to_string(dsts[i]) + " is the destination of two copies");
+    for (uint32_t d : dsts)
+        if (std::binary_search(srcs.begin(), srcs.end(), d))
+            return fail(THB_ERR_INVALID, "page " + std::to_string(d) + " is both a source and a destination");
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
@@ -941,7 +980,7 @@ int thb_rope_rows(void* x, uint32_t dtype, uint32_t m, uint32_t heads, uint32_t 
     if (!x || !aligned16(x)) return fail(THB_ERR_INVALID, "x must be a 16-byte aligned device buffer");
     if (dtype != THB_DT_F32 && dtype != THB_DT_F16)
         return fail(THB_ERR_INVALID, "rope rows take f32 or f16 (dtype " + std::to_string(dtype) + ")");
-    if (int rc = thb_check_head_dim(head_dim)) return rc;
+    if (int rc = thb_backend_head_dim(head_dim)) return rc;
     if (int rc = check_rope(rope, head_dim, rows, row_off, m)) return rc;
     if (!aligned16(norm_w)) return fail(THB_ERR_INVALID, "norm weight must be 16-byte aligned");
     const uint64_t waves = static_cast<uint64_t>(m) * heads;

@@ -86,58 +86,6 @@ void* DevBuf::reserve(size_t bytes, bool zero) {
     return ptr_;
 }
 
-// Splits the pending copies into batches in which no page is both read and
-// written, uploads each batch and launches the copy kernel for it.
-static void run_copies(thb_pool* p, hipStream_t stream) {
-    auto& copies = p->arena.a.copies();
-    size_t i = 0;
-    std::vector<uint32_t> batch;
-    std::vector<uint32_t> touched;
-    while (i < copies.size()) {
-        batch.clear();
-        touched.clear();
-        uint32_t max_tok = 0;
-        for (; i < copies.size(); i++) {
-            const PageCopy& c = copies[i];
-            bool clash = std::find(touched.begin(), touched.end(), c.src) != touched.end() ||
-                         std::find(touched.begin(), touched.end(), c.dst) != touched.end();
-            if (clash) break;
-            batch.insert(batch.end(), {c.src, c.dst, c.tokens});
-            touched.push_back(c.src);
-            touched.push_back(c.dst);
-            max_tok = std::max(max_tok, c.tokens);
-        }
-        uint32_t n = static_cast<uint32_t>(batch.size() / 3);
-        launch_block_copy(p, batch.data(), n, max_tok, stream);
-    }
-    copies.clear();
-}
-
-void pool_flush(thb_pool* p, hipStream_t stream) {
-    Arena& a = p->arena.a;
-    if (!a.copies().empty()) run_copies(p, stream);
-    if (!a.any_dirty()) return;
-    const auto& dirty = a.dirty();
-    uint32_t lo = 0, hi = 0;
-    bool first = true;
-    for (uint32_t s = 0; s < a.seqs(); s++)
-        if (dirty[s]) {
-            if (first) lo = s;
-            hi = s + 1;
-            first = false;
-        }
-    const uint32_t mp = a.max_pages();
-    for (uint32_t s = lo; s < hi; s++) {
-        uint32_t* row = p->table_host.data() + static_cast<size_t>(s) * mp;
-        const auto& t = a.table_of(s);
-        std::fill(row, row + mp, THB_NO_PAGE);
-        std::copy(t.begin(), t.end(), row);
-    }
-    p->stager.upload(p->table_dev + static_cast<size_t>(lo) * mp, p->table_host.data() + static_cast<size_t>(lo) * mp,
-                     static_cast<size_t>(hi - lo) * mp * 4, stream);
-    a.clear_dirty();
-}
-
 }  // namespace thb
 
 using namespace thb;
@@ -149,11 +97,18 @@ const char* thb_last_error(void) { return g_error.c_str(); }
 uint32_t thb_abi_version(void) { return THB_ABI_VERSION; }
 
 int thb_check_head_dim(uint32_t head_dim) {
-    // ops/attn.rs:83-90
+    // ops/attn.rs:83-90, exactly: any head_dim in [64, 512].
     if (head_dim < 64 || head_dim > 512)
         return fail(THB_ERR_CONFIG, "head_dim " + std::to_string(head_dim) + " outside [64, 512]");
+    return THB_OK;
+}
+
+int thb_backend_head_dim(uint32_t head_dim) {
+    if (int rc = thb_check_head_dim(head_dim)) return rc;
     if (head_dim % 8 != 0)
-        return fail(THB_ERR_CONFIG, "head_dim " + std::to_string(head_dim) + " is not a multiple of 8");
+        return fail(THB_ERR_CONFIG, "head_dim " + std::to_string(head_dim) +
+                                        " is not supported by the HIP backend: it must be a multiple of 8 "
+                                        "(16-byte vector lanes)");
     return THB_OK;
 }
 
@@ -269,6 +224,28 @@ int thb_arena_take_copies(thb_arena* arena, uint32_t* triples, size_t cap, uint3
     return THB_OK;
 }
 
+int thb_arena_free_list(const thb_arena* arena, uint32_t* free_list, size_t cap, uint32_t* n) {
+    if (!arena || !n) return fail(THB_ERR_INVALID, "null argument");
+    const auto& f = arena->a.free_list();
+    *n = static_cast<uint32_t>(f.size());
+    if (free_list) {
+        if (cap < f.size())
+            return fail(THB_ERR_INVALID, "free list holds " + std::to_string(cap) + " < " + std::to_string(f.size()) +
+                                             " pages");
+        std::copy(f.begin(), f.end(), free_list);
+    }
+    return THB_OK;
+}
+
+int thb_arena_refs(const thb_arena* arena, uint32_t* refs, size_t cap) {
+    if (!arena || !refs) return fail(THB_ERR_INVALID, "null argument");
+    const auto& r = arena->a.refs();
+    if (cap < r.size())
+        return fail(THB_ERR_INVALID, "refs holds " + std::to_string(cap) + " < " + std::to_string(r.size()) + " pages");
+    std::copy(r.begin(), r.end(), refs);
+    return THB_OK;
+}
+
 // ----------------------------------------------------------------- pool
 int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
     if (!d || !out) return fail(THB_ERR_INVALID, "null argument");
@@ -285,7 +262,7 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
                                         " must be a multiple of 16 and of page_len, at most 1024 pages");
     for (uint32_t l = 0; l < d->layers; l++) {
         uint32_t hd = d->head_dims ? d->head_dims[l] : d->head_dim;
-        if (int rc = thb_check_head_dim(hd)) return rc;
+        if (int rc = thb_backend_head_dim(hd)) return rc;
     }
     return guarded([&]() -> int {
         auto p = std::make_unique<thb_pool>();
@@ -332,12 +309,11 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
         const size_t tbl = static_cast<size_t>(p->arena.a.seqs()) * p->arena.a.max_pages();
         THB_HIP(hipMalloc(reinterpret_cast<void**>(&p->table_dev), tbl * 4));
         THB_HIP(hipMemset(p->table_dev, 0xFF, tbl * 4));
-        p->table_host.assign(tbl, THB_NO_PAGE);
+        init_page_state(p.get());
         std::vector<DevLayer> dl;
         for (const auto& g : p->geom) dl.push_back({g.k_off, g.v_off, g.head_dim, 0});
         void* gd = p->geom_buf.reserve(dl.size() * sizeof(DevLayer), false);
         THB_HIP(hipMemcpy(gd, dl.data(), dl.size() * sizeof(DevLayer), hipMemcpyHostToDevice));
-        p->arena.a.clear_dirty();
         THB_HIP(hipDeviceSynchronize());
         *out = p.release();
         return THB_OK;
@@ -349,27 +325,46 @@ void thb_pool_destroy(thb_pool* pool) {
     (void)hipDeviceSynchronize();
     if (pool->owns_mem && pool->mem) (void)hipFree(pool->mem);
     if (pool->table_dev) (void)hipFree(pool->table_dev);
+    if (pool->state_dev) (void)hipFree(pool->state_dev);
     delete pool;
 }
 
+// Each page-API call runs on the host mirror (which reports errors as the
+// reference does) and, when it changed the allocator, is queued for the
+// device allocator; pool_flush replays the queue before the next kernel.
 int thb_pool_alloc(thb_pool* pool, uint32_t seq, uint32_t pos, uint32_t tokens) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
-    return thb_arena_alloc(&pool->arena, seq, pos, tokens);
+    const uint64_t v = pool->arena.a.version();
+    const size_t c = pool->arena.a.copies().size();
+    if (int rc = thb_arena_alloc(&pool->arena, seq, pos, tokens)) return rc;
+    if (pool->arena.a.version() != v) queue_page_op(pool, kPageOpAlloc, seq, pos, tokens, c);
+    return THB_OK;
 }
 
 int thb_pool_free_seq(thb_pool* pool, uint32_t seq) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
-    return thb_arena_free_seq(&pool->arena, seq);
+    const uint64_t v = pool->arena.a.version();
+    const size_t c = pool->arena.a.copies().size();
+    if (int rc = thb_arena_free_seq(&pool->arena, seq)) return rc;
+    if (pool->arena.a.version() != v) queue_page_op(pool, kPageOpFree, seq, 0, 0, c);
+    return THB_OK;
 }
 
 int thb_pool_truncate(thb_pool* pool, uint32_t seq, uint32_t keep_tokens) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
-    return thb_arena_truncate(&pool->arena, seq, keep_tokens);
+    const uint64_t v = pool->arena.a.version();
+    const size_t c = pool->arena.a.copies().size();
+    if (int rc = thb_arena_truncate(&pool->arena, seq, keep_tokens)) return rc;
+    if (pool->arena.a.version() != v) queue_page_op(pool, kPageOpTruncate, seq, keep_tokens, 0, c);
+    return THB_OK;
 }
 
 int thb_pool_fork(thb_pool* pool, uint32_t src, uint32_t dst, uint32_t tokens) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
-    return thb_arena_fork(&pool->arena, src, dst, tokens);
+    const size_t c = pool->arena.a.copies().size();
+    if (int rc = thb_arena_fork(&pool->arena, src, dst, tokens)) return rc;
+    queue_page_op(pool, kPageOpFork, src, dst, tokens, c);
+    return THB_OK;
 }
 
 int thb_pool_sync(thb_pool* pool, void* stream) {

@@ -41,8 +41,26 @@ struct AttnPlan {
     bool split = false;  // some group spans several partitions: merge kernel runs
     uint32_t n_merge = 0, merge_off = 0;  // groups of several partitions: count, blob offset (words)
     bool fusable = false;  // an append of the call's rows can run inside the launch
-    DevBuf dev;  // [groups | items | row ranges]
+    std::vector<uint32_t> blob;  // [groups | items | row ranges | prefill items | order | merge list]
+    DevBuf dev;                  // blob on the device, when uploaded
+    bool uploaded = false;
     uint64_t last_use = 0;
+};
+
+// Page-API calls the device allocator replays (pages.hip).
+enum : uint32_t { kPageOpAlloc = 1, kPageOpFree = 2, kPageOpTruncate = 3, kPageOpFork = 4, kPageOpAllocRows = 5 };
+
+// A page-API call queued for the device allocator (pages.hip): it has run on
+// the host mirror and runs on the device before the pool's next kernel.
+struct PageOp {
+    uint32_t kind, a, b, c;
+    uint32_t copy_begin, copy_end;  // its copy-on-write copies in the mirror's list
+};
+
+// Word offsets of the device page state (one allocation).
+struct PageStateLayout {
+    uint32_t free_off, refs_off, npages_off, lens_off, copies_off;
+    size_t words;
 };
 
 }  // namespace thb
@@ -68,7 +86,12 @@ struct thb_pool {
     uint64_t mem_bytes = 0;
     bool owns_mem = false;
     uint32_t* table_dev = nullptr;   // [seqs * max_pages]
-    std::vector<uint32_t> table_host;
+    // Device page allocator: header, free stack, reference counts, page
+    // counts, sequence budgets and the copy-on-write list (pages.hip).  The
+    // host arena above mirrors it: every page-API call runs on both.
+    uint32_t* state_dev = nullptr;
+    thb::PageStateLayout state;
+    std::vector<thb::PageOp> page_ops;  // queued for the device
     thb::Stager stager;
     thb::DevBuf copy_buf;            // copy triples
     thb::DevBuf geom_buf;            // per-layer DevLayer records
@@ -86,8 +109,16 @@ struct thb_pool {
 };
 
 namespace thb {
-// Uploads dirty block-table rows and executes pending page copies.
+// Runs the queued page-API calls on the device allocator (and their page
+// copies) before the next kernel on `stream`.  Allocates nothing.
 void pool_flush(thb_pool* p, hipStream_t stream);
+// Queues a page-API call that has run on the host mirror (pages.hip).
+void queue_page_op(thb_pool* p, uint32_t kind, uint32_t a, uint32_t b, uint32_t c, size_t copies_before);
+// Allocates and initialises the device page state of a new pool.
+void init_page_state(thb_pool* p);
+// Launches the block-copy kernel over n triples already on the device.
+void launch_block_copy_dev(thb_pool* p, const uint32_t* triples_dev, uint32_t n, uint32_t max_tokens,
+                           hipStream_t stream);
 // Validates a thb_rope for rows [row_off, row_off + m) of head_dim vectors.
 int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint32_t row_off, uint32_t m);
 // Launches the block-copy kernel for n non-chaining host triples (passed in

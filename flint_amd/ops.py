@@ -15,7 +15,7 @@ from typing import Optional, Sequence
 
 from . import _lib
 from ._lib import ThubanError, check, lib
-from .pool import KvPool, RowMeta, _ptr, _stream_ptr
+from .pool import KvPool, RowMeta, _stream_ptr
 
 _DTYPES = {"f32": _lib.DT_F32, "f16": _lib.DT_F16, "bf16": _lib.DT_BF16}
 
@@ -35,6 +35,51 @@ def _dtype_code(x, default="f32") -> int:
     code = {"float32": _lib.DT_F32, "float16": _lib.DT_F16, "bfloat16": _lib.DT_BF16}[name]
     _DTYPE_OF[x] = code
     return code
+
+
+_HALF = ("float16", "bfloat16", "int16")  # 16-bit words (KV types) in gather/scatter buffers
+_ACT = ("float32", "float16", "bfloat16")   # sources, queries, outputs and gates
+
+
+def _dtype_name(t) -> str:
+    return str(t.dtype).replace("torch.", "")
+
+
+def _buf(name: str, x, elems: int, dtypes, extent: Optional[int] = None):
+    """Checks argument ``x`` and returns it.  A torch tensor must have one of
+    ``dtypes``, be contiguous and hold ``elems`` elements; with ``extent``
+    (a strided view such as a query read q_stride elements apart) it may be
+    non-contiguous, but its storage must hold ``extent`` elements from its
+    first one.  A raw int address passes unchecked, as at the C ABI.
+    Raises ThubanError (kind "Invalid") instead of letting a kernel read or
+    write out of bounds.  _addr then checks the device."""
+    if isinstance(x, int):
+        return x
+    if x is None:
+        raise ThubanError(_lib.THB_ERR_INVALID, f"{name} is None")
+    dt = _dtype_name(x)
+    if dt not in dtypes:
+        raise ThubanError(_lib.THB_ERR_INVALID, f"{name}: dtype {dt} is not one of {', '.join(dtypes)}")
+    if extent is None:
+        if not x.is_contiguous():
+            raise ThubanError(_lib.THB_ERR_INVALID, f"{name} must be contiguous")
+        if x.numel() < elems:
+            raise ThubanError(_lib.THB_ERR_INVALID, f"{name} holds {x.numel()} elements, the call needs {elems}")
+    else:
+        have = x.untyped_storage().nbytes() // x.element_size() - x.storage_offset()
+        if have < extent:
+            raise ThubanError(_lib.THB_ERR_INVALID,
+                              f"{name}: storage holds {have} elements from the view's start, the call reads {extent}")
+    return x
+
+
+def _addr(name: str, x) -> int:
+    """Device address of a checked argument; a tensor must live on the GPU."""
+    if isinstance(x, int):
+        return x
+    if not x.is_cuda:
+        raise ThubanError(_lib.THB_ERR_INVALID, f"{name} must be a GPU tensor (device {x.device})")
+    return x.data_ptr()
 
 
 @dataclass
@@ -57,10 +102,27 @@ def check_head_dim(head_dim: int) -> None:
     check(lib().thb_check_head_dim(head_dim))
 
 
+def _head_dim(kv: KvPool, layer: int) -> int:
+    hds = getattr(kv, "_hd_arr", None)
+    if hds is not None and 0 <= layer < len(hds):
+        return hds[layer]
+    return kv.head_dim
+
+
+def _src_bufs(kv: KvPool, layer: int, m: int, k_src, v_src):
+    n = m * kv.kv_heads * _head_dim(kv, layer)
+    _buf("k_src", k_src, n, _ACT)
+    _buf("v_src", v_src, n, _ACT)
+    if not isinstance(k_src, int) and not isinstance(v_src, int) and k_src.dtype != v_src.dtype:
+        raise ThubanError(_lib.THB_ERR_INVALID, f"k_src and v_src dtypes differ ({k_src.dtype}, {v_src.dtype})")
+
+
 def kv_store(k_src, v_src, kv: KvPool, layer: int, m: int, meta: RowMeta, row_off: int = 0, stream=None) -> None:
     """ops/attn.rs:53-81: append rows [row_off, row_off+m) of K/V (shape
     [m, kv_heads, head_dim], f32/f16/bf16) into the paged cache."""
-    check(lib().thb_kv_store(kv.handle, layer, _ptr(k_src), _ptr(v_src), _dtype_code(getattr(k_src, "dtype", None)),
+    _src_bufs(kv, layer, m, k_src, v_src)
+    k, v = _addr("k_src", k_src), _addr("v_src", v_src)
+    check(lib().thb_kv_store(kv.handle, layer, k, v, _dtype_code(getattr(k_src, "dtype", None)),
                              meta.handle, row_off, m, _stream_ptr(stream)))
 
 
@@ -75,21 +137,31 @@ def _spec_c(spec: AttnSpec, q, y) -> _lib.AttnSpecC:
     return c
 
 
+def _qy_bufs(kv: KvPool, layer: int, spec: AttnSpec, q, y):
+    n = spec.m * spec.q_heads * _head_dim(kv, layer)
+    _buf("q", q, n, _ACT)
+    _buf("y", y, n, _ACT)
+
+
 def attn(q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
     """ops/attn.rs:18-51: paged attention of spec.m rows; q and y are
     [m, q_heads, head_dim] (f32 as the reference, or f16)."""
+    _qy_bufs(kv, layer, spec, q, y)
+    qp, yp = _addr("q", q), _addr("y", y)
     c = _spec_c(spec, q, y)
-    check(lib().thb_attn(kv.handle, layer, _ptr(q), _ptr(y), ctypes.byref(c), spec.args.handle, _stream_ptr(stream)))
+    check(lib().thb_attn(kv.handle, layer, qp, yp, ctypes.byref(c), spec.args.handle, _stream_ptr(stream)))
 
 
 def kv_store_attn(k_src, v_src, q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
     """kv_store of the spec's rows followed by attn (the per-layer step of
     transformer/forward.rs:300-336), in one launch where the rows allow it;
     bit-identical to calling the two."""
+    _src_bufs(kv, layer, spec.m, k_src, v_src)
+    _qy_bufs(kv, layer, spec, q, y)
+    k, v, qp, yp = _addr("k_src", k_src), _addr("v_src", v_src), _addr("q", q), _addr("y", y)
     c = _spec_c(spec, q, y)
-    check(lib().thb_attn_append(kv.handle, layer, _ptr(k_src), _ptr(v_src),
-                                _dtype_code(getattr(k_src, "dtype", None)), _ptr(q), _ptr(y), ctypes.byref(c),
-                                spec.args.handle, _stream_ptr(stream)))
+    check(lib().thb_attn_append(kv.handle, layer, k, v, _dtype_code(getattr(k_src, "dtype", None)), qp, yp,
+                                ctypes.byref(c), spec.args.handle, _stream_ptr(stream)))
 
 
 def attn_step(kv: KvPool, layer: int, spec: AttnSpec, q, y, q_stride: int = 0, gate=None, gate_stride: int = 0,
@@ -100,15 +172,25 @@ def attn_step(kv: KvPool, layer: int, spec: AttnSpec, q, y, q_stride: int = 0, g
     multiplies the output by sigmoid(gate) (qwen35/layers.rs:231-238); k_src
     and v_src are appended first; rope (flint_amd.rope.Rope) rotates q and k.
     q, gate and y are device tensors or raw device addresses."""
-    c = _spec_c(spec, q, y)
+    hd = _head_dim(kv, layer)
+    heads = spec.m * spec.q_heads
     io = _lib.AttnIoC()
-    io.q_dev, io.y_dev, io.q_stride = _ptr(q), _ptr(y), q_stride
-    io.gate_dev = _ptr(gate) if gate is not None else None
+    q_ext = (heads - 1) * q_stride + hd if q_stride and heads else None
+    _buf("q", q, heads * hd, _ACT, extent=q_ext)
+    _buf("y", y, heads * hd, _ACT)
+    if gate is not None:
+        g_ext = (heads - 1) * (gate_stride or hd) + hd if heads else 0
+        _buf("gate", gate, heads * hd, _ACT, extent=g_ext if gate_stride else None)
+    if k_src is not None:
+        _src_bufs(kv, layer, spec.m, k_src, v_src)
+    io.q_dev, io.y_dev, io.q_stride = _addr("q", q), _addr("y", y), q_stride
+    io.gate_dev = _addr("gate", gate) if gate is not None else None
     io.gate_stride = gate_stride
     if k_src is not None:
-        io.k_src_dev, io.v_src_dev = _ptr(k_src), _ptr(v_src)
+        io.k_src_dev, io.v_src_dev = _addr("k_src", k_src), _addr("v_src", v_src)
         io.src_dtype = _dtype_code(getattr(k_src, "dtype", None))
     io.rope = ctypes.pointer(rope._c) if rope is not None else None
+    c = _spec_c(spec, q, y)
     check(lib().thb_attn_step(kv.handle, layer, ctypes.byref(io), ctypes.byref(c), spec.args.handle,
                               _stream_ptr(stream)))
 
@@ -119,11 +201,22 @@ def default_scale(head_dim: int) -> float:
 
 
 def kv_gather(kv: KvPool, layer: int, seq: int, t0: int, n: int, k_dst, v_dst, stream=None) -> None:
-    check(lib().thb_kv_gather(kv.handle, layer, seq, t0, n, _ptr(k_dst), _ptr(v_dst), _stream_ptr(stream)))
+    """Tokens [t0, t0+n) of seq into contiguous [kv_heads, n, head_dim]
+    16-bit buffers (no reference counterpart)."""
+    e = n * kv.kv_heads * _head_dim(kv, layer)
+    _buf("k_dst", k_dst, e, _HALF)
+    _buf("v_dst", v_dst, e, _HALF)
+    check(lib().thb_kv_gather(kv.handle, layer, seq, t0, n, _addr("k_dst", k_dst), _addr("v_dst", v_dst),
+                              _stream_ptr(stream)))
 
 
 def kv_scatter(kv: KvPool, layer: int, seq: int, t0: int, n: int, k_src, v_src, stream=None) -> None:
-    check(lib().thb_kv_scatter(kv.handle, layer, seq, t0, n, _ptr(k_src), _ptr(v_src), _stream_ptr(stream)))
+    """Inverse of kv_gather (no reference counterpart)."""
+    e = n * kv.kv_heads * _head_dim(kv, layer)
+    _buf("k_src", k_src, e, _HALF)
+    _buf("v_src", v_src, e, _HALF)
+    check(lib().thb_kv_scatter(kv.handle, layer, seq, t0, n, _addr("k_src", k_src), _addr("v_src", v_src),
+                               _stream_ptr(stream)))
 
 
 def block_copy(kv: KvPool, triples: Sequence[Sequence[int]], stream=None) -> None:

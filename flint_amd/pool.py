@@ -145,6 +145,21 @@ class KvArena:
         check(lib().thb_arena_table_of(self._h, seq, out, n.value, ctypes.byref(n)))
         return list(out[: n.value])
 
+    def free_list(self) -> List[int]:
+        """The free stack, bottom first: the last entry is the next page
+        handed out (KvArena::free, pool.rs:16)."""
+        n = ctypes.c_uint32()
+        check(lib().thb_arena_free_list(self._h, None, 0, ctypes.byref(n)))
+        out = (ctypes.c_uint32 * max(n.value, 1))()
+        check(lib().thb_arena_free_list(self._h, out, n.value, ctypes.byref(n)))
+        return list(out[: n.value])
+
+    def refs(self) -> List[int]:
+        pages = self.pages()
+        out = (ctypes.c_uint32 * max(pages, 1))()
+        check(lib().thb_arena_refs(self._h, out, pages))
+        return list(out[:pages])
+
     def take_copies(self) -> List[tuple]:
         pending = self.info().pending_copies
         out = (ctypes.c_uint32 * max(3 * pending, 1))()
@@ -212,6 +227,34 @@ class KvPool:
 
     def sync(self, stream=None) -> None:
         check(lib().thb_pool_sync(self._h, _stream_ptr(stream)))
+
+    # device page allocator ------------------------------------------------
+    def alloc_rows(self, rows: "RowMeta", m: int, row_off: int = 0, stream=None) -> None:
+        """The engine's per-plan alloc_pages loop (engine.rs:197-200) for
+        rows [row_off, row_off + m) of the row meta, on the device."""
+        check(lib().thb_pool_alloc_rows(self._h, rows.handle, row_off, m, _stream_ptr(stream)))
+
+    def status(self, stream=None) -> None:
+        """Raises the first failure the device allocator met since the last
+        call (ThubanError with the reference's message), and clears it."""
+        check(lib().thb_pool_status(self._h, _stream_ptr(stream)))
+
+    def read_state(self, stream=None):
+        """(free stack bottom first, reference counts, flattened block
+        table) of the device allocator after the stream's work."""
+        info = self.arena.info()
+        n_tab = info.seqs * info.max_pages
+        free = (ctypes.c_uint32 * max(info.pages, 1))()
+        refs = (ctypes.c_uint32 * max(info.pages, 1))()
+        table = (ctypes.c_uint32 * max(n_tab, 1))()
+        n_free = ctypes.c_uint32()
+        check(lib().thb_pool_read_state(self._h, _stream_ptr(stream), free, info.pages, ctypes.byref(n_free), refs,
+                                        info.pages, table, n_tab))
+        return list(free[: n_free.value]), list(refs[: info.pages]), list(table[:n_tab])
+
+    def pull(self, stream=None) -> None:
+        """Reloads the host mirror from the device allocator."""
+        check(lib().thb_pool_pull(self._h, _stream_ptr(stream)))
 
     # device views ---------------------------------------------------------
     def layer_info(self, layer: int) -> _lib.LayerInfo:

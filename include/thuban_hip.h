@@ -54,12 +54,15 @@ extern "C" {
 const char* thb_last_error(void);
 /* ABI revision of this header. */
 uint32_t thb_abi_version(void);
-#define THB_ABI_VERSION 5u
+#define THB_ABI_VERSION 6u
 
-/* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90):
- * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]".  This backend also needs
- * head_dim % 8 == 0 (16-byte vector lanes). */
+/* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90) exactly:
+ * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]". */
 int thb_check_head_dim(uint32_t head_dim);
+/* No reference counterpart: what this backend accepts, thb_check_head_dim
+ * plus head_dim % 8 == 0 (16-byte vector lanes); THB_ERR_CONFIG otherwise.
+ * thb_pool_create and thb_rope_rows apply it. */
+int thb_backend_head_dim(uint32_t head_dim);
 
 /* ------------------------------------------------ host page allocator */
 
@@ -107,6 +110,10 @@ int thb_arena_info_get(const thb_arena* arena, thb_arena_info* info);
 /* Moves the pending copy-on-write copies (src_page, dst_page, tokens) out of
  * the arena; a device pool executes them itself before its next kernel. */
 int thb_arena_take_copies(thb_arena* arena, uint32_t* triples, size_t cap, uint32_t* n);
+/* The free stack, bottom first (free_list[n - 1] is the next page handed
+ * out; KvArena::free, pool.rs:16), and the reference counts [pages]. */
+int thb_arena_free_list(const thb_arena* arena, uint32_t* free_list, size_t cap, uint32_t* n);
+int thb_arena_refs(const thb_arena* arena, uint32_t* refs, size_t cap);
 
 /* ---------------------------------------------------------- device pool */
 
@@ -155,20 +162,54 @@ typedef struct thb_layer_info {
 } thb_layer_info;
 
 /* KvArena::new + KvPool::new for every layer (pool.rs:20-45,131-153).  The
- * memory is zero-filled, as Backend::zero_tensor does (lib.rs:192-206). */
+ * memory is zero-filled, as Backend::zero_tensor does (lib.rs:192-206).
+ *
+ * The page allocator lives on the device: the free stack, per-page reference
+ * counts and per-sequence page counts sit in HBM next to the block table,
+ * and kernels change them with KvArena's semantics (pops yield pages 0, 1,
+ * 2, ...; freed pages return in table order).  The pool's host arena
+ * (thb_pool_arena) is a mirror that runs every page-API call first, so that
+ * errors return synchronously with the reference's messages and attention
+ * can plan its launch without reading the GPU. */
 int thb_pool_create(const thb_pool_desc* desc, thb_pool** out);
 void thb_pool_destroy(thb_pool* pool);
 /* Page API of LanguageModel::{alloc,free,truncate}_pages (traits.rs:39-41,
- * transformer/forward.rs:534-550).  Host-side; the device block table and
- * any copy-on-write copies are pushed on the next device call (or by
- * thb_pool_sync), replacing upload_tables (model.rs:413-418). */
+ * transformer/forward.rs:534-550).  Runs on the host mirror now and on the
+ * device allocator (with any copy-on-write copies) before the pool's next
+ * kernel, or at thb_pool_sync; no block table is uploaded (the reference
+ * re-uploads the whole table to every layer, model.rs:413-418). */
 int thb_pool_alloc(thb_pool* pool, uint32_t seq, uint32_t pos, uint32_t tokens);
 int thb_pool_free_seq(thb_pool* pool, uint32_t seq);
 int thb_pool_truncate(thb_pool* pool, uint32_t seq, uint32_t keep_tokens);
 /* No reference counterpart: fork with block sharing + partial-page copy. */
 int thb_pool_fork(thb_pool* pool, uint32_t src, uint32_t dst, uint32_t tokens);
-/* Uploads dirty block-table rows and runs pending page copies on stream. */
+/* Runs the queued page-API calls on the device allocator, on stream. */
 int thb_pool_sync(thb_pool* pool, void* stream);
+
+typedef struct thb_rows thb_rows;
+/* The engine's per-plan allocation (thuban_generate/src/engine.rs:197-200:
+ * alloc_pages(seq, tokens) -> KvArena::alloc(seq, pos, tokens), pool.rs
+ * :47-65) for the rows [row_off, row_off + m) of the row meta, run by the
+ * device allocator on stream: each maximal run of rows of one sequence is
+ * KvArena::alloc(seq, position of its first row, rows in the run), in row
+ * order, with copy-on-write of shared pages the write touches.  Each
+ * sequence may head one run only (THB_ERR_INVALID).  A failing run (context
+ * limit, arena exhausted) ends the call with the reference's message; the
+ * runs before it keep their pages, as the engine's loop does. */
+int thb_pool_alloc_rows(thb_pool* pool, const thb_rows* rows, uint32_t row_off, uint32_t m, void* stream);
+/* First failure the device allocator met since the last call (THB_OK if
+ * none), with the reference's message; clears it.  Synchronises stream. */
+int thb_pool_status(thb_pool* pool, void* stream);
+/* Copies the device allocator's state to host memory after stream's work:
+ * the free stack (bottom first, so free_list[n_free - 1] is the next page
+ * handed out), the reference counts [pages] and the flattened block table
+ * [seqs * max_pages] (KvArena::table layout, pool.rs:85-93).  Any pointer
+ * may be NULL. */
+int thb_pool_read_state(thb_pool* pool, void* stream, uint32_t* free_list, size_t free_cap, uint32_t* n_free,
+                        uint32_t* refs, size_t refs_cap, uint32_t* table, size_t table_n);
+/* Reloads the host mirror from the device allocator (after changes the host
+ * did not see, such as replays of a captured thb_pool_alloc_rows). */
+int thb_pool_pull(thb_pool* pool, void* stream);
 /* The pool's allocator (queries; mutate through thb_pool_* instead). */
 const thb_arena* thb_pool_arena(const thb_pool* pool);
 /* Device pointers of layer `layer`'s K and V planes (KvPool::k / ::v, in the
@@ -184,7 +225,6 @@ int thb_pool_memory(const thb_pool* pool, void** base_dev, uint64_t* bytes);
 /* Row metadata, rows::row_meta / write_row_meta (rows.rs:11-30): 8 u32 per
  * row, [pos, seq, 0 x 6].  The object keeps a host mirror of what it last
  * wrote so that attention can plan its launch without reading the GPU. */
-typedef struct thb_rows thb_rows;
 int thb_rows_create(uint32_t max_m, thb_rows** out);
 void thb_rows_destroy(thb_rows* rows);
 /* rows::write_row_meta: uploads rows [0, m) on stream. */

@@ -70,6 +70,24 @@ class KvArena:
             self.refs[p] = 1
             table.append(p)
 
+    def alloc_rows(self, positions, seqs):
+        """The engine's per-plan allocation driven from row meta: Engine::step
+        calls alloc_pages(seq, tokens) once per plan (thuban_generate/src/
+        engine.rs:197-200), which is alloc(seq, pos, tokens) at the
+        sequence's position (transformer/forward.rs:534-538).  Here a plan is
+        a maximal run of rows of one sequence (its first row's position, its
+        row count), in row order; the first failure propagates and the runs
+        before it keep their pages, as the engine's `?` leaves them."""
+        runs, r, m = [], 0, len(seqs)
+        while r < m:
+            e = r + 1
+            while e < m and seqs[e] == seqs[r]:
+                e += 1
+            runs.append((seqs[r], positions[r], e - r))
+            r = e
+        for seq, pos, n in runs:
+            self.alloc(seq, pos, n)
+
     def free_seq(self, seq):
         """pool.rs:67-71 (pages return in table order once unreferenced)."""
         for p in self.tables[seq]:

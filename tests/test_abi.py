@@ -36,7 +36,7 @@ def test_abi_version_and_struct_layouts(tmp_path):
 
     from flint_amd import _lib
 
-    assert _lib.lib().thb_abi_version() == _lib.ABI_VERSION == 5
+    assert _lib.lib().thb_abi_version() == _lib.ABI_VERSION == 6
     structs = {"thb_pool_desc": _lib.PoolDesc, "thb_attn_spec": _lib.AttnSpecC,
                "thb_layer_info": _lib.LayerInfo, "thb_arena_info": _lib.ArenaInfo, "thb_rope": _lib.RopeC,
                "thb_attn_io": _lib.AttnIoC}
@@ -59,15 +59,23 @@ def test_abi_version_and_struct_layouts(tmp_path):
 
 
 def test_check_head_dim():
-    from flint_amd import ThubanError, check_head_dim
+    """ops::check_head_dim (ops/attn.rs:83-90) exactly: any value in
+    [64, 512]; the backend's own limit (multiples of 8) is a separate check."""
+    from flint_amd import ThubanError, _lib, check_head_dim
 
-    for hd in (64, 80, 128, 256, 512):
+    for hd in (64, 80, 100, 127, 128, 256, 512):
         check_head_dim(hd)
-    for hd, msg in ((32, "head_dim 32 outside [64, 512]"), (513, "outside"), (100, "multiple of 8")):
+    for hd, msg in ((32, "head_dim 32 outside [64, 512]"), (63, "outside"), (513, "outside")):
         with pytest.raises(ThubanError) as e:
             check_head_dim(hd)
         assert msg in str(e.value)
         assert e.value.kind == "Config"
+    L = _lib.lib()
+    for hd in (64, 80, 128, 512):
+        assert L.thb_backend_head_dim(hd) == 0
+    for hd, msg in ((100, "multiple of 8"), (127, "multiple of 8"), (32, "outside [64, 512]")):
+        assert L.thb_backend_head_dim(hd) == _lib.THB_ERR_CONFIG
+        assert msg in L.thb_last_error().decode()
 
 
 def test_product_does_not_reference_the_oracle():

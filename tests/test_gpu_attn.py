@@ -154,6 +154,35 @@ def test_reference_mode_chunk(torch_cuda, causal):
         assert err <= TIGHT, ("reference-mode chunk", "precision regression", err)
 
 
+def test_empty_key_range_is_nan(torch_cuda):
+    """A row with no valid key: reference mode, causal, window 5, a chunk
+    whose second row (position 10) sets the 8-row block's kv_len to 11 while
+    the first row (position 100) starts its window at 96.  attn.wgsl divides
+    0 by 0 there (NaN); the other row stays finite and matches the oracle."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    lens = [128]
+    pool = make_pool(lens, kv_heads=2, head_dim=64, page_len=16, kv_dtype="f16")
+    scattered_alloc(pool, lens, random.Random(9), 16)
+    rows = RowMeta(8)
+    fill(torch, pool, rows, lens, seed=9)
+    positions, seqs = [100, 10], [0, 0]
+    q = torch.randn(2, 4, 64, device="cuda")
+    rows.write(positions, seqs, 2)
+    y = torch.empty_like(q)
+    ops.attn(q, pool, 0, y, ops.AttnSpec(q_heads=4, window=5, scale=0.125, m=2, causal=True, seq=0, args=rows))
+    torch.cuda.synchronize()
+    want = oracle_layer(torch, pool).attn(q.cpu().numpy(), oracle.row_meta(positions, seqs), 2, 4, 0.125,
+                                          window=5, causal=True, seq=0)
+    got = y.cpu().numpy()
+    say("empty key range", got[0, 0, :2], want[0, 0, :2])
+    assert np.isnan(want[0]).all() and np.isnan(got[0]).all()
+    assert np.isfinite(got[1]).all()
+    assert float(np.max(np.abs(got[1] - want[1]))) <= TIGHT
+
+
 def test_reference_anchor_through_gpu(torch_cuda, golden):
     """anchor_attn_causal_and_window (kernels.rs:1439-1481) embedded in the
     first two dims of a head_dim-64 pool: [2, 3] full, [3, 4] window 1."""
@@ -277,6 +306,9 @@ FUSE_CASES = [
     ("decode-llama3-f16", 32, 8, 128, "f16", "f16", 1, True),
     ("decode-qwen2-bf16-f32src", 14, 2, 64, "bf16", "f32", 1, True),
     ("verify4-gemma2", 16, 8, 256, "f16", "f32", 4, True),
+    # 32 query heads per KV head: each row is two query groups in two
+    # workgroups, and both store the row's token (the same bytes)
+    ("decode-mqa32-two-groups", 32, 1, 128, "f16", "f16", 1, True),
     ("prefill40-fallback", 8, 2, 128, "f16", "bf16", 40, False),
 ]
 
