@@ -163,6 +163,7 @@ SIGNATURES = [
     ("thb_attn_append_rope", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC),
                                     ctypes.POINTER(RopeC), _vp, _vp]),
     ("thb_attn_step", _int, [_vp, _u32, ctypes.POINTER(AttnIoC), ctypes.POINTER(AttnSpecC), _vp, _vp]),
+    ("thb_attn_noalloc", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_block_copy", _int, [_vp, _pu32, _u32, _vp]),

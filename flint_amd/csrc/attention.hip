@@ -41,6 +41,7 @@
 //    them in partition order; there are no device-wide fences or atomics.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <queue>
 #include <string>
 
@@ -2230,4 +2231,82 @@ extern "C" int thb_attn_append_rope(thb_pool* pool, uint32_t layer, const void* 
 extern "C" int thb_attn_step(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_attn_spec* spec,
                              const thb_rows* rows, void* stream) {
     return step_impl(pool, layer, io, spec, rows, stream);
+}
+
+// ------------------------------------------------ no-allocation entry point
+// thb_attn_noalloc keeps the launch plan and the split-K partial results of
+// one call in this fixed array instead of buffers the pool grows with
+// hipMalloc: the plan in its first THB_NOALLOC_PLAN_BYTES, the partial
+// results after it.  Each device holds its own copy for the life of the
+// process, and every call on a device shares it (the last call's contents
+// stay; nothing in it needs to start at zero: each partial slot is written
+// before it is read, and the plan is uploaded by each call).  Host code uses
+// the address hipGetSymbolAddress returns for the current device, never the
+// array's name.
+static __device__ __align__(256) uint8_t scratch[THB_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[kMaxDevices] = {};
+
+// This device's scratch address, resolved once per device with the device
+// current (the first no-allocation call on it).
+int scratch_for(int device, uint8_t** out) {
+    if (device < 0 || device >= kMaxDevices)
+        return fail(THB_ERR_INVALID, "device " + std::to_string(device) + " beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[device]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            return fail(THB_ERR_GPU, std::string("no-allocation scratch unavailable: ") + hipGetErrorString(e));
+        }
+        g_scratch[device] = static_cast<uint8_t*>(ptr);
+    }
+    *out = g_scratch[device];
+    return THB_OK;
+}
+
+}  // namespace
+
+extern "C" int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_attn_spec* spec,
+                                const thb_rows* rows, void* stream) {
+    if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
+    if (int rc = check_attn_call(pool, layer, q, y, *spec, rows)) return rc;
+    if (spec->m == 0) return THB_OK;
+    const uint32_t hd = pool->geom[layer].head_dim;
+    return guarded([&]() -> int {
+        int device = -1;
+        THB_HIP(hipGetDevice(&device));
+        if (device != pool->device)
+            return fail(THB_ERR_INVALID, "the pool lives on device " + std::to_string(pool->device) + ", device " +
+                                             std::to_string(device) + " is current");
+        uint8_t* scr = nullptr;
+        if (int rc = scratch_for(device, &scr)) return rc;
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);  // page ops in kernel arguments, copies from the device list: no allocation
+        AttnPlan* plan = nullptr;
+        if (int rc = get_plan(pool, rows, *spec, hd, s, false, &plan)) return rc;
+        const uint64_t plan_bytes = plan->blob.size() * 4;
+        if (plan_bytes > THB_NOALLOC_PLAN_BYTES)
+            return fail(THB_ERR_INVALID, "launch plan of " + std::to_string(plan_bytes) +
+                                             " bytes exceeds the no-allocation scratch's " +
+                                             std::to_string(THB_NOALLOC_PLAN_BYTES) + " (use thb_attn)");
+        uint64_t o_bytes = 0;
+        const uint64_t pb = partial_bytes(pool, *plan, &o_bytes);
+        constexpr uint64_t kPartCap = static_cast<uint64_t>(THB_NOALLOC_SCRATCH_BYTES) - THB_NOALLOC_PLAN_BYTES;
+        if (pb > kPartCap)
+            return fail(THB_ERR_INVALID, "split-K partial results of " + std::to_string(pb) +
+                                             " bytes exceed the no-allocation scratch's " + std::to_string(kPartCap) +
+                                             " (use thb_attn, or a longer part_len)");
+        pool->fixed_stager.upload(scr, plan->blob.data(), plan_bytes, s);
+        const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
+        const uint32_t* meta = rows->dev + 8 * static_cast<size_t>(spec->row_off);
+        launch_plan(pool, layer, io, *spec, *plan, false, meta, reinterpret_cast<const uint32_t*>(scr),
+                    scr + THB_NOALLOC_PLAN_BYTES, s);
+        return THB_OK;
+    });
 }

@@ -68,6 +68,29 @@ private:
     int next_ = 0;
 };
 
+// Pinned host staging of a fixed size, allocated once (init) and never
+// grown: two slots, each reused after the event behind its last copy.
+// upload() allocates nothing.
+class FixedStager {
+public:
+    FixedStager() = default;
+    FixedStager(const FixedStager&) = delete;
+    FixedStager& operator=(const FixedStager&) = delete;
+    ~FixedStager();
+    void init(size_t bytes);
+    size_t capacity() const { return cap_; }
+    // Copies `bytes` (at most capacity()) from host `src` to device `dst`.
+    void upload(void* dst, const void* src, size_t bytes, hipStream_t stream);
+
+private:
+    static constexpr int kSlots = 2;
+    void* host_[kSlots] = {nullptr, nullptr};
+    hipEvent_t done_[kSlots] = {nullptr, nullptr};
+    bool pending_[kSlots] = {false, false};
+    size_t cap_ = 0;
+    int next_ = 0;
+};
+
 // Device buffer that grows on demand (hipMalloc outside the hot path: only
 // when a larger size than ever before is requested).
 class DevBuf {

@@ -62,6 +62,39 @@ void Stager::upload(void* dst, const void* src, size_t bytes, hipStream_t stream
     s.pending = true;
 }
 
+FixedStager::~FixedStager() {
+    for (int i = 0; i < kSlots; i++) {
+        if (done_[i]) {
+            (void)hipEventSynchronize(done_[i]);
+            (void)hipEventDestroy(done_[i]);
+        }
+        if (host_[i]) (void)hipHostFree(host_[i]);
+    }
+}
+
+void FixedStager::init(size_t bytes) {
+    for (int i = 0; i < kSlots; i++) {
+        THB_HIP(hipHostMalloc(&host_[i], bytes, hipHostMallocDefault));
+        THB_HIP(hipEventCreateWithFlags(&done_[i], hipEventDisableTiming));
+    }
+    cap_ = bytes;
+}
+
+void FixedStager::upload(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return;
+    if (bytes > cap_) throw HipError{hipErrorInvalidValue, "fixed staging upload larger than its slots"};
+    const int i = next_;
+    next_ = (next_ + 1) % kSlots;
+    if (pending_[i]) {
+        THB_HIP(hipEventSynchronize(done_[i]));
+        pending_[i] = false;
+    }
+    std::memcpy(host_[i], src, bytes);
+    THB_HIP(hipMemcpyAsync(dst, host_[i], bytes, hipMemcpyHostToDevice, stream));
+    THB_HIP(hipEventRecord(done_[i], stream));
+    pending_[i] = true;
+}
+
 DevBuf::~DevBuf() {
     if (ptr_) {
         (void)hipDeviceSynchronize();
@@ -310,6 +343,7 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
         THB_HIP(hipMalloc(reinterpret_cast<void**>(&p->table_dev), tbl * 4));
         THB_HIP(hipMemset(p->table_dev, 0xFF, tbl * 4));
         init_page_state(p.get());
+        p->fixed_stager.init(THB_NOALLOC_PLAN_BYTES);
         std::vector<DevLayer> dl;
         for (const auto& g : p->geom) dl.push_back({g.k_off, g.v_off, g.head_dim, 0});
         void* gd = p->geom_buf.reserve(dl.size() * sizeof(DevLayer), false);

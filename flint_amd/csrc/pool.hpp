@@ -93,6 +93,7 @@ struct thb_pool {
     thb::PageStateLayout state;
     std::vector<thb::PageOp> page_ops;  // queued for the device
     thb::Stager stager;
+    thb::FixedStager fixed_stager;   // plan uploads of thb_attn_noalloc (never grows)
     thb::DevBuf copy_buf;            // copy triples
     thb::DevBuf geom_buf;            // per-layer DevLayer records
     thb::DevBuf partials;            // split-K partial results

@@ -359,6 +359,23 @@ typedef struct thb_attn_io {
 int thb_attn_step(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_attn_spec* spec,
                   const thb_rows* rows, void* stream);
 
+/* No reference counterpart.  thb_attn for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops or harnesses
+ * that forbid hipMalloc): the launch plan and the split-K partial results go
+ * to a fixed device array of THB_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each device until the process ends, and the plan is staged
+ * through pinned memory the pool allocated at creation, so the call runs no
+ * hipMalloc, hipFree or other allocating routine.  The first
+ * THB_NOALLOC_PLAN_BYTES hold the plan, the rest the partial results; a call
+ * needing more returns THB_ERR_INVALID.  Results are bit-identical to
+ * thb_attn.  Every call on a device shares the array: calls that overlap on
+ * one device (other streams, other threads) race.  The pool's device must be
+ * current. */
+#define THB_NOALLOC_SCRATCH_BYTES (32u << 20)
+#define THB_NOALLOC_PLAN_BYTES (256u << 10)
+int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
+                     const thb_rows* rows, void* stream);
+
 /* No reference counterpart.  Copies tokens [t0, t0 + n) of seq, layer
  * `layer`, into contiguous k_dst/v_dst [kv_heads, n, head_dim] in the KV type
  * (bit copy). */
