@@ -210,6 +210,88 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
                                     "(2 B read + 2 B write) x K,V"}}
 
 
+def time_o_proj(torch, ops, dev, B, nq, hd, layers=32, reps=5):
+    """The attention consumer at the C2 shape: o_proj (Llama-3-8B: 4096 x
+    4096 bf16 weights, one matrix per layer) on the bf16 attention output of
+    B rows, accumulated into the f32 residual (ops::gemm_acc with acc, as
+    transformer/forward.rs:338-351 calls it).  A graph of one call per layer,
+    replayed `reps` times between events; distinct weights per layer, so
+    every launch streams its 32 MiB from HBM."""
+    hidden = nq * hd
+    w = [(torch.randn(hidden, hidden, device=dev) * 0.02).to(torch.bfloat16) for _ in range(layers)]
+    x = torch.randn(B, hidden, device=dev).to(torch.bfloat16)
+    y = torch.zeros(B, hidden, device=dev)
+
+    def run():
+        for layer in range(layers):
+            ops.gemm_acc(x, w[layer], y, B, True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        run()
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / (reps * layers) * 1e3
+    nbytes = hidden * hidden * 2 + B * hidden * 2 + 2 * B * hidden * 4  # W, x, y read + write
+    del graph, w
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"us_per_call": round(us, 2), "GBps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
+            "bytes_per_call": nbytes,
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / PEAK_HBM_GBPS, 4)},
+            "note": f"thb_gemm_acc (gemm_skinny): y[{B}, {hidden}] += x[{B}, {hidden}] bf16 . W[{hidden}, {hidden}]^T "
+                    f"bf16, acc into f32, distinct W per layer, graph of {layers} calls; bytes = W + x + y read/write"}
+
+
+def time_identity_leg(torch, ops, cfg, q, k_new, v_new, steps=5):
+    """The reference's attention probe (thuban_bench/src/probes/attn.rs
+    :97-133) times one attention with an identity block table and with a
+    shuffled one.  Here: the same fused append + decode step over a second
+    pool whose sequences own consecutive pages (sequence s holds pages
+    s * ctx / P ...), events around layers 1..L-1 of `steps` steps; returns
+    us per layer."""
+    from flint_amd.pool import ArenaSpec, KvPool, RowMeta
+
+    L, B, ctx = cfg["layers"], cfg["batch"], cfg["ctx"]
+    nq, nkv, hd, pl = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"], cfg["page_len"]
+    pool = KvPool(ArenaSpec([ctx] * B, B * (-(-ctx // pl))), nkv, hd, layers=L, page_len=pl, kv_dtype="f16")
+    for s in range(B):
+        pool.alloc(s, 0, ctx)
+    g = torch.Generator(device=q.device)
+    g.manual_seed(1002)
+    for layer in range(L):
+        for t in pool.layer_tensors(layer):
+            t.view(torch.float16).normal_(generator=g)
+    rows = RowMeta(B)
+    rows.write([ctx - 1] * B, list(range(B)), B)
+    y = torch.empty_like(q[0])
+    spec = ops.AttnSpec(q_heads=nq, window=0, scale=1.0 / math.sqrt(hd), m=B, causal=True, seq=None, args=rows)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for i in range(-2, steps):
+        for layer in range(L):
+            if i >= 0 and layer == 1:
+                ev[i][0].record()
+            ops.kv_store_attn(k_new[layer], v_new[layer], q[layer], pool, layer, y, spec)
+        if i >= 0:
+            ev[i][1].record()
+    torch.cuda.synchronize()
+    us = sum(e[0].elapsed_time(e[1]) for e in ev) / steps / (L - 1) * 1e3
+    pool.close()
+    return us
+
+
 def time_rope_step(torch, ops, pool, rows, positions, seqs, q, k_new, v_new, L, B, nq, hd, scale, steps=5):
     """The per-layer step with rotary embedding (Llama-3: theta 500000,
     rot = head_dim) two ways: the reference's four launches (rope q, rope k,
@@ -251,8 +333,49 @@ def time_rope_step(torch, ops, pool, rows, positions, seqs, q, k_new, v_new, L, 
     return out
 
 
+def cpu_model():
+    """The host CPU's model name and logical core count (nproc)."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return name, os.cpu_count()
+
+
+def cpu_median(fn, seconds, min_runs=20, warmup=3):
+    """Median wall time of fn() over at least min_runs runs (and at least
+    `seconds` of work) after `warmup` untimed runs; returns (median s, runs,
+    last result)."""
+    for _ in range(warmup):
+        out = fn()
+    times, t_start = [], time.perf_counter()
+    while len(times) < min_runs or time.perf_counter() - t_start < seconds:
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times), out
+
+
+def cpu_baseline_record(value_gbps, median_s, runs, sample):
+    import oracle
+
+    name, nproc = cpu_model()
+    return {"value": round(value_gbps, 3), "unit": "GB/s", "cores": oracle.num_threads(), "kind": "port",
+            "sample": sample, "median_us": round(median_s * 1e6, 1), "runs": runs, "warmup": 3, "nproc": nproc,
+            "cpu_model": name,
+            "label": "restatement of reference algorithm (oracle/oracle.c, f32 online softmax of attn.wgsl), "
+                     "not reference binary"}
+
+
 def cpu_baseline(torch, pool, q0, y0, cfg, scale, seconds):
-    """Times the oracle on layer 0 of the workload (bounded sample)."""
+    """Times the oracle on layer 0 of the workload: median of >= 20 runs
+    after 3 warm-ups."""
     import numpy as np
 
     import oracle
@@ -264,17 +387,40 @@ def cpu_baseline(torch, pool, q0, y0, cfg, scale, seconds):
     B, ctx = cfg["batch"], cfg["ctx"]
     args = oracle.row_meta([ctx - 1] * B, list(range(B)))
     qn = q0.float().cpu().numpy()
-    runs, t0 = 0, time.perf_counter()
-    y = None
-    while True:
-        y = ref.attn(qn, args, B, cfg["q_heads"], scale, precision=1)
-        runs += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+    med, runs, y = cpu_median(lambda: ref.attn(qn, args, B, cfg["q_heads"], scale, precision=1), seconds)
     err = float(np.max(np.abs(y - y0.float().cpu().numpy())))
-    log(f"cpu baseline: {runs} runs in {el:.2f}s; max |cpu - gpu| = {err:.2e}")
-    return el / runs, runs, err
+    log(f"cpu baseline: median {med * 1e3:.1f} ms over {runs} runs; max |cpu - gpu| = {err:.2e}")
+    return med, runs, err
+
+
+def c1_cpu_baseline(torch, pool, rows, k, v, q, y, ctx, nq, hd, byts, seconds):
+    """C1, the shape BASELINE.json defines on the reference's CPU path: the
+    oracle's append (kv_store.wgsl) + f32 blockwise attention (attn.wgsl) of
+    the 4-row step on a host copy of the layer, median of >= 20 runs after 3
+    warm-ups."""
+    import numpy as np
+
+    import oracle
+
+    torch.cuda.synchronize()
+    kw, vw = pool.read_layer(0)
+    info = pool.arena.info()
+    ref = oracle.Layer(pool.kv_heads, hd, info.pages, pool.page_len, np.array(pool.arena.table(), np.uint32),
+                       info.max_pages, oracle.KV_F16, k=kw, v=vw)
+    B = len(ctx)
+    args = oracle.row_meta(ctx, list(range(B)))
+    kn, vn, qn = k.float().cpu().numpy(), v.float().cpu().numpy(), q.float().cpu().numpy()
+
+    def step():
+        ref.kv_store(kn, vn, args, B)
+        return ref.attn(qn, args, B, nq, 1.0 / math.sqrt(hd), precision=1)
+
+    med, runs, yc = cpu_median(step, seconds)
+    err = float(np.max(np.abs(yc - y.float().cpu().numpy())))
+    log(f"C1 cpu baseline: median {med * 1e6:.1f} us over {runs} runs; max |cpu - gpu| = {err:.2e}")
+    return cpu_baseline_record(byts / med / 1e9, med, runs,
+                               f"the C1 step (append 1 token + decode of {B} seqs, ctx {ctx}), median of {runs} "
+                               f"runs after 3 warm-ups, {med * 1e6:.1f} us/run, max |cpu-gpu| {err:.1e}")
 
 
 def _time_steps(torch, step, steps, warmup):
@@ -339,6 +485,9 @@ def run_secondary(args):
         sp = spec(rows, nq, hd, B)
         us = _time_steps(torch, lambda: ops.kv_store_attn(k, v, q, pool, 0, y, sp), args.steps, args.warmup)
         byts = sum(c + 1 for c in ctx) * nkv * hd * 2 * 2
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = c1_cpu_baseline(torch, pool, rows, k, v, q, y, ctx, nq, hd, byts,
+                                                  min(args.cpu_seconds, 3.0))
         out["config"] = {"workload": f"qwen2-0.5b C1: 1 layer, B=4, ctx {ctx}, 14q/2kv/hd64, page 16, f16 KV, "
                                      "step = append 1 token + decode (fused), f32 sources"}
     elif name == "qwen3-8b":  # C3: 64 ragged decode rows + 8 x 512 prefill rows in one call per layer
@@ -638,6 +787,15 @@ def main():
                    "fused_GBps": round(fused_bytes / (rope_us["fused"] * 1e-6) / 1e9, 1),
                    "note": "step with rotary embedding (theta 5e5, rot = head_dim): rope(q), rope(k), kv_store, "
                            "attn as four launches vs thb_attn_append_rope as one"}
+    ident_us = time_identity_leg(torch, ops, cfg, q, k_new, v_new)
+    log(f"identity block tables: {ident_us:.2f} us/layer vs scattered {attn_us:.2f}")
+    out["identity_vs_scattered"] = {
+        "identity_us_per_layer": round(ident_us, 2), "scattered_us_per_layer": round(attn_us, 2),
+        "scattered_over_identity": round(attn_us / ident_us, 4),
+        "note": "the same fused append + decode with every sequence on consecutive pages vs pages scattered "
+                "at random (thuban_bench probes/attn.rs:97-133 compares identity and shuffled tables)"}
+    out["o_proj"] = time_o_proj(torch, ops, dev, B, nq, hd, layers=L)
+    log(f"o_proj: {out['o_proj']['us_per_call']} us/call, {out['o_proj']['GBps']} GB/s")
     moves = time_gather_copy(torch, ops, pool, 1 % L, B, ctx, nkv, hd, pl, dev)
     log("gather/scatter/copy: " + ", ".join(f"{k} {v['us_per_call']} us {v['GBps']} GB/s" for k, v in moves.items()))
     out.update(moves)
@@ -649,14 +807,11 @@ def main():
         torch.cuda.synchronize()
         log(f"calibration: 3 copies of {args.calibrate_copy_mib} MiB")
     if not args.no_cpu_baseline:
-        per_run, runs, err = cpu_baseline(torch, pool, q[0], y[0], cfg, scale, args.cpu_seconds)
-        threads = __import__("oracle").num_threads()
-        out["cpu_baseline"] = {
-            "value": round(attn_bytes / per_run / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"layer 0 of the step (decode of {B} seqs x {nq} heads x {ctx} keys), oracle f32 "
-                      f"online-softmax restatement of attn.wgsl, {runs} runs, {per_run * 1e3:.1f} ms/run, "
-                      f"max |cpu-gpu| {err:.1e}",
-            "us_per_layer": round(per_run * 1e6, 1)}
+        med, runs, err = cpu_baseline(torch, pool, q[0], y[0], cfg, scale, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline_record(
+            attn_bytes / med / 1e9, med, runs,
+            f"layer 0 of the step (decode of {B} seqs x {nq} heads x {ctx} keys), median of {runs} runs after 3 "
+            f"warm-ups, {med * 1e3:.1f} ms/run, max |cpu-gpu| {err:.1e}")
     print(json.dumps(out), flush=True)
 
 

@@ -163,6 +163,8 @@ SIGNATURES = [
     ("thb_attn_append_rope", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC),
                                     ctypes.POINTER(RopeC), _vp, _vp]),
     ("thb_attn_step", _int, [_vp, _u32, ctypes.POINTER(AttnIoC), ctypes.POINTER(AttnSpecC), _vp, _vp]),
+    ("thb_check_gemm_dims", _int, [_u32, _u32]),
+    ("thb_gemm_acc", _int, [_vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _vp]),
     ("thb_attn_noalloc", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),

@@ -219,11 +219,31 @@ def kv_scatter(kv: KvPool, layer: int, seq: int, t0: int, n: int, k_src, v_src, 
                                _stream_ptr(stream)))
 
 
+def check_gemm_dims(pairs: Sequence[Sequence[int]]) -> None:
+    """ops::check_gemm_dims (crates/thuban_model/src/ops/gemm.rs:133-146):
+    every (N, K) pair needs N % 16 == 0 and K % 64 == 0 (ThubanError kind
+    "Config" otherwise)."""
+    for n, k in pairs:
+        check(lib().thb_check_gemm_dims(n, k))
+
+
+def gemm_acc(x, w, y, rows: int, acc: bool, stream=None) -> None:
+    """ops::gemm_acc (crates/thuban_model/src/ops/gemm.rs:113-131): y[rows, n]
+    = x[rows, k] . w[n, k]^T (+ y when acc); rows == 1 is the gemv.  x is
+    f32, f16 or bf16 (the attention output), w bf16 or f16 [n, k], y f32."""
+    n, k = w.shape
+    _buf("x", x, rows * k, _ACT)
+    _buf("w", w, n * k, ("bfloat16", "float16"))
+    _buf("y", y, rows * n, ("float32",))
+    check(lib().thb_gemm_acc(_addr("x", x), _dtype_code(x.dtype), _addr("w", w), _dtype_code(w.dtype),
+                             _addr("y", y), rows, n, k, 1 if acc else 0, _stream_ptr(stream)))
+
+
 def block_copy(kv: KvPool, triples: Sequence[Sequence[int]], stream=None) -> None:
     flat = [int(x) for t in triples for x in t]
     check(lib().thb_block_copy(kv.handle, _lib.u32_array(flat) if flat else None, len(flat) // 3,
                                _stream_ptr(stream)))
 
 
-__all__ = ["AttnSpec", "ThubanError", "attn", "attn_step", "block_copy", "check_head_dim", "default_scale", "kv_gather",
-           "kv_scatter", "kv_store", "kv_store_attn"]
+__all__ = ["AttnSpec", "ThubanError", "attn", "attn_step", "block_copy", "check_gemm_dims", "check_head_dim",
+           "default_scale", "gemm_acc", "kv_gather", "kv_scatter", "kv_store", "kv_store_attn"]

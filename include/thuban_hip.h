@@ -359,6 +359,25 @@ typedef struct thb_attn_io {
 int thb_attn_step(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_attn_spec* spec,
                   const thb_rows* rows, void* stream);
 
+/* ------------------------------------------------ the attention consumer */
+
+/* ops::check_gemm_dims (crates/thuban_model/src/ops/gemm.rs:133-146) for one
+ * pair: THB_ERR_CONFIG "dimension pair (N={n}, K={k}) does not satisfy N%16
+ * and K%64". */
+int thb_check_gemm_dims(uint32_t n, uint32_t k);
+/* ops::gemm_acc (crates/thuban_model/src/ops/gemm.rs:113-131), the o_proj
+ * product after attention (transformer/forward.rs:338-351), for plain 16-bit
+ * weights: y[rows, n] = x[rows, k] . w[n, k]^T, plus y's old value when acc
+ * (the reference adds into the residual stream).  rows == 1 is the
+ * reference's gemv.  x: THB_DT_F32 (the reference's activations),
+ * THB_DT_F16 or THB_DT_BF16 (thb_attn_spec.y_dtype); w: THB_DT_BF16 or
+ * THB_DT_F16; y: f32; all 16-byte aligned; n and k as thb_check_gemm_dims.
+ * Products on the matrix cores in f32 accumulation; an x wider than the
+ * weight type is split into high and low parts (f32-grade products).
+ * Deterministic: the same inputs give the same bits. */
+int thb_gemm_acc(const void* x_dev, uint32_t x_dtype, const void* w_dev, uint32_t w_dtype, float* y_dev,
+                 uint32_t rows, uint32_t n, uint32_t k, uint32_t acc, void* stream);
+
 /* No reference counterpart.  thb_attn for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops or harnesses
  * that forbid hipMalloc): the launch plan and the split-K partial results go

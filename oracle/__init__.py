@@ -99,6 +99,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_block_copy.restype = None
     L.orc_rope_rows.argtypes = [vp, u32, u32, u32, u32, vp, vp, u32, vp, vp, ctypes.c_float]
     L.orc_rope_rows.restype = ctypes.c_int
+    L.orc_gemm.argtypes = [vp, vp, vp, u32, u32, u32, ctypes.c_int, ctypes.c_int]
+    L.orc_gemm.restype = None
     L.orc_num_threads.argtypes = []
     L.orc_num_threads.restype = ctypes.c_int
 
@@ -239,6 +241,29 @@ def row_meta(positions, seqs) -> np.ndarray:
     a[0::8] = np.asarray(positions, np.uint32)
     a[1::8] = np.asarray(seqs, np.uint32)
     return a
+
+
+def gemm(x, w, m, n, k, y0=None, exact=False) -> np.ndarray:
+    """cpu_ref::gemm / gemv (cpu_ref.rs:11-35): x [m, k] . w[n, k]^T as f32
+    sums in k order, + y0 when given (acc).  exact=True sums in double and
+    rounds once."""
+    x = np.ascontiguousarray(x, np.float32).reshape(m, k)
+    w = np.ascontiguousarray(w, np.float32).reshape(n, k)
+    y = np.zeros((m, n), np.float32) if y0 is None else np.array(y0, np.float32).reshape(m, n)
+    lib().orc_gemm(_ptr(x), _ptr(w), _ptr(y), m, n, k, int(y0 is not None), int(bool(exact)))
+    return y
+
+
+def lcg_fill(seed: int, n: int) -> np.ndarray:
+    """The reference tests' Rng (crates/thuban_backend/tests/kernels.rs
+    :112-124): a 64-bit LCG, each draw (state >> 33) / 2^31 * 2 - 1 in f32."""
+    out = np.empty(n, np.float32)
+    state = seed & 0xFFFFFFFFFFFFFFFF
+    mul, inc, mask = 6364136223846793005, 1442695040888963407, 0xFFFFFFFFFFFFFFFF
+    for i in range(n):
+        state = (state * mul + inc) & mask
+        out[i] = np.float32(np.float32(state >> 33) / np.float32(1 << 31)) * np.float32(2.0) - np.float32(1.0)
+    return out
 
 
 def num_threads() -> int:

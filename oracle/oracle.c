@@ -14,6 +14,7 @@
  *   crates/thuban_backend/tests/support/cpu_ref.rs:172-228 exact softmax
  *   crates/thuban_kernel/wgsl/rope.wgsl:16-40     rotary embedding
  *   crates/thuban_kernel/wgsl/norm.wgsl:122-160   RMSNorm + rotation (MODE 4)
+ *   crates/thuban_backend/tests/support/cpu_ref.rs:11-35 gemm / gemv
  *
  * How each function is pinned (checked by tests/test_oracle.py):
  *   codecs        thuban_num known-answer tests (lib.rs:78-139) + exhaustive
@@ -28,6 +29,10 @@
  *                 round trips against kv_store)
  *   softcap       closed form cap*tanh(s/cap); parity vs the reference is
  *                 unpinned because the reference has no attention soft-cap.
+ *   gemm          cpu_ref::gemm/gemv (cpu_ref.rs:11-35): f32 sums in k order;
+ *                 pinned by numpy's float64 matmul within the f32 rounding
+ *                 bound, the identity-weight closed form y = x (+ y0), and
+ *                 rows == 1 equal to gemv
  *   rope_rows     reference anchor kernels.rs:1410-1436, the rope_case vectors
  *                 of kernels.rs:1200-1263 (LCG inputs) against a double-
  *                 precision rotation, position 0 = identity, dims >= rot
@@ -471,6 +476,35 @@ void orc_block_copy(orc_layer* L, const uint32_t* triples, uint32_t n) {
             size_t d = ((size_t)h * L->pool_len + (size_t)dp * L->page_len) * hd;
             memmove(L->k + d, L->k + s, (size_t)nt * hd * 2);
             memmove(L->v + d, L->v + s, (size_t)nt * hd * 2);
+        }
+    }
+}
+
+/* ----------------------------------------------------------------- gemm */
+
+/* cpu_ref::gemm (cpu_ref.rs:11-25): y[mi][ni] = sum over k in order of
+ * x[mi][k] * w[ni][k], an f32 sum, plus y's old value when acc (the
+ * reference's acc tests add y0 afterwards, kernels.rs:566-571).  rows == 1
+ * is cpu_ref::gemv (cpu_ref.rs:27-35), the same loop.  With exact != 0 the
+ * sums are taken in double and rounded once (the tight check). */
+void orc_gemm(const float* x, const float* w, float* y, uint32_t m, uint32_t n, uint32_t k, int acc, int exact) {
+#pragma omp parallel for schedule(static)
+    for (int64_t mi = 0; mi < (int64_t)m; mi++) {
+        for (uint32_t ni = 0; ni < n; ni++) {
+            const float* xr = x + (size_t)mi * k;
+            const float* wr = w + (size_t)ni * k;
+            float out;
+            if (exact) {
+                double s = 0.0;
+                for (uint32_t ki = 0; ki < k; ki++) s += (double)xr[ki] * (double)wr[ki];
+                if (acc) s += (double)y[(size_t)mi * n + ni];
+                out = (float)s;
+            } else {
+                float s = 0.0f;
+                for (uint32_t ki = 0; ki < k; ki++) s += xr[ki] * wr[ki];
+                out = acc ? s + y[(size_t)mi * n + ni] : s;
+            }
+            y[(size_t)mi * n + ni] = out;
         }
     }
 }

@@ -305,3 +305,52 @@ def test_rope_rmsnorm_matches_double(orc):
     assert np.allclose(only, t, rtol=1e-6, atol=1e-7)
     with pytest.raises(ValueError):
         orc.rope_rows(x, [3, 16], rot, cos, sin)  # position outside the tables
+
+
+def test_lcg_reproduces_the_reference_vector(orc, golden):
+    """oracle.lcg_fill restates the reference tests' Rng (kernels.rs
+    :112-124): Rng(111) draws the k_src then v_src of kv_store_writes_both_caches
+    (kernels.rs:1271-1273), transcribed bit by bit in kv_store_cases.json."""
+    case = [c for c in golden("kv_store_cases.json") if c["name"] == "kv_store_writes_both_caches"][0]
+    n = len(case["k_src"])
+    draws = orc.lcg_fill(111, 2 * n).view(np.uint32)
+    assert draws[:n].tolist() == case["k_src"] and draws[n:].tolist() == case["v_src"]
+
+
+def test_gemm_matches_float64_within_the_f32_bound(orc):
+    """cpu_ref::gemm's f32 sums in k order (cpu_ref.rs:11-25) against numpy's
+    float64 matmul: |f32 sum - exact| <= k * 2^-24 * sum |x w| (the textbook
+    bound of a sequential sum), and the double mode within one rounding."""
+    rng = np.random.default_rng(5)
+    for m, n, k in ((1, 32, 128), (7, 48, 256), (33, 16, 1024)):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        exact = x.astype(np.float64) @ w.astype(np.float64).T
+        bound = k * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+        got = orc.gemm(x, w, m, n, k)
+        assert np.all(np.abs(got - exact) <= bound + 1e-30)
+        ex = orc.gemm(x, w, m, n, k, exact=True)
+        assert np.all(np.abs(ex - exact) <= np.abs(exact) * 2.0 ** -24 + 1e-30)
+        y0 = rng.standard_normal((m, n)).astype(np.float32)
+        acc = orc.gemm(x, w, m, n, k, y0=y0, exact=True)
+        assert np.all(np.abs(acc - (exact + y0)) <= np.abs(exact + y0) * 2.0 ** -24 + 1e-30)
+
+
+def test_gemm_closed_forms(orc):
+    """Identity weights give y = x exactly (+ y0 with one rounding); a
+    single row equals cpu_ref::gemv, the same loop (cpu_ref.rs:27-35); a
+    transposed-operand mistake would break the rectangular case."""
+    rng = np.random.default_rng(6)
+    k = 64
+    x = rng.standard_normal((5, k)).astype(np.float32)
+    eye = np.eye(k, dtype=np.float32)
+    assert np.array_equal(orc.gemm(x, eye, 5, k, k), x)
+    y0 = rng.standard_normal((5, k)).astype(np.float32)
+    assert np.array_equal(orc.gemm(x, eye, 5, k, k, y0=y0), x + y0)
+    w = rng.standard_normal((16, k)).astype(np.float32)
+    full = orc.gemm(x, w, 5, 16, k)
+    for r in range(5):
+        assert np.array_equal(orc.gemm(x[r:r + 1], w, 1, 16, k), full[r:r + 1])
+    sel = np.zeros((3, k), np.float32)
+    sel[0, 2], sel[1, 7], sel[2, 63] = 1.0, 2.0, -1.0  # picks columns of x
+    assert np.array_equal(orc.gemm(x, sel, 5, 3, k), np.stack([x[:, 2], 2 * x[:, 7], -x[:, 63]], 1))
