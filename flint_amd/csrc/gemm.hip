@@ -13,17 +13,22 @@
 // (f16) bits of x against the exact weight, accumulated in f32.
 //
 // Two kernels:
-//  * gemm_skinny (rows <= 64, decode): one workgroup per 16 output columns,
+//  * gemm_skinny (rows <= 16, decode): one workgroup per 16 output columns,
 //    its 8 waves splitting the k-steps of 32.  Every wave issues the loads of
 //    all its weight slices and x operands (a batch of up to NB steps) before
 //    its first product, so a CU keeps 128 KiB of weights in flight; each
 //    weight byte is read once (non-temporal), x comes from L2.  The 8 waves'
 //    partial sums are added through LDS in wave order: one launch, no
 //    atomics, deterministic.
+//  * gemm_split + gemm_merge (rows 17..64): K in slices of 1024, x's slice
+//    staged once per workgroup in LDS, partial sums merged in slice order
+//    by a second kernel (the reference's split-K merge_gemm.wgsl order).
 //  * gemm_tile (rows > 64, prefill): 128 x 128 output tiles, 4 waves of
 //    64 x 64, k-tiles of 64 staged in double-buffered LDS (rows of 144
 //    bytes: conflict-free 16-byte operand reads), the next tile's loads in
 //    flight during the products.
+#include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -137,9 +142,19 @@ __global__ __launch_bounds__(512) void gemm_skinny(GemmArgs a) {
     const uint32_t c = lane & 15u, g = lane >> 4;
     const uint32_t n0 = blockIdx.x * 16u;
     const uint32_t steps = a.k >> 5;
-    const uint32_t s0 = wave * steps / 8u, s1 = (wave + 1) * steps / 8u;
+    // The wave's chunk of k-steps, rotated by the workgroup index: at any
+    // moment the workgroups read different parts of x (every workgroup reads
+    // all of x from L2; in the same order they queued on the same lines).
+    const uint32_t chunk = (wave + blockIdx.x) & 7u;
+    const uint32_t s0 = chunk * steps / 8u, s1 = (chunk + 1) * steps / 8u;
     // A operand: weight row n0 + c, k = 32 s + 8 g .. + 8 (16 bytes).
     const uint16_t* wrow = a.w + static_cast<uint64_t>(n0 + c) * a.k + 8u * g;
+    // The accumulated y of the writing waves is requested with the first
+    // loads, not after the products (one round trip less).
+    f32x4 y_old = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t y_row = 16u * wave + c;
+    f32x4* yp = reinterpret_cast<f32x4*>(a.y + static_cast<uint64_t>(y_row) * a.n + n0 + 4u * g);
+    if (a.acc && wave < static_cast<uint32_t>(MT) && y_row < a.m) y_old = *yp;
     f32x4 d[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) d[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -178,19 +193,17 @@ __global__ __launch_bounds__(512) void gemm_skinny(GemmArgs a) {
         }
     }
     // Lane (c, g) holds D[n = 4 g + r][m = c] of each m-tile: add the 8
-    // waves' sums in wave order and write y[16 t + c][n0 + 4 g .. + 4].
+    // chunks' sums in k order and write y[16 t + c][n0 + 4 g .. + 4].
     __shared__ f32x4 red[8][MT][64];
 #pragma unroll
-    for (int t = 0; t < MT; t++) red[wave][t][lane] = d[t];
+    for (int t = 0; t < MT; t++) red[chunk][t][lane] = d[t];
     __syncthreads();
     if (wave < static_cast<uint32_t>(MT)) {
         f32x4 s = red[0][wave][lane];
 #pragma unroll
         for (int q = 1; q < 8; q++) s += red[q][wave][lane];
-        const uint32_t row = 16u * wave + c;
-        if (row < a.m) {
-            f32x4* yp = reinterpret_cast<f32x4*>(a.y + static_cast<uint64_t>(row) * a.n + n0 + 4u * g);
-            if (a.acc) s += *yp;
+        if (y_row < a.m) {
+            if (a.acc) s += y_old;
             *yp = s;
         }
     }
@@ -299,6 +312,160 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmArgs a) {
     }
 }
 
+// Rows 17..64: K split into S slices.  Workgroup (n-block of 64 columns, k
+// slice q) stages x's slice once in LDS as B operands ([8-element k chunk]
+// [row] x 16 bytes, high and low parts), so the 256 workgroups read x's
+// slice once instead of all of x once per 16 columns (at 32 rows and k =
+// 4096, reading all of x per workgroup measured 8.4 us of L2 traffic that
+// did not overlap the 7.5 us weight stream; split: 12.2 us + the merge,
+// against 16.3 us in one pass).  Wave w: n-tile
+// w % 4, half w / 4 of the slice's k-steps, every weight load issued before
+// the first product.  Partial sums go to part[q][m][n]; gemm_merge adds them
+// in slice order.
+struct SplitArgs {
+    GemmArgs g;
+    float* part;  // [S][m][n]
+    uint32_t S, m16;
+};
+
+template <uint32_t XT, bool WF16, int MT>
+__global__ __launch_bounds__(512) void gemm_split(SplitArgs sa) {
+    using O = WOps<WF16>;
+    constexpr bool LO = needs_lo(XT, WF16);
+    constexpr int XW = x_words(XT);
+    constexpr int NWB = 16;  // weight loads per wave issued up front (more: a second batch)
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs_lds[];
+    const GemmArgs& a = sa.g;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t c = lane & 15u, g = lane >> 4, nt = wave & 3u, half = wave >> 2;
+    const uint32_t n0 = blockIdx.x * 64u + 16u * nt, q = blockIdx.y;
+    const uint32_t steps = a.k >> 5;
+    const uint32_t q0 = q * steps / sa.S, q1 = (q + 1) * steps / sa.S, nq = q1 - q0;
+    const uint32_t s0 = q0 + half * nq / 2u, s1 = q0 + (half + 1) * nq / 2u;
+    const uint32_t m16 = sa.m16, chunks = 4u * nq;  // 8-element k chunks of the slice
+    // LDS: operand (chunk ch, row r) at (ch * (m16 + 1) + r) * 16 bytes; the
+    // padding row keeps both the staging stores (consecutive chunks of a
+    // row) and the operand reads (consecutive rows of a chunk) free of bank
+    // conflicts.
+    const uint32_t rs = m16 + 1u;
+    uint8_t* lo_base = xs_lds + static_cast<size_t>(chunks) * rs * 16u;
+    // Order of the loads: the first XB items of the x slice, then the first
+    // batch of weights, so x arrives first (a wave's loads return in order)
+    // and is staged while the weights stream.
+    constexpr int XB = 8;
+    const uint32_t items = chunks * m16;  // item i: row i / chunks, chunk i % chunks (coalesced reads)
+    uint32_t xv[XB][XW];
+    auto load_items = [&](uint32_t i0) {
+#pragma unroll
+        for (int j = 0; j < XB; j++) {
+            const uint32_t i = i0 + 512u * j + tid, r = i / chunks, ch = i - r * chunks;
+            if (i < items && r < a.m) {
+                load_x8<XT>(a.x, static_cast<uint64_t>(r) * a.k + 8u * (4u * q0 + ch), xv[j]);
+            } else {
+#pragma unroll
+                for (int w = 0; w < XW; w++) xv[j][w] = 0u;
+            }
+        }
+    };
+    auto store_items = [&](uint32_t i0) {
+#pragma unroll
+        for (int j = 0; j < XB; j++) {
+            const uint32_t i = i0 + 512u * j + tid, r = i / chunks, ch = i - r * chunks;
+            if (i < items) {
+                typename O::v8 hi, lo;
+                x_operands<XT, WF16>(xv[j], hi, lo);
+                const size_t off = (static_cast<size_t>(ch) * rs + r) * 16u;
+                *reinterpret_cast<typename O::v8*>(xs_lds + off) = hi;
+                if constexpr (LO) *reinterpret_cast<typename O::v8*>(lo_base + off) = lo;
+            }
+        }
+    };
+    load_items(0);
+    const uint16_t* wrow = a.w + static_cast<uint64_t>(n0 + c) * a.k + 8u * g;
+    u32x4 wv[NWB];
+#pragma unroll
+    for (int i = 0; i < NWB; i++)
+        if (s0 + i < s1) wv[i] = ld_nt16(wrow + 32u * (s0 + i));
+    store_items(0);
+    for (uint32_t i0 = 512u * XB; i0 < items; i0 += 512u * XB) {  // more rows than fit one batch
+        load_items(i0);
+        store_items(i0);
+    }
+    __syncthreads();
+    f32x4 d[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) d[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t sb = s0; sb < s1; sb += NWB) {
+        if (sb != s0) {  // later batches (more than NWB steps per wave)
+#pragma unroll
+            for (int i = 0; i < NWB; i++)
+                if (sb + i < s1) wv[i] = ld_nt16(wrow + 32u * (sb + i));
+        }
+#pragma unroll
+        for (int i = 0; i < NWB; i++) {
+            if (sb + i < s1) {
+                const typename O::v8 A = __builtin_bit_cast(typename O::v8, wv[i]);
+                const uint32_t ch = 4u * (sb + i - q0) + g;
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const size_t off = (static_cast<size_t>(ch) * rs + 16u * t + c) * 16u;
+                    d[t] = O::mfma(A, *reinterpret_cast<const typename O::v8*>(xs_lds + off), d[t]);
+                    if constexpr (LO)
+                        d[t] = O::mfma(A, *reinterpret_cast<const typename O::v8*>(lo_base + off), d[t]);
+                }
+            }
+        }
+    }
+    // The two halves of each n-tile add through LDS (half 0 + half 1), then
+    // half 0 writes part[q][16 t + c][n0 + 4 g .. + 4].
+    __syncthreads();
+    f32x4* red = reinterpret_cast<f32x4*>(xs_lds);  // [4 n-tiles][MT][64]
+    if (half == 1)
+#pragma unroll
+        for (int t = 0; t < MT; t++) red[(nt * MT + t) * 64u + lane] = d[t];
+    __syncthreads();
+    if (half == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const uint32_t row = 16u * t + c;
+            if (row < a.m) {
+                const f32x4 s = d[t] + red[(nt * MT + t) * 64u + lane];
+                *reinterpret_cast<f32x4*>(sa.part + (static_cast<uint64_t>(q) * a.m + row) * a.n + n0 + 4u * g) = s;
+            }
+        }
+    }
+}
+
+// y = (acc ? y : 0) + part[0] + part[1] + ... in slice order, as the
+// reference's merge_gemm.wgsl adds its segments; 4 columns per thread.
+__global__ __launch_bounds__(256) void gemm_merge(const float* part, float* y, uint32_t mn4, uint32_t S, uint32_t acc) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= mn4) return;
+    const f32x4* p = reinterpret_cast<const f32x4*>(part) + i;
+    f32x4 s = acc ? reinterpret_cast<const f32x4*>(y)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t q0 = 0; q0 < S; q0 += 8) {  // 8 slices requested at once, added in order
+        f32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (q0 + j < S) v[j] = p[static_cast<uint64_t>(q0 + j) * mn4];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (q0 + j < S) s += v[j];
+    }
+    reinterpret_cast<f32x4*>(y)[i] = s;
+}
+
+// k-steps of 32 per slice of the split kernel (half that with a low part).
+#ifndef THB_GEMM_SLICE_STEPS
+#define THB_GEMM_SLICE_STEPS 32
+#endif
+
+// Library-owned partial sums of the split kernel, per device (the
+// reference's backend keeps gemm_partial the same way, matmul.rs:9-18).
+constexpr int kMaxDev = 64;
+DevBuf g_part[kMaxDev];
+std::mutex g_part_mu;
+
 template <uint32_t XT, bool WF16>
 void launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.m > 64) {
@@ -306,19 +473,59 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
         hipLaunchKernelGGL((gemm_tile<XT, WF16>), grid, dim3(256), 0, s, a);
         return;
     }
-    const dim3 grid(a.n / 16);
-    // Steps prefetched per batch: all 16 of a wave at k = 4096 for up to 32
-    // rows of 16-bit x; fewer where the operands take more registers.
-    constexpr int NB2 = XT == THB_DT_F32 ? 8 : 16;
-    constexpr int NB4 = XT == THB_DT_F32 ? 4 : 8;
+    constexpr int NB = XT == THB_DT_F32 ? 8 : 16;  // steps prefetched per batch
+    if (a.m <= 16 || a.n % 64 != 0) {
+        // Up to 16 rows (the gemv included), and widths that are not a
+        // multiple of 64: one pass, every workgroup reading all of x.  At 16
+        // rows and k = 4096 that is 128 KiB per workgroup from L2, cheaper
+        // than the split kernel's partial round trip (Llama-3-8B o_proj,
+        // kernel trace: 9.6 us one pass; 11.2 us split + 1.5-4 us merge).
+        const dim3 grid(a.n / 16);
+        if (a.m <= 16)
+            hipLaunchKernelGGL((gemm_skinny<XT, WF16, 1, NB>), grid, dim3(512), 0, s, a);
+        else if (a.m <= 32)
+            hipLaunchKernelGGL((gemm_skinny<XT, WF16, 2, NB>), grid, dim3(512), 0, s, a);
+        else if (a.m <= 48)
+            hipLaunchKernelGGL((gemm_skinny<XT, WF16, 3, NB / 2>), grid, dim3(512), 0, s, a);
+        else
+            hipLaunchKernelGGL((gemm_skinny<XT, WF16, 4, NB / 2>), grid, dim3(512), 0, s, a);
+        return;
+    }
+    // Slices of at most 1024 k (512 with a low part), so that x's slice for
+    // 64 rows fits 128 KiB of LDS; a function of k and the types only, so a
+    // row's sums do not depend on how many rows the call has.
+    constexpr bool LO = needs_lo(XT, WF16);
+    const uint32_t steps = a.k / 32, kq = LO ? THB_GEMM_SLICE_STEPS / 2 : THB_GEMM_SLICE_STEPS;
+    const uint32_t S = std::max<uint32_t>(1, (steps + kq - 1) / kq);
+    const uint32_t m16 = (a.m + 15) / 16 * 16;
+    const uint32_t nq_max = (steps + S - 1) / S;
+    const size_t lds = std::max<size_t>(static_cast<size_t>(4u * nq_max) * (m16 + 1) * 16u * (LO ? 2 : 1),
+                                        4u * 4u * 64u * 16u);
+    int dev = 0;
+    THB_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDev) throw HipError{hipErrorInvalidDevice, "gemm partial buffer"};
+    float* part;
+    {
+        std::lock_guard<std::mutex> lock(g_part_mu);
+        part = static_cast<float*>(g_part[dev].reserve(static_cast<size_t>(S) * a.m * a.n * 4, false));
+    }
+    SplitArgs sa;
+    sa.g = a;
+    sa.part = part;
+    sa.S = S;
+    sa.m16 = m16;
+    const dim3 grid(a.n / 64, S);
     if (a.m <= 16)
-        hipLaunchKernelGGL((gemm_skinny<XT, WF16, 1, NB2>), grid, dim3(512), 0, s, a);
+        hipLaunchKernelGGL((gemm_split<XT, WF16, 1>), grid, dim3(512), lds, s, sa);
     else if (a.m <= 32)
-        hipLaunchKernelGGL((gemm_skinny<XT, WF16, 2, NB2>), grid, dim3(512), 0, s, a);
+        hipLaunchKernelGGL((gemm_split<XT, WF16, 2>), grid, dim3(512), lds, s, sa);
     else if (a.m <= 48)
-        hipLaunchKernelGGL((gemm_skinny<XT, WF16, 3, NB4>), grid, dim3(512), 0, s, a);
+        hipLaunchKernelGGL((gemm_split<XT, WF16, 3>), grid, dim3(512), lds, s, sa);
     else
-        hipLaunchKernelGGL((gemm_skinny<XT, WF16, 4, NB4>), grid, dim3(512), 0, s, a);
+        hipLaunchKernelGGL((gemm_split<XT, WF16, 4>), grid, dim3(512), lds, s, sa);
+    THB_HIP(hipGetLastError());
+    const uint32_t mn4 = a.m * a.n / 4;
+    hipLaunchKernelGGL(gemm_merge, dim3((mn4 + 255) / 256), dim3(256), 0, s, part, a.y, mn4, S, a.acc);
 }
 
 template <bool WF16>
