@@ -133,9 +133,13 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
         return graph
 
     gg, gs = graph_of_fn(lambda: sweep(ops.kv_gather)), graph_of_fn(lambda: sweep(ops.kv_scatter))
-    gg.replay()
-    gs.replay()
+    ranges = [(s, layer, 0, ctx) for s in range(B)]
+    bg = graph_of_fn(lambda: ops.kv_gather_batch(pool, ranges, kb, vb))
+    bs = graph_of_fn(lambda: ops.kv_scatter_batch(pool, ranges, kb, vb))
+    for gr in (gg, gs, bg, bs):
+        gr.replay()
     torch.cuda.synchronize()
+    ev += [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     ev[0].record()
     for _ in range(reps):
         gg.replay()
@@ -143,11 +147,19 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
     for _ in range(reps):
         gs.replay()
     ev[2].record()
+    for _ in range(reps):
+        bg.replay()
+    ev[3].record()
+    for _ in range(reps):
+        bs.replay()
+    ev[4].record()
     torch.cuda.synchronize()
-    del gg, gs
+    del gg, gs, bg, bs
     moved = B * nkv * ctx * hd * 2 * 2
     g_us = ev[0].elapsed_time(ev[1]) / reps * 1e3
     s_us = ev[1].elapsed_time(ev[2]) / reps * 1e3
+    bg_us = ev[2].elapsed_time(ev[3]) / reps * 1e3
+    bs_us = ev[3].elapsed_time(ev[4]) / reps * 1e3
     del kb, vb
     spare, held = 512, 3584  # pages: copy destinations / held by the second pool's sequences
     cpool = KvPool(ArenaSpec([ctx] * (-(-held * pl // ctx)), held + spare), nkv, hd, layers=pool.layers,
@@ -201,6 +213,8 @@ def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
     return {"gather": rec(g_us, moved, f"kv_gather of all {B} sequences x {ctx} tokens of one layer "
                                        f"({B} calls, one graph) into [kv_heads, ctx, head_dim]"),
             "scatter": rec(s_us, moved, f"kv_scatter of the same {B} buffers back ({B} calls, one graph)"),
+            "gather_batch": rec(bg_us, moved, f"kv_gather_batch: the same {B} sequences in one call (one launch)"),
+            "scatter_batch": rec(bs_us, moved, f"kv_scatter_batch: the same {B} buffers back in one call"),
             "block_copy": rec(c_us, c_moved, f"one block_copy call of {len(triples)} whole pages x "
                                              f"{pool.layers} layers x K,V x {nkv} heads"),
             "append_bulk": {"us_per_call": round(a_us, 2), "GBps": round(a_bytes / (a_us * 1e-6) / 1e9, 1),

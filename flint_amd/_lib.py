@@ -112,6 +112,10 @@ class AttnIoC(ctypes.Structure):
     ]
 
 
+class KvRangeC(ctypes.Structure):
+    _fields_ = [("seq", ctypes.c_uint32), ("layer", ctypes.c_uint32), ("t0", ctypes.c_uint32), ("n", ctypes.c_uint32)]
+
+
 # (name, restype, argtypes) for every symbol declared in include/thuban_hip.h.
 _vp, _u32, _u64, _i64, _sz, _int = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int64,
                                     ctypes.c_size_t, ctypes.c_int)
@@ -168,6 +172,8 @@ SIGNATURES = [
     ("thb_attn_noalloc", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
+    ("thb_kv_gather_batch", _int, [_vp, ctypes.POINTER(KvRangeC), _u32, _vp, _vp, _vp]),
+    ("thb_kv_scatter_batch", _int, [_vp, ctypes.POINTER(KvRangeC), _u32, _vp, _vp, _vp]),
     ("thb_block_copy", _int, [_vp, _pu32, _u32, _vp]),
 ]
 

@@ -6,6 +6,7 @@
 // ([P/4][hd][4], the operand layout of the attention kernel's PV product),
 // so the lane's 8 V elements are 8 16-bit accesses 8 bytes apart.
 #include <algorithm>
+#include <array>
 #include <string>
 
 #include "codec.hpp"
@@ -330,7 +331,15 @@ struct GatherArgs {
     uint32_t page_shift, head_dim, n, t0;
     uint32_t tile;   // tokens per LDS tile of V (min(page_len, 64))
     uint32_t heads;  // KV heads per workgroup
+    // Batched calls (null otherwise): work item x = (range, page of the
+    // range), and the range records, kRangeWords each: seq table row offset,
+    // t0, n, pad, then K plane, V plane and flat element offsets (64 bits
+    // each).  k / v / k_flat / v_flat are then the bases those offsets add to.
+    const uint32_t* items;
+    const uint32_t* ranges;
 };
+
+constexpr uint32_t kRangeWords = 10;
 
 // Copies a 16-byte V unit (dims d, d + 1 x the 4 slots of a group; element
 // i is slot i % 4 of dim d + i / 4) from `src` to `dst`, keeping the slots
@@ -385,13 +394,28 @@ struct DivSmall {
 //   [slot][dim] (rows of head_dim + 8 elements, 16-byte aligned), and a group
 //   that the range cuts is merged into its 16 bytes by one lane.
 template <bool TO_FLAT>
-__global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
+__global__ __launch_bounds__(256) void gather_kernel(GatherArgs args) {
     extern __shared__ uint4 s_tile[];
+    GatherArgs a = args;
+    uint32_t page = blockIdx.x;  // page of the range
+    if (args.items) {  // batched: this workgroup's range
+        const uint32_t r = args.items[2 * blockIdx.x];
+        page = args.items[2 * blockIdx.x + 1];
+        const uint32_t* R = args.ranges + static_cast<uint64_t>(r) * kRangeWords;
+        auto off64 = [&](int w) { return static_cast<uint64_t>(R[w]) | (static_cast<uint64_t>(R[w + 1]) << 32); };
+        a.table_row = args.table_row + R[0];
+        a.t0 = R[1];
+        a.n = R[2];
+        a.k = args.k + off64(4);
+        a.v = args.v + off64(6);
+        a.k_flat = args.k_flat + off64(8);
+        a.v_flat = args.v_flat + off64(8);
+    }
     const uint32_t shift = a.page_shift, hd = a.head_dim, cph = hd >> 3, T = a.tile;
     const uint32_t RS = hd + 8;                // LDS row stride (16-bit elements)
     const uint32_t tile_elems = T * RS;
     uint16_t* tile16 = reinterpret_cast<uint16_t*>(s_tile);
-    const uint32_t pi = (a.t0 >> shift) + blockIdx.x, h0 = blockIdx.y * a.heads;
+    const uint32_t pi = (a.t0 >> shift) + page, h0 = blockIdx.y * a.heads;
     const uint32_t p0 = pi << shift;
     const uint32_t ja = max(a.t0, p0) - p0;
     const uint32_t jb = static_cast<uint32_t>(
@@ -862,6 +886,41 @@ int thb_kv_store(thb_pool* pool, uint32_t layer, const void* k_src, const void* 
     });
 }
 
+// A scatter writes in place: a page another sequence also holds (a fork's
+// shared prefix) would change under it.
+static int check_unshared(const thb_pool* pool, uint32_t seq, uint32_t t0, uint32_t n) {
+    const Arena& ar = pool->arena.a;
+    const auto& tbl = ar.table_of(seq);
+    const uint32_t p0 = t0 >> pool->page_shift;
+    const uint32_t p1 = static_cast<uint32_t>((static_cast<uint64_t>(t0) + n - 1) >> pool->page_shift);
+    for (uint32_t i = p0; i <= p1; i++)
+        if (ar.refs()[tbl[i]] > 1)
+            return fail(THB_ERR_MODEL, "scatter into page " + std::to_string(tbl[i]) + " of sequence " +
+                                           std::to_string(seq) + ", which is shared with another sequence");
+    return THB_OK;
+}
+
+// Launch shape of the gather kernel at one head_dim: LDS tile of V and KV
+// heads per workgroup.  V tile: up to 64 slots x (head_dim + 8) elements,
+// at most 32 KiB of LDS per head.  Heads per workgroup: enough for 4 KiB of
+// K per page (small pages), at most 4, within 64 KiB of LDS.  More heads
+// per workgroup serialise load rounds and measured slower at 4 KiB pages.
+static void gather_shape(const thb_pool* pool, uint32_t hd, GatherArgs& a, size_t& lds) {
+    uint32_t tile = std::min(pool->page_len, 64u);
+    while (tile > 4 && tile * (hd + 8) * 2 > 32768) tile >>= 1;
+    a.tile = tile;
+    const size_t tile_bytes = static_cast<size_t>(tile) * (hd + 8) * 2;
+    const uint32_t want = std::min<uint32_t>(4, std::max<uint32_t>(1, 2048 / (pool->page_len * hd)));
+    uint32_t heads = 1;
+    for (uint32_t hpw = want; hpw > 1; hpw--)
+        if (pool->kv_heads % hpw == 0 && hpw * tile_bytes <= 65536) {
+            heads = hpw;
+            break;
+        }
+    a.heads = heads;
+    lds = heads * tile_bytes;
+}
+
 static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uint32_t n, void* k, void* v,
                          void* stream, bool to_flat) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
@@ -870,23 +929,13 @@ static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t 
     if (!k || !v) return fail(THB_ERR_INVALID, "null buffer");
     if (!aligned16(k) || !aligned16(v)) return fail(THB_ERR_INVALID, "buffers must be 16-byte aligned");
     if (int rc = check_cover(pool, seq, static_cast<uint64_t>(t0) + n)) return rc;
-    if (!to_flat) {
-        // A scatter writes in place: a page another sequence also holds (a
-        // fork's shared prefix) would change under it.
-        const Arena& ar = pool->arena.a;
-        const auto& tbl = ar.table_of(seq);
-        const uint32_t p0 = t0 >> pool->page_shift;
-        const uint32_t p1 = static_cast<uint32_t>((static_cast<uint64_t>(t0) + n - 1) >> pool->page_shift);
-        for (uint32_t i = p0; i <= p1; i++)
-            if (ar.refs()[tbl[i]] > 1)
-                return fail(THB_ERR_MODEL, "scatter into page " + std::to_string(tbl[i]) + " of sequence " +
-                                               std::to_string(seq) + ", which is shared with another sequence");
-    }
+    if (!to_flat)
+        if (int rc = check_unshared(pool, seq, t0, n)) return rc;
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
         const LayerGeom& g = pool->geom[layer];
-        GatherArgs a;
+        GatherArgs a{};
         a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
         a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
         a.k_flat = static_cast<uint16_t*>(k);
@@ -897,26 +946,102 @@ static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t 
         a.head_dim = g.head_dim;
         a.n = n;
         a.t0 = t0;
-        // V tile: up to 64 slots x (head_dim + 8) elements, at most 32 KiB of
-        // LDS per head.  Heads per workgroup: enough for 4 KiB of K per page
-        // (small pages), at most 4, within 64 KiB of LDS.  More heads per
-        // workgroup serialise load rounds and measured slower at 4 KiB pages.
-        uint32_t tile = std::min(pool->page_len, 64u);
-        while (tile > 4 && tile * (g.head_dim + 8) * 2 > 32768) tile >>= 1;
-        a.tile = tile;
-        const size_t tile_bytes = static_cast<size_t>(tile) * (g.head_dim + 8) * 2;
-        const uint32_t want = std::min<uint32_t>(4, std::max<uint32_t>(1, 2048 / (pool->page_len * g.head_dim)));
-        uint32_t heads = 1;
-        for (uint32_t hpw = want; hpw > 1; hpw--)
-            if (pool->kv_heads % hpw == 0 && hpw * tile_bytes <= 65536) {
-                heads = hpw;
-                break;
-            }
-        a.heads = heads;
-        const size_t lds = heads * tile_bytes;
+        size_t lds = 0;
+        gather_shape(pool, g.head_dim, a, lds);
         const uint32_t pages = static_cast<uint32_t>(((static_cast<uint64_t>(t0) + n - 1) >> pool->page_shift) -
                                                      (t0 >> pool->page_shift) + 1);
-        dim3 grid(pages, pool->kv_heads / heads);
+        dim3 grid(pages, pool->kv_heads / a.heads);
+        if (to_flat)
+            hipLaunchKernelGGL(gather_kernel<true>, grid, dim3(256), lds, s, a);
+        else
+            hipLaunchKernelGGL(gather_kernel<false>, grid, dim3(256), lds, s, a);
+        THB_HIP(hipGetLastError());
+        return THB_OK;
+    });
+}
+
+// One launch over many ranges: range i moves to / from [kv_heads, n_i,
+// head_dim] at element offset sum_{j < i} kv_heads * n_j * head_dim.
+static int gather_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t count, void* k, void* v, void* stream,
+                        bool to_flat) {
+    if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (count == 0) return THB_OK;
+    if (!ranges) return fail(THB_ERR_INVALID, "ranges is null");
+    if (!k || !v) return fail(THB_ERR_INVALID, "null buffer");
+    if (!aligned16(k) || !aligned16(v)) return fail(THB_ERR_INVALID, "buffers must be 16-byte aligned");
+    uint32_t hd = 0;
+    for (uint32_t i = 0; i < count; i++) {
+        const thb_kv_range& r = ranges[i];
+        if (int rc = check_layer(pool, r.layer)) return rc;
+        if (r.n == 0) continue;
+        if (hd == 0) hd = pool->geom[r.layer].head_dim;
+        if (pool->geom[r.layer].head_dim != hd)
+            return fail(THB_ERR_INVALID, "the ranges of one batched call must share a head_dim");
+        if (int rc = check_cover(pool, r.seq, static_cast<uint64_t>(r.t0) + r.n)) return rc;
+        if (!to_flat)
+            if (int rc = check_unshared(pool, r.seq, r.t0, r.n)) return rc;
+    }
+    if (hd == 0) return THB_OK;
+    if (!to_flat) {  // two ranges writing one token would race
+        std::vector<std::array<uint64_t, 3>> spans;
+        for (uint32_t i = 0; i < count; i++)
+            if (ranges[i].n)
+                spans.push_back({(static_cast<uint64_t>(ranges[i].layer) << 32) | ranges[i].seq, ranges[i].t0,
+                                 static_cast<uint64_t>(ranges[i].t0) + ranges[i].n});
+        std::sort(spans.begin(), spans.end());
+        for (size_t i = 1; i < spans.size(); i++)
+            if (spans[i][0] == spans[i - 1][0] && spans[i][1] < spans[i - 1][2])
+                return fail(THB_ERR_INVALID, "scatter ranges of one sequence and layer overlap");
+    }
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        const uint32_t mp = pool->arena.a.max_pages();
+        std::vector<uint32_t> blob;  // items (2 words each), then the range records
+        std::vector<uint32_t> recs;
+        uint64_t flat = 0;
+        for (uint32_t i = 0; i < count; i++) {
+            const thb_kv_range& r = ranges[i];
+            const uint32_t rec = static_cast<uint32_t>(recs.size() / kRangeWords);
+            if (r.n) {
+                const uint32_t pages = static_cast<uint32_t>(
+                    ((static_cast<uint64_t>(r.t0) + r.n - 1) >> pool->page_shift) - (r.t0 >> pool->page_shift) + 1);
+                for (uint32_t p = 0; p < pages; p++) blob.insert(blob.end(), {rec, p});
+                const LayerGeom& g = pool->geom[r.layer];
+                const uint64_t ko = g.k_off / 2, vo = g.v_off / 2;  // 16-bit elements from the arena base
+                recs.insert(recs.end(), {r.seq * mp, r.t0, r.n, 0u, static_cast<uint32_t>(ko),
+                                         static_cast<uint32_t>(ko >> 32), static_cast<uint32_t>(vo),
+                                         static_cast<uint32_t>(vo >> 32), static_cast<uint32_t>(flat),
+                                         static_cast<uint32_t>(flat >> 32)});
+            }
+            flat += static_cast<uint64_t>(pool->kv_heads) * r.n * hd;
+        }
+        const uint32_t n_items = static_cast<uint32_t>(blob.size() / 2);
+        if (n_items > 0x7FFFFFFFu) throw HipError{hipErrorInvalidConfiguration, "batched gather too large"};
+        const size_t items_words = blob.size();
+        blob.insert(blob.end(), recs.begin(), recs.end());
+        // Uploaded only when the ranges change: repeating a call (or
+        // capturing it in a graph after a first call) moves nothing.
+        if (blob != pool->range_key) {
+            void* d = pool->range_buf.reserve(blob.size() * 4, false);
+            pool->stager.upload(d, blob.data(), blob.size() * 4, s);
+            pool->range_key.swap(blob);
+        }
+        const uint32_t* dev = static_cast<const uint32_t*>(pool->range_buf.get());
+        GatherArgs a{};
+        a.k = reinterpret_cast<uint16_t*>(pool->mem);
+        a.v = reinterpret_cast<uint16_t*>(pool->mem);
+        a.k_flat = static_cast<uint16_t*>(k);
+        a.v_flat = static_cast<uint16_t*>(v);
+        a.table_row = pool->table_dev;
+        a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
+        a.page_shift = pool->page_shift;
+        a.head_dim = hd;
+        a.items = dev;
+        a.ranges = dev + items_words;
+        size_t lds = 0;
+        gather_shape(pool, hd, a, lds);
+        dim3 grid(n_items, pool->kv_heads / a.heads);
         if (to_flat)
             hipLaunchKernelGGL(gather_kernel<true>, grid, dim3(256), lds, s, a);
         else
@@ -934,6 +1059,16 @@ int thb_kv_gather(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uin
 int thb_kv_scatter(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uint32_t n, const void* k_src,
                    const void* v_src, void* stream) {
     return gather_common(pool, layer, seq, t0, n, const_cast<void*>(k_src), const_cast<void*>(v_src), stream, false);
+}
+
+int thb_kv_gather_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t count, void* k_dst, void* v_dst,
+                        void* stream) {
+    return gather_batch(pool, ranges, count, k_dst, v_dst, stream, true);
+}
+
+int thb_kv_scatter_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t count, const void* k_src,
+                         const void* v_src, void* stream) {
+    return gather_batch(pool, ranges, count, const_cast<void*>(k_src), const_cast<void*>(v_src), stream, false);
 }
 
 int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* stream) {

@@ -98,6 +98,8 @@ struct thb_pool {
     thb::DevBuf geom_buf;            // per-layer DevLayer records
     thb::DevBuf partials;            // split-K partial results
     thb::DevBuf run_buf;             // append runs of the last row meta the append cut into runs
+    thb::DevBuf range_buf;           // work items and range records of a batched gather / scatter
+    std::vector<uint32_t> range_key; // what range_buf holds
     // Key of run_buf's contents: the model appends the same rows to every
     // layer, so the runs are cut and uploaded once per row-meta write.
     const void* runs_rows = nullptr;

@@ -219,6 +219,37 @@ def kv_scatter(kv: KvPool, layer: int, seq: int, t0: int, n: int, k_src, v_src, 
                                _stream_ptr(stream)))
 
 
+def _ranges_c(kv: KvPool, ranges):
+    arr = (_lib.KvRangeC * max(len(ranges), 1))()
+    hd, total = None, 0
+    for i, (seq, layer, t0, n) in enumerate(ranges):
+        arr[i].seq, arr[i].layer, arr[i].t0, arr[i].n = seq, layer, t0, n
+        if n:
+            hd = _head_dim(kv, layer) if hd is None else hd
+            total += n * kv.kv_heads * hd
+    return arr, total
+
+
+def kv_gather_batch(kv: KvPool, ranges: Sequence[Sequence[int]], k_dst, v_dst, stream=None) -> None:
+    """kv_gather of many (seq, layer, t0, n) ranges in one launch; range i
+    lands after ranges 0..i-1, each [kv_heads, n_i, head_dim] (no reference
+    counterpart)."""
+    arr, total = _ranges_c(kv, ranges)
+    _buf("k_dst", k_dst, total, _HALF)
+    _buf("v_dst", v_dst, total, _HALF)
+    check(lib().thb_kv_gather_batch(kv.handle, arr, len(ranges), _addr("k_dst", k_dst), _addr("v_dst", v_dst),
+                                    _stream_ptr(stream)))
+
+
+def kv_scatter_batch(kv: KvPool, ranges: Sequence[Sequence[int]], k_src, v_src, stream=None) -> None:
+    """Inverse of kv_gather_batch (no reference counterpart)."""
+    arr, total = _ranges_c(kv, ranges)
+    _buf("k_src", k_src, total, _HALF)
+    _buf("v_src", v_src, total, _HALF)
+    check(lib().thb_kv_scatter_batch(kv.handle, arr, len(ranges), _addr("k_src", k_src), _addr("v_src", v_src),
+                                     _stream_ptr(stream)))
+
+
 def check_gemm_dims(pairs: Sequence[Sequence[int]]) -> None:
     """ops::check_gemm_dims (crates/thuban_model/src/ops/gemm.rs:133-146):
     every (N, K) pair needs N % 16 == 0 and K % 64 == 0 (ThubanError kind
@@ -246,4 +277,5 @@ def block_copy(kv: KvPool, triples: Sequence[Sequence[int]], stream=None) -> Non
 
 
 __all__ = ["AttnSpec", "ThubanError", "attn", "attn_step", "block_copy", "check_gemm_dims", "check_head_dim",
-           "default_scale", "gemm_acc", "kv_gather", "kv_scatter", "kv_store", "kv_store_attn"]
+           "default_scale", "gemm_acc", "kv_gather", "kv_gather_batch", "kv_scatter", "kv_scatter_batch", "kv_store",
+           "kv_store_attn"]

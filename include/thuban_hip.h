@@ -402,9 +402,33 @@ int thb_kv_gather(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uin
                   void* v_dst_dev, void* stream);
 
 /* No reference counterpart.  Inverse of thb_kv_gather: writes contiguous
- * [kv_heads, n, head_dim] words (KV type) into tokens [t0, t0 + n) of seq. */
+ * [kv_heads, n, head_dim] words (KV type) into tokens [t0, t0 + n) of seq.
+ * Writes in place, so a page the sequence shares with another (after
+ * thb_pool_fork) is refused with THB_ERR_MODEL. */
 int thb_kv_scatter(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t t0, uint32_t n, const void* k_src_dev,
                    const void* v_src_dev, void* stream);
+
+/* One range of a batched gather or scatter: tokens [t0, t0 + n) of seq in
+ * layer `layer`. */
+typedef struct thb_kv_range {
+    uint32_t seq;
+    uint32_t layer;
+    uint32_t t0;
+    uint32_t n;
+} thb_kv_range;
+
+/* No reference counterpart.  thb_kv_gather of `count` ranges in one launch:
+ * range i lands in k_dst / v_dst at element offset sum_{j < i} kv_heads *
+ * n_j * head_dim, laid out [kv_heads, n_i, head_dim].  The ranges' layers
+ * share one head_dim. */
+int thb_kv_gather_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t count, void* k_dst_dev,
+                        void* v_dst_dev, void* stream);
+/* No reference counterpart.  The inverse of thb_kv_gather_batch.  Like
+ * thb_kv_scatter, pages shared with another sequence are refused
+ * (THB_ERR_MODEL), and so are ranges of one sequence and layer that overlap
+ * (THB_ERR_INVALID). */
+int thb_kv_scatter_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t count, const void* k_src_dev,
+                         const void* v_src_dev, void* stream);
 
 /* No reference counterpart.  For each host triple (src_page, dst_page,
  * tokens) copies slots [0, tokens) of src_page to dst_page, K and V, every

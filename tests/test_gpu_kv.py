@@ -362,3 +362,60 @@ def test_block_copy_partial_pages_bit_exact(torch_cuda, page_len):
         want[layer].block_copy(triples)
         k2, v2 = pool.read_layer(layer)
         assert np.array_equal(k2, want[layer].k) and np.array_equal(v2, want[layer].v), layer
+
+
+@pytest.mark.parametrize("page_len,hd", [(16, 128), (8, 64), (32, 80)])
+def test_batched_gather_and_scatter(torch_cuda, page_len, hd):
+    """thb_kv_gather_batch over ranges of several sequences and layers (whole
+    pages and ranges cut at both ends, one empty range) equals the oracle's
+    gathers laid back to back; thb_kv_scatter_batch writes them back so the
+    pool is unchanged, and new words land exactly in the scattered ranges.
+    Overlapping scatter ranges and pages shared with a fork are refused."""
+    torch = torch_cuda
+    from flint_amd import ThubanError, ops
+
+    say("batched gather", page_len, hd)
+    rng = np.random.default_rng(7 * page_len + hd)
+    lens = [5 * page_len + 3, 2 * page_len, 7 * page_len - 1, 40]
+    pool = make_pool(lens, kv_heads=2, head_dim=hd, page_len=page_len, kv_dtype="f16", layers=2, extra_pages=8)
+    scattered_alloc(pool, lens, random.Random(page_len), page_len)
+    info = pool.layer_info(0)
+    refs = []
+    for layer in range(2):
+        k = rng.integers(0, 1 << 16, size=(2, info.pool_len, hd), dtype=np.uint16)
+        v = rng.integers(0, 1 << 16, size=(2, info.pool_len, hd), dtype=np.uint16)
+        pool.write_layer(layer, k, v)
+        refs.append(oracle.Layer(2, hd, pool.arena.pages(), page_len, np.array(pool.arena.table(), np.uint32),
+                                 pool.arena.max_pages(), oracle.KV_F16, k=k, v=v))
+    ranges = [(0, 0, 0, lens[0]), (2, 1, 3, lens[2] - 5), (1, 1, page_len - 2, 5), (3, 0, 7, 0), (3, 1, 0, 40),
+              (2, 0, page_len, page_len)]
+    total = sum(n for *_, n in ranges) * 2 * hd
+    kd = torch.empty(total, dtype=torch.int16, device="cuda")
+    vd = torch.empty_like(kd)
+    ops.kv_gather_batch(pool, ranges, kd, vd)
+    torch.cuda.synchronize()
+    kh, vh = kd.cpu().numpy().view(np.uint16), vd.cpu().numpy().view(np.uint16)
+    off = 0
+    for seq, layer, t0, n in ranges:
+        rk, rv = refs[layer].gather(seq, t0, n)
+        assert np.array_equal(kh[off:off + rk.size].reshape(rk.shape), rk), (seq, layer, t0, n)
+        assert np.array_equal(vh[off:off + rv.size].reshape(rv.shape), rv), (seq, layer, t0, n)
+        off += rk.size
+    # scatter new words into the ranges (the empty and the overlapping-free set)
+    new_k = torch.from_numpy(rng.integers(0, 1 << 16, size=total, dtype=np.uint16).view(np.int16)).cuda()
+    new_v = torch.from_numpy(rng.integers(0, 1 << 16, size=total, dtype=np.uint16).view(np.int16)).cuda()
+    ops.kv_scatter_batch(pool, ranges, new_k, new_v)
+    k2 = torch.empty_like(kd)
+    v2 = torch.empty_like(vd)
+    ops.kv_gather_batch(pool, ranges, k2, v2)
+    torch.cuda.synchronize()
+    assert torch.equal(k2, new_k) and torch.equal(v2, new_v)
+    # tokens outside the ranges are untouched: seq 1 token 0 of layer 1
+    k1 = torch.empty(2, 1, hd, dtype=torch.int16, device="cuda")
+    v1 = torch.empty_like(k1)
+    ops.kv_gather(pool, 1, 1, 0, 1, k1, v1)
+    torch.cuda.synchronize()
+    assert np.array_equal(k1.cpu().numpy().view(np.uint16), refs[1].gather(1, 0, 1)[0])
+    with pytest.raises(ThubanError) as e:
+        ops.kv_scatter_batch(pool, [(0, 0, 0, 10), (0, 0, 5, 10)], new_k, new_v)
+    assert "overlap" in str(e.value)
