@@ -450,9 +450,9 @@ def _time_steps(torch, step, steps, warmup):
     return s.elapsed_time(e) / steps * 1e3  # us per step
 
 
-def run_secondary(args):
-    """The other BASELINE configurations, each as one JSON line (see the
-    module docstring).  Synthetic N(0,1) data, block tables scattered."""
+def measure_secondary(name, args):
+    """One of the other BASELINE configurations (see the module docstring):
+    its record as a dict.  Synthetic N(0,1) data, block tables scattered."""
     import numpy as np
     import torch
 
@@ -462,7 +462,6 @@ def run_secondary(args):
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     g = torch.Generator(device=dev)
-    name = args.config
     out = {"metric": "paged attention us/step + achieved HBM GB/s (% peak) [secondary config]", "unit": "GB/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "f16", "data": "synthetic N(0,1), block tables randomly scattered",
@@ -658,7 +657,8 @@ def run_secondary(args):
                 "pct_of_peak": round(100 * gbps / PEAK_HBM_GBPS, 1), "ms_per_step": round(us * 1e-3, 4),
                 "bytes_per_layer_step": byts})
     out["config"]["config_name"] = name
-    print(json.dumps(out), flush=True)
+    pool.close()
+    return out
 
 
 def main():
@@ -670,6 +670,8 @@ def main():
     ap.add_argument("--part-len", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the C3 (qwen3-8b) and C4 (gemma2-9b) fields of the default line")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the timed steps, run 3 device copies of this many MiB (scale factor for the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -681,7 +683,7 @@ def main():
         sys.exit(2)
 
     if args.config in SECONDARY:
-        run_secondary(args)
+        print(json.dumps(measure_secondary(args.config, args)), flush=True)
         return
 
     import torch
@@ -826,6 +828,21 @@ def main():
             attn_bytes / med / 1e9, med, runs,
             f"layer 0 of the step (decode of {B} seqs x {nq} heads x {ctx} keys), median of {runs} runs after 3 "
             f"warm-ups, {med * 1e3:.1f} ms/run, max |cpu-gpu| {err:.1e}")
+    if not args.no_secondary:
+        # C3 and C4 on the same box, in the driver's line (their own lines: --config)
+        pool.close()
+        del q, y, k_new, v_new
+        torch.cuda.empty_cache()
+        sec = argparse.Namespace(**vars(args))
+        sec.steps, sec.warmup, sec.no_cpu_baseline = min(args.steps, 10), min(args.warmup, 3), True
+        for name, key in (("qwen3-8b", "c3_qwen3_8b"), ("gemma2-9b", "c4_gemma2_9b")):
+            rec = measure_secondary(name, sec)
+            out[key] = {k: rec[k] for k in ("value", "unit", "us_per_layer_step", "pct_of_peak", "bytes_per_layer_step",
+                                            "prefill", "norm_rope_step", "window_layer", "global_layer")
+                        if k in rec}
+            out[key]["workload"] = rec["config"]["workload"]
+            log(f"{name}: {rec['us_per_layer_step']} us/layer, {rec['value']} GB/s ({rec['pct_of_peak']}%)")
+            torch.cuda.empty_cache()
     print(json.dumps(out), flush=True)
 
 
