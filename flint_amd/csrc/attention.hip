@@ -84,6 +84,7 @@ constexpr int ring_for(int hd) { return hd >= 256 ? 1 : THB_ATTN_RING; }
 // workgroup's waves, which share the query group) instead of registers.
 constexpr bool q_in_lds(int hd) { return hd >= 512; }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -224,6 +225,21 @@ struct Ops<true> {
             l[e] = b;
         }
     }
+    // The same split (both halves rounded to nearest even), two elements per
+    // conversion: three vector instructions per element.
+    __device__ static void split8_fast(const float* x, in8& h, in8& l) {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const f16x2 hh = __builtin_convertvector((f32x2{x[e], x[e + 1]}), f16x2);
+            const f16x2 ll = __builtin_convertvector(
+                (f32x2{x[e] - static_cast<float>(hh[0]), x[e + 1] - static_cast<float>(hh[1])}), f16x2);
+            h[e] = hh[0];
+            h[e + 1] = hh[1];
+            l[e] = ll[0];
+            l[e + 1] = ll[1];
+        }
+    }
 };
 
 template <>
@@ -261,6 +277,7 @@ struct Ops<false> {
             l[e] = b;
         }
     }
+    __device__ static void split8_fast(const float* x, in8& h, in8& l) { split8(x, h, l); }
 };
 
 // One scalar of the sigmoid gate (same type as the query).
@@ -1189,6 +1206,9 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
     }
 
     // This wave's two column groups; [wlo, whi) spans both groups' keys.
+    // Each column's key range is requested here and used after the first
+    // tile's loads and the queries' loads are out, so the three round trips
+    // overlap.
     bool con[NCG];
     uint32_t row[NCG], head[NCG], clo[NCG], chi[NCG], cspan[NCG], item0[NCG];
     uint32_t wlo = 0xFFFFFFFFu, whi = 0;
@@ -1204,12 +1224,8 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
         const uint32_t rr = con[g] ? c / H : 0u;
         row[g] = r0 + rr;
         head[g] = kvh * a.nq_per_kv + h0 + (con[g] ? c - rr * H : 0u);
-        clo[g] = chi[g] = 0;
-        if (con[g]) {
-            clo[g] = max(a.ranges[2 * row[g]], tb);
-            chi[g] = min(a.ranges[2 * row[g] + 1], te);
-        }
-        cspan[g] = chi[g] > clo[g] ? chi[g] - clo[g] : 0u;  // key t is read iff t - clo < cspan
+        clo[g] = a.ranges[2 * row[g]];  // row r0 of an unused column: a valid index
+        chi[g] = a.ranges[2 * row[g] + 1];
         if (gon) {
             const uint32_t glo = max(G[5], tb), ghi = min(G[6], te);
             if (glo < ghi) {
@@ -1221,25 +1237,68 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
     // Per group, the keys every column reads: a 32-key step inside
     // [lomax, himin) needs no mask.
     uint32_t lomax[NCG], himin[NCG];
+    auto column_ranges = [&]() {
 #pragma unroll
-    for (int g = 0; g < NCG; g++) {
-        uint32_t lo = con[g] ? clo[g] : 0u, hi = con[g] ? chi[g] : 0xFFFFFFFFu;
+        for (int g = 0; g < NCG; g++) {
+            clo[g] = con[g] ? max(clo[g], tb) : 0u;
+            chi[g] = con[g] ? min(chi[g], te) : 0u;
+            cspan[g] = chi[g] > clo[g] ? chi[g] - clo[g] : 0u;  // key t is read iff t - clo < cspan
+            uint32_t lo = con[g] ? clo[g] : 0u, hi = con[g] ? chi[g] : 0xFFFFFFFFu;
 #pragma unroll
-        for (int sh = 1; sh < 64; sh <<= 1) {
-            lo = max(lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo), sh)));
-            hi = min(hi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi), sh)));
+            for (int sh = 1; sh < 64; sh <<= 1) {
+                lo = max(lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo), sh)));
+                hi = min(hi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi), sh)));
+            }
+            lomax[g] = __builtin_amdgcn_readfirstlane(lo);
+            himin[g] = __builtin_amdgcn_readfirstlane(hi);
         }
-        lomax[g] = __builtin_amdgcn_readfirstlane(lo);
-        himin[g] = __builtin_amdgcn_readfirstlane(hi);
-    }
+    };
     in8 qh[NCG][KS], ql[NCG][KS];
 
     const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
     const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
 
     // Global -> registers for one tile; tokens outside [tb, te) are clamped
-    // into it (their scores are masked).
+    // into it (their scores are masked).  At the template's own head_dim
+    // every unit is in range: the page numbers of all units are read from
+    // LDS first (one round trip), then every load is issued, with no guards.
     auto load = [&](uint32_t t0, u32x4 (&kr)[KPT], u32x4 (&vr)[VPT][2]) {
+        if constexpr (KU % NT == 0 && VP % NT == 0) {
+            if (hd == static_cast<uint32_t>(HD)) {
+                uint32_t kpg[KPT], kin[KPT], vpg[VPT][2], vin[VPT][2];
+#pragma unroll
+                for (int k = 0; k < KPT; k++) {
+                    const uint32_t u = tid + k * NT;
+                    const uint32_t st = u / (16 * CPH), rem = u - st * (16 * CPH);
+                    const uint32_t ch = rem >> 4, tok = rem & 15u;
+                    const uint32_t t = min(max(t0 + 16u * st + tok, tb), last);
+                    kpg[k] = s_page[(t - pbeg) >> pshift];
+                    kin[k] = ((8u * ch & ~31u) << pshift) + 32u * (t & pmask) + (8u * ch & 31u);
+                }
+#pragma unroll
+                for (int k = 0; k < VPT; k++) {
+                    const uint32_t u = tid + k * NT;
+                    const uint32_t st = u / (4 * (HD / 2)), rem = u - st * (4 * (HD / 2));
+                    const uint32_t ag = rem / (HD / 2), d = 2u * (rem - ag * (HD / 2));
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const uint32_t t = min(max(t0 + 32u * st + 16u * h + 4u * ag, tb & ~3u), last & ~3u);
+                        vpg[k][h] = s_page[(t - pbeg) >> pshift];
+                        vin[k][h] = ((t & pmask) >> 2) * (4u * HD) + 4u * d;
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < KPT; k++)
+                    kr[k] = *reinterpret_cast<const u32x4*>(kplane + ((static_cast<uint64_t>(kpg[k]) * HD) << pshift) + kin[k]);
+#pragma unroll
+                for (int k = 0; k < VPT; k++)
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+                        vr[k][h] = *reinterpret_cast<const u32x4*>(vplane + ((static_cast<uint64_t>(vpg[k][h]) * HD) << pshift) +
+                                                                 vin[k][h]);
+                return;
+            }
+        }
 #pragma unroll
         for (int k = 0; k < KPT; k++) {
             const uint32_t u = tid + k * NT;
@@ -1303,7 +1362,14 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
     {
         const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;
         ones = u32x4{one2, one2, one2, one2};
+        asm volatile("" : "+v"(ones));  // held in registers, not rebuilt before every use
     }
+    // Lazy-rescale thresholds, in the units of the scores x (m + kTau, over
+    // qpost without a cap).
+    const float inv_qpost = 1.0f / a.qpost;
+    float thr[NCG];
+#pragma unroll
+    for (int g = 0; g < NCG; g++) thr[g] = CAP ? m[g] + kTau : (m[g] + kTau) * inv_qpost;
 
     // 32-key steps, software-pipelined: the QK^T products of step s + 1 are
     // issued before the softmax of step s, so the matrix cores work on them
@@ -1336,6 +1402,20 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
     };
     auto softmax_pv = [&](int buf, int st, uint32_t ts, const f32x4 (&sc)[NCG][2]) {
         in8 ph[NCG], pl[NCG];
+        // Without the query's low half (the lean f16 kernel, whose registers
+        // allow it) the step's V operands are requested before the softmax,
+        // whose vector work covers their LDS latency; the other kernels read
+        // them pair by pair beside the products.
+        constexpr bool VPRE = !FULL && !QLO;
+        auto vread = [&](int i) {
+            const uint32_t d = 16u * i + c;
+            return s_v[buf][(st * HD + d) * 4 + (a4 ^ ((d >> 2) & 3u))];
+        };
+        u32x4 vop[VPRE ? MT : 1];
+        if constexpr (VPRE) {
+#pragma unroll
+            for (int i = 0; i < MT; i++) vop[i] = vread(i);
+        }
 #pragma unroll
         for (int g = 0; g < NCG; g++) {
             float x[8];
@@ -1360,9 +1440,15 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
             // The column max (two cross-lane steps) is needed only when some
             // score beats its column's running max by more than kTau; without
             // one, no column rescales, exactly as if the max had been taken.
-            float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-            if constexpr (!CAP) mx *= a.qpost;  // log2 units (qpost > 0)
-            if (__builtin_amdgcn_ballot_w64(mx > m[g] + kTau) != 0) {  // wave-uniform
+            // The test compares each score with the column's threshold
+            // (m + kTau in score units, kept with m): eight compares whose
+            // lane masks the scalar unit ORs, instead of a max tree.
+            uint64_t hit = 0;  // lanes with a score above the threshold (2: ordered >)
+#pragma unroll
+            for (int e = 0; e < 8; e++) hit |= __builtin_amdgcn_fcmpf(x[e], thr[g], 2);
+            if (hit != 0) {  // wave-uniform
+                float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+                if constexpr (!CAP) mx *= a.qpost;  // log2 units (qpost > 0)
                 mx = col_max(mx);
                 if (mx > m[g] + kTau) {
                     const float alpha = fast_exp2(m[g] - mx);
@@ -1370,6 +1456,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
 #pragma unroll
                     for (int i = 0; i < MT; i++) o[g][i] *= alpha;
                     m[g] = mx;
+                    thr[g] = CAP ? mx + kTau : (mx + kTau) * inv_qpost;
                 }
             }
             float p[8];
@@ -1378,15 +1465,17 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
             // High and low halves, as in the decode kernels: one f16 operand
             // alone (relative error 2^-12) measured 1e-4 .. 5e-4 against the
             // exact softmax on N(0,1) .. N(0,4) data, both halves 3e-7.
-            O::split8(p, ph[g], pl[g]);
+            O::split8_fast(p, ph[g], pl[g]);
         }
 #pragma unroll
         for (int i = 0; i < MT; i += 2) {
             u32x4 vv[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t d = 16u * (i + u) + c;
-                vv[u] = s_v[buf][(st * HD + d) * 4 + (a4 ^ ((d >> 2) & 3u))];
+                if constexpr (VPRE)
+                    vv[u] = vop[i + u];
+                else
+                    vv[u] = vread(i + u);
             }
 #pragma unroll
             for (int u = 0; u < 2; u++)
@@ -1428,6 +1517,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
         // in flight (their round trips overlap).
 #pragma unroll
         for (int g = 0; g < NCG; g++) load_q<KS, O, FULL>(a, con[g], row[g], head[g], a4, qh[g], ql[g], a.qpre);
+        column_ranges();
         if (n_tiles) store(0, kr, vr);
         __syncthreads();
         for (uint32_t i = 0; i < n_tiles; i++) {
