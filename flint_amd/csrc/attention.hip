@@ -59,6 +59,7 @@ constexpr uint32_t kGroupWords = 11;  // r0, R, h0, H, seq, lo, hi, n_parts, bas
 constexpr uint32_t kMaxPartPages = 1024;
 constexpr uint32_t kMaxParts = 512;   // partitions of one group the merge kernel takes
 constexpr uint32_t kCols = 16;        // query vectors per group (MFMA N)
+constexpr uint32_t kMergeWords = 8;   // merge record: r0, R, h0, H, n_parts, item0, 0, 0
 constexpr uint32_t kBlockWords = 9;   // g0, ng, seq, lo, hi, n_parts, base, plen, bitem0
 // Work-item records carry their group's (or block's) words and the
 // partition index, so a workgroup finds its work in one dependent load.
@@ -834,69 +835,64 @@ __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
 // workgroups.
 template <int HD, bool FULL>
 __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
-    __shared__ float s_w[kMaxParts * kCols];
-    __shared__ float s_inv[kCols];
-    const uint32_t g = a.merge_groups[blockIdx.x], kvh = blockIdx.y, tid = threadIdx.x;
-    const uint32_t* G = a.groups + g * kGroupWords;
-    const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3];
-    const uint32_t n_parts = G[7], item0 = G[10];
-    if (n_parts <= 1) return;
-    const uint32_t ncols = R * H;
-    const uint32_t hd = a.head_dim;
+    // Merge record (kMergeWords): the group's r0, R, h0, H, n_parts, item0,
+    // so the partials are requested one round trip after the launch.
+    const uint32_t* E = a.merge_groups + static_cast<uint64_t>(blockIdx.x) * kMergeWords;
+    const uint32_t kvh = blockIdx.y, tid = threadIdx.x;
+    const uint32_t r0 = E[0], R = E[1], h0 = E[2], H = E[3], n_parts = E[4], item0 = E[5];
+    const uint32_t ncols = R * H, hd = a.head_dim, q4 = hd >> 2;
     const uint64_t base = static_cast<uint64_t>(item0) * a.n_kvh + kvh;  // partition pi: base + pi * n_kvh
-    // Partitions are read eight at a time, all eight loads issued before the
-    // first is used (one round trip per eight partitions, not one each); the
-    // sums still run in partition order.
-    constexpr uint32_t U = 8;
-    if (tid < ncols) {
-        const uint64_t mstep = 2 * static_cast<uint64_t>(a.n_kvh) * kCols;
-        const float* ml = a.part_ml + 2 * (base * kCols + tid);
+    const uint64_t mstep = 2 * static_cast<uint64_t>(a.n_kvh) * kCols;   // (m, l) of the next partition
+    const uint64_t ostep = static_cast<uint64_t>(a.n_kvh) * kCols * HD;  // o of the next partition
+    // Each thread owns 4-dimension units of the group's outputs (unit u:
+    // column u / q4, dims 4 (u % q4) .. + 4) and reads its column's (m, l)
+    // itself.  Up to U partitions are requested at once, (m, l) and o
+    // together; the sums run in partition order.
+    constexpr uint32_t U = 8, NU = (kCols * HD / 4 + 255) / 256;
+    for (uint32_t u0 = 0; u0 < NU; u0++) {
+        const uint32_t u = tid + 256u * u0;
+        if (u >= ncols * q4) break;
+        const uint32_t c = u / q4, d = 4u * (u - c * q4);
+        const float* ml = a.part_ml + 2 * (base * kCols + c);
+        const f32x4* op = reinterpret_cast<const f32x4*>(a.part_o + (base * kCols + c) * HD + d);
         float M = kFloor;
-        for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
-            float mv[U];
+        if (n_parts > U) {  // long merges: the maximum first
+            for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
+                float mv[U];
 #pragma unroll
-            for (uint32_t u = 0; u < U; u++) mv[u] = p0 + u < n_parts ? ml[(p0 + u) * mstep] : kFloor;
+                for (uint32_t k = 0; k < U; k++) mv[k] = p0 + k < n_parts ? ml[(p0 + k) * mstep] : kFloor;
 #pragma unroll
-            for (uint32_t u = 0; u < U; u++) M = fmaxf(M, mv[u]);
+                for (uint32_t k = 0; k < U; k++) M = fmaxf(M, mv[k]);
+            }
         }
         float L = 0.0f;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
         for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
             float mv[U], lv[U];
+            f32x4 ov[U];
 #pragma unroll
-            for (uint32_t u = 0; u < U; u++) {
-                const bool in = p0 + u < n_parts;
-                mv[u] = in ? ml[(p0 + u) * mstep] : kFloor;
-                lv[u] = in ? ml[(p0 + u) * mstep + 1] : 0.0f;
+            for (uint32_t k = 0; k < U; k++) {
+                const bool in = p0 + k < n_parts;
+                mv[k] = in ? ml[(p0 + k) * mstep] : kFloor;
+                lv[k] = in ? ml[(p0 + k) * mstep + 1] : 0.0f;
+                ov[k] = in ? op[(p0 + k) * ostep / 4] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            if (n_parts <= U) {
+#pragma unroll
+                for (uint32_t k = 0; k < U; k++) M = fmaxf(M, mv[k]);
             }
 #pragma unroll
-            for (uint32_t u = 0; u < U; u++) {
-                if (p0 + u >= n_parts) break;
-                const float w = fast_exp2(mv[u] - M);
-                s_w[(p0 + u) * kCols + tid] = w;
-                L += w * lv[u];
-            }
-        }
-        s_inv[tid] = 1.0f / L;
-    }
-    __syncthreads();
-    const uint64_t step = static_cast<uint64_t>(a.n_kvh) * kCols * HD;
-    for (uint32_t idx = tid; idx < ncols * hd; idx += 256) {
-        const uint32_t c = idx / hd, d = idx - c * hd;
-        const float* src = a.part_o + (base * kCols + c) * HD + d;
-        float acc = 0.0f;
-        for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
-            float ov[U];
-#pragma unroll
-            for (uint32_t u = 0; u < U; u++) ov[u] = p0 + u < n_parts ? src[(p0 + u) * step] : 0.0f;
-#pragma unroll
-            for (uint32_t u = 0; u < U; u++) {
-                if (p0 + u >= n_parts) break;
-                acc += s_w[(p0 + u) * kCols + c] * ov[u];
+            for (uint32_t k = 0; k < U; k++) {
+                if (p0 + k >= n_parts) break;
+                const float w = fast_exp2(mv[k] - M);
+                L += w * lv[k];
+                acc += w * ov[k];
             }
         }
-        const float yv[1] = {acc * s_inv[c]};
+        const float inv = 1.0f / L;
+        const float yv[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
         const uint32_t rr = c / H, hh = c - rr * H;
-        store_y<1, FULL>(a, r0 + rr, kvh * a.nq_per_kv + h0 + hh, d, yv);
+        store_y<4, FULL>(a, r0 + rr, kvh * a.nq_per_kv + h0 + hh, d, yv);
     }
 }
 
@@ -1983,9 +1979,11 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     }
     // The groups the merge kernel combines (more than one partition).
     const size_t merge_off = blob.size();
-    for (uint32_t gi = 0; gi < n_groups; gi++)
-        if (groups[static_cast<size_t>(gi) * kGroupWords + 7] > 1) blob.push_back(gi);
-    const uint32_t n_merge = static_cast<uint32_t>(blob.size() - merge_off);
+    for (uint32_t gi = 0; gi < n_groups; gi++) {
+        const uint32_t* G = groups.data() + static_cast<size_t>(gi) * kGroupWords;
+        if (G[7] > 1) blob.insert(blob.end(), {G[0], G[1], G[2], G[3], G[7], G[10], 0u, 0u});
+    }
+    const uint32_t n_merge = static_cast<uint32_t>((blob.size() - merge_off) / kMergeWords);
     plan.blob.swap(blob);
     plan.uploaded = false;
     plan.n_groups = n_groups;
