@@ -79,8 +79,17 @@ constexpr uint32_t kBItemWords = kBlockWords + 1;
 #ifndef THB_ATTN_RING
 #define THB_ATTN_RING 2
 #endif
+#ifndef THB_ATTN_WAVES_256
+#define THB_ATTN_WAVES_256 8
+#endif
+#ifndef THB_ATTN_RING_256
+#define THB_ATTN_RING_256 1
+#endif
 constexpr int waves_for(int hd) { return hd >= 512 ? 4 : THB_ATTN_WAVES; }
-constexpr int ring_for(int hd) { return hd >= 256 ? 1 : THB_ATTN_RING; }
+constexpr int ring_for(int hd) { return hd >= 512 ? 1 : hd >= 256 ? THB_ATTN_RING_256 : THB_ATTN_RING; }
+// Decode workgroups: head_dim 256 has its own wave count (fewer waves hold
+// more tiles in flight each).
+constexpr int decode_waves(int hd) { return hd == 256 ? THB_ATTN_WAVES_256 : waves_for(hd); }
 // Decode keeps the query's high and low halves in LDS (one copy for the
 // workgroup's waves, which share the query group) instead of registers.
 constexpr bool q_in_lds(int hd) { return hd >= 512; }
@@ -633,7 +642,7 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     // pages hold 4-slot groups ([page_len/4][hd][4]): a lane's 4 slots of one
     // dim are 8 bytes, and 16 lanes read 128 contiguous bytes.  The loads are
     // non-temporal: every byte is read once.
-    auto load = [&](uint32_t t0, u32x4 (&kr)[KS], u32x2 (&vr)[MT]) {
+    auto load_k = [&](uint32_t t0, u32x4 (&kr)[KS]) {
         const uint32_t tk = min(max(t0 + c, tb), last);
         const uint32_t kpage = s_page[(tk - pbeg) >> pshift];
         const uint16_t* kbase = kplane + (static_cast<uint64_t>(kpage) * hd << pshift);
@@ -644,6 +653,8 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
                                   reinterpret_cast<const u32x4*>(kbase + k_off(tk & pmask, d0, hd, pshift)))
                             : u32x4{0u, 0u, 0u, 0u};
         }
+    };
+    auto load_v = [&](uint32_t t0, u32x2 (&vr)[MT]) {
         const uint32_t tv = min(max(t0 + 4u * a4, tb & ~3u), last & ~3u);
         const uint32_t vpage = s_page[(tv - pbeg) >> pshift];
         const uint16_t* vbase = vplane + (static_cast<uint64_t>(vpage) * hd << pshift) + v_off(tv & pmask, 0, hd);
@@ -654,8 +665,15 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
                            : u32x2{0u, 0u};
         }
     };
+    auto load = [&](uint32_t t0, u32x4 (&kr)[KS], u32x2 (&vr)[MT]) {
+        load_k(t0, kr);
+        load_v(t0, vr);
+    };
 
-    auto compute = [&](uint32_t t0, const u32x4 (&kr)[KS], const u32x2 (&vr)[MT]) {
+    // after_qk runs once the tile's K operands are consumed (one tile in
+    // flight: the next tile's K is requested there, before the softmax and
+    // the PV products of this one).
+    auto compute = [&](uint32_t t0, const u32x4 (&kr)[KS], const u32x2 (&vr)[MT], auto&& after_qk) {
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < KS; j++) {
@@ -667,6 +685,7 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
                 s = O::qk(kr[j], ql[j], s);
             }
         }
+        after_qk();
         float sv[4];
         float mx = -INFINITY;
 #pragma unroll
@@ -717,18 +736,33 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
             for (int b = 0; b < NB; b++) {
                 const uint32_t t = t0 + 16u * b;
                 if (t < we) {
-                    compute(t, kr[b], vr[b]);
                     const uint32_t tn = t + 16u * NB;
-                    if (tn < we) {
-                        // The token lies beyond tile NB of this wave: it is
-                        // stored just before the load of its own tile, so
-                        // only the waits for that tile (whose load latency
-                        // covers the store's) also wait for the store.
+                    // The token lies beyond tile NB of this wave: it is
+                    // stored just before the load of its own tile, so only
+                    // the waits for that tile (whose load latency covers
+                    // the store's) also wait for the store.
+                    auto store_late = [&]() {
                         if (app_late && app_pos - tn < 16u) {
                             app_store(app_pos, app_v, app_d, app_w);
                             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
                         }
-                        load(tn, kr[b], vr[b]);
+                    };
+                    if constexpr (NB == 1) {
+                        // One tile in flight: the next tile's K goes out as soon
+                        // as this tile's K is consumed, its V after the PV.
+                        compute(t, kr[b], vr[b], [&]() {
+                            if (tn < we) {
+                                store_late();
+                                load_k(tn, kr[b]);
+                            }
+                        });
+                        if (tn < we) load_v(tn, vr[b]);
+                    } else {
+                        compute(t, kr[b], vr[b], []() {});
+                        if (tn < we) {
+                            store_late();
+                            load(tn, kr[b], vr[b]);
+                        }
                     }
                 }
             }
@@ -1581,7 +1615,7 @@ uint32_t template_hd(uint32_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : hd 
 
 template <int HD, bool F16>
 void launch_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
-    constexpr int W = waves_for(HD);
+    constexpr int W = decode_waves(HD);
     if (a.full)
         hipLaunchKernelGGL((attn_mfma<HD, F16, W, ring_for(HD), true>), grid, dim3(64 * W), 0, s, a);
     else
