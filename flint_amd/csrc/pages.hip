@@ -35,7 +35,10 @@ namespace {
 enum : uint32_t { kStOk = 0, kStLimit = 1, kStExhausted = 2, kStForkTarget = 3, kStForkCover = 4, kStBadSeq = 5 };
 enum : uint32_t { kHdrTop = 0, kHdrStatus = 1, kHdrA = 2, kHdrB = 3, kHdrC = 4, kHdrCopies = 5, kHdrWords = 64 };
 
-constexpr uint32_t kOpsPerLaunch = 16;  // page ops passed in one launch's arguments
+constexpr uint32_t kOpsPerLaunch = 64;  // page ops passed in one launch's arguments
+// Set on an alloc op that runs in one batch with the alloc op before it
+// (consecutive allocs of distinct sequences in one launch).
+constexpr uint32_t kOpBatched = 0x100u;
 constexpr uint32_t kT = 1024;           // threads of the page-op workgroup
 constexpr uint32_t kNone = 0xFFFFFFFFu;
 
@@ -402,18 +405,25 @@ __global__ __launch_bounds__(kT) void page_ops_kernel(PageOpArgs a) {
         L.ncopy = a.reset_copies ? 0u : st.hdr[kHdrCopies];
     }
     __syncthreads();
-    for (uint32_t o = 0; o < a.n_ops; o++) {
-        const uint32_t kind = a.ops[4 * o], x = a.ops[4 * o + 1], y = a.ops[4 * o + 2], z = a.ops[4 * o + 3];
+    for (uint32_t o = 0; o < a.n_ops;) {
+        const uint32_t kind = a.ops[4 * o] & 0xFFu, x = a.ops[4 * o + 1], y = a.ops[4 * o + 2], z = a.ops[4 * o + 3];
+        uint32_t next = o + 1;
         switch (kind) {
-            case kPageOpAlloc:
-                if (threadIdx.x == 0) {
-                    L.seq[0] = x;
-                    L.pos[0] = y;
-                    L.tok[0] = z;
+            case kPageOpAlloc: {
+                // A batch of allocs of distinct sequences: one alloc_chunks
+                // over all of them, in order (the host mirror has run each
+                // call already, so none of them fails).
+                while (next < a.n_ops && (a.ops[4 * next] & kOpBatched)) next++;
+                const uint32_t n = next - o, t = threadIdx.x;
+                if (t < n) {
+                    L.seq[t] = a.ops[4 * (o + t) + 1];
+                    L.pos[t] = a.ops[4 * (o + t) + 2];
+                    L.tok[t] = a.ops[4 * (o + t) + 3];
                 }
                 __syncthreads();
-                alloc_chunks(st, 1, L);
+                alloc_chunks(st, n, L);
                 break;
+            }
             case kPageOpAllocRows: alloc_rows(st, a.meta, x, L); break;
             case kPageOpFree: release(st, x, kNone, L); break;
             case kPageOpTruncate: release(st, x, y, L); break;
@@ -421,6 +431,7 @@ __global__ __launch_bounds__(kT) void page_ops_kernel(PageOpArgs a) {
             default: break;
         }
         __syncthreads();
+        o = next;
     }
     if (threadIdx.x == 0) {
         st.hdr[kHdrTop] = L.top;
@@ -511,9 +522,20 @@ void pool_flush(thb_pool* p, hipStream_t stream) {
             PageOpArgs a = op_args(p);
             a.n_ops = static_cast<uint32_t>(std::min<size_t>(kOpsPerLaunch, i1 - k));
             a.reset_copies = k == i0;
+            std::vector<uint32_t> batch;  // sequences of the alloc batch being formed
             for (uint32_t o = 0; o < a.n_ops; o++) {
                 const PageOp& op = ops[k + o];
-                a.ops[4 * o] = op.kind;
+                uint32_t kind = op.kind;
+                if (kind == kPageOpAlloc) {
+                    if (!batch.empty() && std::find(batch.begin(), batch.end(), op.a) == batch.end())
+                        kind |= kOpBatched;
+                    else
+                        batch.clear();
+                    batch.push_back(op.a);
+                } else {
+                    batch.clear();
+                }
+                a.ops[4 * o] = kind;
                 a.ops[4 * o + 1] = op.a;
                 a.ops[4 * o + 2] = op.b;
                 a.ops[4 * o + 3] = op.c;
