@@ -137,6 +137,9 @@ FUSED_CASES = [
     ("qwen3-decode-norm", 32, 8, 128, 128, "f32", "f16", True, 1),
     ("verify4-partial-bf16", 16, 8, 128, 64, "f16", "bf16", True, 4),
     ("gemma-hd256", 16, 8, 256, 256, "f32", "f16", False, 1),
+    # 32 query heads per KV head: each row's two query groups run in two
+    # workgroups, and both rotate and store the row's key (the same bytes)
+    ("mqa32-two-groups-norm", 32, 1, 128, 128, "f16", "f16", True, 1),
     ("prefill-fallback", 8, 2, 128, 128, "f32", "f16", True, 40),
 ]
 
