@@ -41,8 +41,15 @@ _HALF = ("float16", "bfloat16", "int16")  # 16-bit words (KV types) in gather/sc
 _ACT = ("float32", "float16", "bfloat16")   # sources, queries, outputs and gates
 
 
+_NAME_OF = {}  # dtype object -> name, filled on first use
+
+
 def _dtype_name(t) -> str:
-    return str(t.dtype).replace("torch.", "")
+    dt = t.dtype
+    name = _NAME_OF.get(dt)
+    if name is None:
+        name = _NAME_OF[dt] = str(dt).replace("torch.", "")
+    return name
 
 
 def _buf(name: str, x, elems: int, dtypes, extent: Optional[int] = None):
