@@ -12,7 +12,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libthuban_hip.so")
 
-ABI_VERSION = 6  # THB_ABI_VERSION of include/thuban_hip.h
+ABI_VERSION = 7  # THB_ABI_VERSION of include/thuban_hip.h
 
 THB_OK = 0
 THB_ERR_MODEL = -1
@@ -170,6 +170,10 @@ SIGNATURES = [
     ("thb_check_gemm_dims", _int, [_u32, _u32]),
     ("thb_gemm_acc", _int, [_vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _vp]),
     ("thb_attn_noalloc", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
+    ("thb_dplan_create", _int, [_vp, _u32, _u32, ctypes.POINTER(_vp)]),
+    ("thb_dplan_destroy", None, [_vp]),
+    ("thb_dplan_build", _int, [_vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
+    ("thb_attn_dplan", _int, [_vp, _u32, _vp, _vp, _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_gather_batch", _int, [_vp, ctypes.POINTER(KvRangeC), _u32, _vp, _vp, _vp]),

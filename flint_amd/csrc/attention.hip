@@ -41,6 +41,7 @@
 //    them in partition order; there are no device-wide fences or atomics.
 #include <algorithm>
 #include <cmath>
+#include <memory>
 #include <mutex>
 #include <queue>
 #include <string>
@@ -468,6 +469,9 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     const uint32_t* G = a.items + static_cast<uint64_t>(item) * kItemWords;
     const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3], seq = G[4];
     const uint32_t glo = G[5], ghi = G[6], n_parts = G[7], gbase = G[8], P = G[9];
+    // A device-planned call's fixed grid holds slots past a group's last
+    // partition (and groups past the call's last): they do nothing.
+    if (G[kGroupWords] >= n_parts) return;
     const uint32_t pbeg = gbase + G[kGroupWords] * P;
     const uint32_t tb = max(glo, pbeg), te = min(ghi, pbeg + P);
     const uint32_t hd = a.head_dim;
@@ -874,6 +878,7 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
     const uint32_t* E = a.merge_groups + static_cast<uint64_t>(blockIdx.x) * kMergeWords;
     const uint32_t kvh = blockIdx.y, tid = threadIdx.x;
     const uint32_t r0 = E[0], R = E[1], h0 = E[2], H = E[3], n_parts = E[4], item0 = E[5];
+    if (n_parts <= 1) return;  // a device-planned call's slot of a one-partition group (or none)
     const uint32_t ncols = R * H, hd = a.head_dim, q4 = hd >> 2;
     const uint64_t base = static_cast<uint64_t>(item0) * a.n_kvh + kvh;  // partition pi: base + pi * n_kvh
     const uint64_t mstep = 2 * static_cast<uint64_t>(a.n_kvh) * kCols;   // (m, l) of the next partition
@@ -1607,6 +1612,210 @@ __global__ __launch_bounds__(64 * W, 2) void attn_mixed(AttnArgs a) {
         prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, bid);
     else
         decode_wg<HD, F16, W, ring_for(HD), FULL>(a, bid);
+}
+
+// ---------------------------------------------------- device-side planning
+// Plans a decode call on the device from the row meta in device memory, so
+// that a step can be captured in a graph once and replayed while the rows'
+// positions move (thb_dplan_*).  The rules are build_plan's: each row's key
+// range (plan_rows: kv_len per 8-row block of its chunk, window, causal), the
+// chunk's groups of up to 16 query vectors, each group's partitions (the same
+// function of its key range), so every (group, partition, KV head) computes
+// what thb_attn computes for it.  The layout differs: group g of the call
+// owns slot g of a fixed grid of gmax groups and its partition p slot
+// g * pmax + p; slots past a group's partitions or past the call's groups do
+// nothing.  Chunks of four or more groups (prefill) run as decode groups too.
+constexpr uint32_t kDPlanMaxRows = 4096;
+constexpr uint32_t kDPlanThreads = 1024;
+
+struct DPlanArgs {
+    const uint32_t* meta;  // row meta of the call's first row
+    uint32_t* blob;        // [groups gmax | items gmax * pmax | ranges 2 m | merge gmax]
+    uint32_t* state;       // device allocator state: page counts, status
+    uint32_t npages_off;
+    uint32_t m, seq_fixed, causal, window, G, PL, align, pmax, gmax, page_shift, seqs;
+    uint32_t items_off, ranges_off, merge_off;
+};
+
+// build_plan's partition of a key range [lo, hi) (lo = hi = 0 when empty).
+__device__ inline void dplan_partition(uint32_t& lo, uint32_t& hi, uint32_t PL, uint32_t align, uint32_t& base,
+                                       uint32_t& n_parts, uint32_t& plen) {
+    base = 0;
+    n_parts = 1;
+    plen = align;
+    if (hi <= lo || lo == 0xFFFFFFFFu) {
+        lo = hi = 0;
+        return;
+    }
+    base = lo & ~(align - 1);
+    const uint64_t span = uint64_t(hi) - base;
+    n_parts = static_cast<uint32_t>((span + PL - 1) / PL);
+    if (n_parts > 1) n_parts = 1u << (32 - __builtin_clz(n_parts - 1));
+    plen = static_cast<uint32_t>(((span + n_parts - 1) / n_parts + align - 1) / align * align);
+    n_parts = static_cast<uint32_t>((span + plen - 1) / plen);
+}
+
+// Inclusive sum over the workgroup; *total gets the sum.  Every thread calls it.
+__device__ uint32_t dplan_scan(uint32_t v, uint32_t* red, uint32_t* total) {
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+        const uint32_t t = __shfl_up(v, d);
+        if (lane >= d) v += t;
+    }
+    if (lane == 63) red[w] = v;
+    __syncthreads();
+    if (w == 0) {
+        uint32_t x = lane < nw ? red[lane] : 0u;
+#pragma unroll
+        for (uint32_t d = 1; d < 64; d <<= 1) {
+            const uint32_t t = __shfl_up(x, d);
+            if (lane >= d) x += t;
+        }
+        if (lane < nw) red[lane] = x;
+    }
+    __syncthreads();
+    if (w > 0) v += red[w - 1];
+    *total = red[nw - 1];
+    __syncthreads();
+    return v;
+}
+
+// First failure of the call, in the device allocator's status word
+// (thb_pool_status reports it).
+__device__ void dplan_fail(uint32_t* hdr, uint32_t code, uint32_t x, uint32_t y, uint32_t z) {
+    if (atomicCAS(&hdr[kPageHdrStatus], 0u, code) == 0u) {
+        hdr[kPageHdrStatus + 1] = x;
+        hdr[kPageHdrStatus + 2] = y;
+        hdr[kPageHdrStatus + 3] = z;
+    }
+}
+
+__global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
+    __shared__ uint32_t s_ck[kDPlanMaxRows];      // chunk of each row
+    __shared__ uint32_t s_cs[kDPlanMaxRows + 1];  // first row of each chunk, then m
+    __shared__ uint32_t s_lo[kDPlanMaxRows], s_hi[kDPlanMaxRows];
+    __shared__ uint32_t s_red[kDPlanThreads / 64];
+    __shared__ uint32_t s_carry;
+    const uint32_t tid = threadIdx.x, m = a.m;
+    const bool per_row = a.seq_fixed == THB_SEQ_PER_ROW;
+    auto seq_of = [&](uint32_t r) { return per_row ? a.meta[8u * r + 1] : a.seq_fixed; };
+
+    // Chunks: maximal runs of rows of one sequence (one chunk with a fixed seq).
+    if (tid == 0) s_carry = 0;
+    __syncthreads();
+    for (uint32_t t0 = 0; t0 < m; t0 += kDPlanThreads) {
+        const uint32_t r = t0 + tid;
+        const bool start = r < m && (r == 0 || (per_row && seq_of(r) != seq_of(r - 1)));
+        uint32_t total = 0;
+        const uint32_t incl = dplan_scan(start ? 1u : 0u, s_red, &total);
+        const uint32_t carry = s_carry;
+        if (r < m) {
+            s_ck[r] = carry + incl - 1;
+            if (start) s_cs[carry + incl - 1] = r;
+        }
+        __syncthreads();
+        if (tid == 0) s_carry = carry + total;
+        __syncthreads();
+    }
+    if (tid == 0) s_cs[s_carry] = m;
+    __syncthreads();
+
+    // Key ranges (plan_rows); a row its pages do not cover reads nothing.
+    const uint32_t* npages = a.state + a.npages_off;
+    for (uint32_t r = tid; r < m; r += kDPlanThreads) {
+        const uint32_t ck = s_ck[r], c0 = s_cs[ck], c1 = s_cs[ck + 1];
+        const uint32_t n = c1 - c0, i = r - c0, pos = a.meta[8u * r];
+        const uint32_t blk_last = min((i / 8u) * 8u + 8u, n);
+        const uint64_t kv_len =
+            a.causal ? uint64_t(a.meta[8u * (c0 + blk_last - 1)]) + 1 : uint64_t(a.meta[8u * (c1 - 1)]) + 1;
+        uint64_t ws = 0;
+        if (a.causal && a.window != 0 && uint64_t(pos) + 1 > a.window) ws = uint64_t(pos) + 1 - a.window;
+        uint64_t h = kv_len;
+        if (a.causal && uint64_t(pos) + 1 < h) h = uint64_t(pos) + 1;
+        uint32_t lo = static_cast<uint32_t>(ws), hi = static_cast<uint32_t>(min(h, uint64_t(0xFFFFFFFFu)));
+        if (hi > lo) {
+            const uint32_t seq = seq_of(r);
+            if (seq >= a.seqs) {
+                dplan_fail(a.state, kPageStBadSeq, seq, a.seqs, 0u);
+                lo = hi = 0;
+            } else if ((uint64_t(npages[seq]) << a.page_shift) < hi) {
+                dplan_fail(a.state, kPageStCover, seq, npages[seq] << a.page_shift, hi);
+                lo = hi = 0;
+            }
+        }
+        s_lo[r] = lo;
+        s_hi[r] = hi;
+        a.blob[a.ranges_off + 2u * r] = lo;
+        a.blob[a.ranges_off + 2u * r + 1] = hi;
+    }
+    __syncthreads();
+
+    // Groups: rows r0 .. r0 + R - 1 of a chunk (R <= 16 / G), or at G > 16 one
+    // row and 16 of its query heads per group; group words as build_plan's.
+    const uint32_t rg = a.G <= kCols ? kCols / a.G : 1u;
+    const uint32_t hs = a.G <= kCols ? 1u : (a.G + kCols - 1) / kCols;
+    auto write_group = [&](uint32_t g, const uint32_t (&w)[kGroupWords]) {
+#pragma unroll
+        for (uint32_t k = 0; k < kGroupWords; k++) a.blob[g * kGroupWords + k] = w[k];
+        for (uint32_t p = 0; p < a.pmax; p++) {
+            uint32_t* it = a.blob + a.items_off + (static_cast<size_t>(g) * a.pmax + p) * kItemWords;
+#pragma unroll
+            for (uint32_t k = 0; k < kGroupWords; k++) it[k] = w[k];
+            it[kGroupWords] = p;
+        }
+        uint32_t* mg = a.blob + a.merge_off + g * kMergeWords;
+        mg[0] = w[0];
+        mg[1] = w[1];
+        mg[2] = w[2];
+        mg[3] = w[3];
+        mg[4] = w[7];
+        mg[5] = w[10];
+        mg[6] = mg[7] = 0u;
+    };
+    if (tid == 0) s_carry = 0;
+    __syncthreads();
+    for (uint32_t t0 = 0; t0 < m; t0 += kDPlanThreads) {
+        const uint32_t r = t0 + tid;
+        bool head = false;
+        uint32_t c1 = 0;
+        if (r < m) {
+            const uint32_t ck = s_ck[r];
+            c1 = s_cs[ck + 1];
+            head = (r - s_cs[ck]) % rg == 0;
+        }
+        uint32_t total = 0;
+        const uint32_t incl = dplan_scan(head ? hs : 0u, s_red, &total);
+        const uint32_t carry = s_carry;
+        if (head) {
+            const uint32_t R = min(rg, c1 - r);
+            uint32_t lo = 0xFFFFFFFFu, hi = 0;
+            for (uint32_t j = r; j < r + R; j++)
+                if (s_hi[j] > s_lo[j]) {
+                    lo = min(lo, s_lo[j]);
+                    hi = max(hi, s_hi[j]);
+                }
+            uint32_t base, np, plen;
+            dplan_partition(lo, hi, a.PL, a.align, base, np, plen);
+            np = min(np, a.pmax);  // pmax covers every span the pool's sequences allow
+            for (uint32_t k = 0; k < hs; k++) {
+                const uint32_t g = carry + incl - hs + k;
+                const uint32_t h0 = k * kCols;
+                const uint32_t H = a.G <= kCols ? a.G : min(kCols, a.G - h0);
+                const uint32_t w[kGroupWords] = {r, a.G <= kCols ? R : 1u, h0, H, seq_of(r), lo, hi, np, base, plen,
+                                                 g * a.pmax};
+                write_group(g, w);
+            }
+        }
+        __syncthreads();
+        if (tid == 0) s_carry = carry + total;
+        __syncthreads();
+    }
+    // Slots past the call's groups: no partitions.
+    for (uint32_t g = s_carry + tid; g < a.gmax; g += kDPlanThreads) {
+        const uint32_t w[kGroupWords] = {0u, 1u, 0u, 1u, 0u, 0u, 0u, 0u, 0u, a.align, g * a.pmax};
+        write_group(g, w);
+    }
 }
 
 // ------------------------------------------------------------ host side
@@ -2432,3 +2641,158 @@ extern "C" int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q, v
         return THB_OK;
     });
 }
+
+// ------------------------------------------- device-planned decode calls
+struct thb_dplan {
+    thb_pool* pool = nullptr;
+    uint32_t max_m = 0, q_heads = 0, gmax = 0, pmax = 0;
+    uint32_t items_off = 0, ranges_off = 0, merge_off = 0;
+    uint32_t hd_max = 0;  // widest head_dim template of the pool's layers
+    bool built = false;
+    thb_attn_spec spec{};
+    const thb_rows* rows = nullptr;
+    thb::DevBuf blob, part;
+};
+
+namespace {
+
+// Blob layout of a device plan for calls of up to max_m rows (build_plan's
+// order: groups, items, ranges, then the merge records).
+void dplan_layout(thb_dplan* p) {
+    p->items_off = p->gmax * kGroupWords;
+    p->ranges_off = p->items_off + p->gmax * p->pmax * kItemWords;
+    p->merge_off = p->ranges_off + 2 * p->max_m;
+}
+
+// The launch-side plan of a device plan: every slot of the fixed grid.
+void dplan_shape(const thb_dplan* p, uint32_t hd, AttnPlan& a) {
+    a.n_groups = p->gmax;
+    a.n_items = p->gmax * p->pmax;
+    a.n_slots = a.n_items;
+    a.hd_t = template_hd(hd);
+    a.split = p->pmax > 1;
+    a.n_merge = p->gmax;
+    a.merge_off = p->merge_off;
+}
+
+}  // namespace
+
+extern "C" {
+
+int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan** out) {
+    if (!pool || !out) return fail(THB_ERR_INVALID, "null pool or out");
+    *out = nullptr;
+    if (max_m == 0 || max_m > kDPlanMaxRows)
+        return fail(THB_ERR_INVALID, "device-planned calls take 1 to " + std::to_string(kDPlanMaxRows) + " rows, not " +
+                                         std::to_string(max_m));
+    if (q_heads == 0 || q_heads % pool->kv_heads != 0)
+        return fail(THB_ERR_CONFIG, "q_heads " + std::to_string(q_heads) + " must be a positive multiple of kv_heads " +
+                                        std::to_string(pool->kv_heads));
+    if (pool->part_len >> pool->page_shift > kMaxPartPages)
+        return fail(THB_ERR_CONFIG, "part_len / page_len must be at most " + std::to_string(kMaxPartPages));
+    return guarded([&]() -> int {
+        auto p = std::make_unique<thb_dplan>();
+        p->pool = pool;
+        p->max_m = max_m;
+        p->q_heads = q_heads;
+        const uint32_t G = q_heads / pool->kv_heads;
+        p->gmax = G <= kCols ? max_m : max_m * ((G + kCols - 1) / kCols);
+        // Partitions of the longest key range any sequence of the pool allows
+        // (partition counts grow with the range).
+        const uint64_t span = static_cast<uint64_t>(pool->arena.a.max_pages()) << pool->page_shift;
+        uint32_t n = static_cast<uint32_t>(std::max<uint64_t>(1, (span + pool->part_len - 1) / pool->part_len));
+        if (n > 1) n = 1u << (32 - __builtin_clz(n - 1));
+        if (n > kMaxParts)
+            return fail(THB_ERR_CONFIG, "sequences of " + std::to_string(span) + " tokens exceed " +
+                                            std::to_string(kMaxParts) + " partitions of " +
+                                            std::to_string(pool->part_len) + " tokens");
+        p->pmax = n;
+        for (const auto& g : pool->geom) p->hd_max = std::max(p->hd_max, template_hd(g.head_dim));
+        dplan_layout(p.get());
+        const size_t words = static_cast<size_t>(p->merge_off) + static_cast<size_t>(p->gmax) * kMergeWords;
+        p->blob.reserve(words * 4, true);
+        AttnPlan shape;
+        dplan_shape(p.get(), p->hd_max, shape);
+        uint64_t o_bytes = 0;
+        const uint64_t pb = partial_bytes(pool, shape, &o_bytes);
+        if (pb) p->part.reserve(pb, false);
+        *out = p.release();
+        return THB_OK;
+    });
+}
+
+void thb_dplan_destroy(thb_dplan* plan) { delete plan; }
+
+int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* rows, void* stream) {
+    if (!plan || !spec || !rows) return fail(THB_ERR_INVALID, "null plan, spec or rows");
+    thb_pool* pool = plan->pool;
+    if (spec->m == 0 || spec->m > plan->max_m)
+        return fail(THB_ERR_INVALID, "the plan takes 1 to " + std::to_string(plan->max_m) + " rows, the call has " +
+                                         std::to_string(spec->m));
+    if (spec->q_heads != plan->q_heads)
+        return fail(THB_ERR_INVALID, "the plan was made for q_heads " + std::to_string(plan->q_heads) + ", not " +
+                                         std::to_string(spec->q_heads));
+    if (static_cast<uint64_t>(spec->row_off) + spec->m > rows->max_m)
+        return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(rows->max_m) + " rows, call needs " +
+                                         std::to_string(static_cast<uint64_t>(spec->row_off) + spec->m));
+    if (spec->seq != THB_SEQ_PER_ROW && spec->seq >= pool->arena.a.seqs())
+        return fail(THB_ERR_INVALID, "sequence " + std::to_string(spec->seq) + " out of range");
+    if (!(spec->softcap >= 0.0f)) return fail(THB_ERR_INVALID, "softcap must be >= 0");
+    if (spec->q_dtype > THB_DT_BF16 || spec->y_dtype > THB_DT_BF16)
+        return fail(THB_ERR_INVALID, "q_dtype and y_dtype must be THB_DT_F32, THB_DT_F16 or THB_DT_BF16");
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);  // queued page-API calls first: the plan reads the page counts
+        DPlanArgs a;
+        a.meta = rows->dev + 8 * static_cast<size_t>(spec->row_off);
+        a.blob = static_cast<uint32_t*>(plan->blob.get());
+        a.state = pool->state_dev;
+        a.npages_off = pool->state.npages_off;
+        a.m = spec->m;
+        a.seq_fixed = spec->seq;
+        a.causal = spec->causal;
+        a.window = spec->window;
+        a.G = spec->q_heads / pool->kv_heads;
+        a.PL = pool->part_len;
+        a.align = std::max<uint32_t>(pool->page_len, 16);
+        a.pmax = plan->pmax;
+        a.gmax = plan->gmax;
+        a.page_shift = pool->page_shift;
+        a.seqs = pool->arena.a.seqs();
+        a.items_off = plan->items_off;
+        a.ranges_off = plan->ranges_off;
+        a.merge_off = plan->merge_off;
+        hipLaunchKernelGGL(dplan_kernel, dim3(1), dim3(kDPlanThreads), 0, s, a);
+        THB_HIP(hipGetLastError());
+        plan->spec = *spec;
+        plan->rows = rows;
+        plan->built = true;
+        return THB_OK;
+    });
+}
+
+int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_dplan* plan, void* stream) {
+    if (!pool || !plan) return fail(THB_ERR_INVALID, "null pool or plan");
+    if (plan->pool != pool) return fail(THB_ERR_INVALID, "the plan belongs to another pool");
+    if (!plan->built) return fail(THB_ERR_INVALID, "the plan has not been built (thb_dplan_build)");
+    if (layer >= pool->layers)
+        return fail(THB_ERR_INVALID, "layer " + std::to_string(layer) + " out of range (" +
+                                         std::to_string(pool->layers) + " layers)");
+    if (!q || !y) return fail(THB_ERR_INVALID, "null q or y");
+    if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u))
+        return fail(THB_ERR_INVALID, "q and y must be 16-byte aligned");
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        const uint32_t hd = pool->geom[layer].head_dim;
+        AttnPlan shape;
+        dplan_shape(plan, hd, shape);
+        const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
+        const uint32_t* meta = plan->rows->dev + 8 * static_cast<size_t>(plan->spec.row_off);
+        launch_plan(pool, layer, io, plan->spec, shape, false, meta, static_cast<const uint32_t*>(plan->blob.get()),
+                    static_cast<uint8_t*>(plan->part.get()), s);
+        return THB_OK;
+    });
+}
+
+}  // extern "C"

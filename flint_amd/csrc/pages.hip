@@ -32,8 +32,17 @@
 namespace thb {
 namespace {
 
-enum : uint32_t { kStOk = 0, kStLimit = 1, kStExhausted = 2, kStForkTarget = 3, kStForkCover = 4, kStBadSeq = 5 };
+enum : uint32_t {
+    kStOk = 0,
+    kStLimit = 1,
+    kStExhausted = 2,
+    kStForkTarget = 3,
+    kStForkCover = 4,
+    kStBadSeq = kPageStBadSeq,
+    kStCover = kPageStCover
+};
 enum : uint32_t { kHdrTop = 0, kHdrStatus = 1, kHdrA = 2, kHdrB = 3, kHdrC = 4, kHdrCopies = 5, kHdrWords = 64 };
+static_assert(kHdrStatus == kPageHdrStatus, "status word shared with the attention planner");
 
 constexpr uint32_t kOpsPerLaunch = 64;  // page ops passed in one launch's arguments
 // Set on an alloc op that runs in one batch with the alloc op before it
@@ -480,6 +489,9 @@ std::string status_message(const uint32_t* hdr) {
         case kStForkCover:
             return "fork source " + std::to_string(a) + " does not cover " + std::to_string(b) + " tokens";
         case kStBadSeq: return "sequence " + std::to_string(a) + " out of range (" + std::to_string(b) + " sequences)";
+        case kStCover:
+            return "pages must cover the chunk: sequence " + std::to_string(a) + " holds " + std::to_string(b) +
+                   " slots, a row reads " + std::to_string(hdr[kHdrC]);
         default: return "device page allocator status " + std::to_string(hdr[kHdrStatus]);
     }
 }

@@ -49,6 +49,13 @@ struct AttnPlan {
 
 // Page-API calls the device allocator replays (pages.hip).
 enum : uint32_t { kPageOpAlloc = 1, kPageOpFree = 2, kPageOpTruncate = 3, kPageOpFork = 4, kPageOpAllocRows = 5 };
+// Device allocator header: the status word (first failure since the last
+// thb_pool_status, then 3 arguments), and the status a device-planned
+// attention call records for a row its sequence's pages do not cover
+// (arguments: sequence, slots held, keys the row reads).
+constexpr uint32_t kPageHdrStatus = 1;
+constexpr uint32_t kPageStBadSeq = 5;
+constexpr uint32_t kPageStCover = 6;
 
 // A page-API call queued for the device allocator (pages.hip): it has run on
 // the host mirror and runs on the device before the pool's next kernel.

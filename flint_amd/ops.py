@@ -159,6 +159,49 @@ def attn(q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
     check(lib().thb_attn(kv.handle, layer, qp, yp, ctypes.byref(c), spec.args.handle, _stream_ptr(stream)))
 
 
+class DevicePlan:
+    """thb_dplan_*: a decode call planned on the device from the row meta in
+    device memory (no reference counterpart), so that a step can be captured
+    in a graph once and replayed while positions move.  ``build`` plans the
+    spec's rows (q and y give the spec's dtypes); ``attn`` runs attention of
+    one layer over the plan.  Each (group, partition) computes what ``attn``
+    computes, bit for bit."""
+
+    def __init__(self, kv: KvPool, max_m: int, q_heads: int):
+        h = ctypes.c_void_p()
+        check(lib().thb_dplan_create(kv.handle, max_m, q_heads, ctypes.byref(h)))
+        self._h = h.value
+        self.kv, self.max_m, self.q_heads = kv, max_m, q_heads
+        self.spec = None
+        self._dt = None
+
+    def build(self, spec: AttnSpec, q, y, stream=None) -> None:
+        c = _spec_c(spec, q, y)
+        check(lib().thb_dplan_build(self._h, ctypes.byref(c), spec.args.handle, _stream_ptr(stream)))
+        self.spec = spec
+        self._dt = (_dtype_name(q), _dtype_name(y))
+
+    def attn(self, layer: int, q, y, stream=None) -> None:
+        if self.spec is None:
+            raise ThubanError(_lib.THB_ERR_INVALID, "the plan has not been built")
+        n = self.spec.m * self.spec.q_heads * _head_dim(self.kv, layer)
+        _buf("q", q, n, (self._dt[0],))
+        _buf("y", y, n, (self._dt[1],))
+        check(lib().thb_attn_dplan(self.kv.handle, layer, _addr("q", q), _addr("y", y), self._h,
+                                   _stream_ptr(stream)))
+
+    def close(self) -> None:
+        if self._h:
+            lib().thb_dplan_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def kv_store_attn(k_src, v_src, q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
     """kv_store of the spec's rows followed by attn (the per-layer step of
     transformer/forward.rs:300-336), in one launch where the rows allow it;

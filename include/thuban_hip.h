@@ -54,7 +54,7 @@ extern "C" {
 const char* thb_last_error(void);
 /* ABI revision of this header. */
 uint32_t thb_abi_version(void);
-#define THB_ABI_VERSION 6u
+#define THB_ABI_VERSION 7u
 
 /* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90) exactly:
  * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]". */
@@ -394,6 +394,30 @@ int thb_gemm_acc(const void* x_dev, uint32_t x_dtype, const void* w_dev, uint32_
 #define THB_NOALLOC_PLAN_BYTES (256u << 10)
 int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
                      const thb_rows* rows, void* stream);
+
+/* No reference counterpart: ops::attn (ops/attn.rs:18-51) for decode steps
+ * captured once in a graph and replayed while the rows' positions move.
+ * thb_dplan_build plans the call on the device from the row meta in device
+ * memory (the key ranges, groups and partitions thb_attn's host planner
+ * makes, by the same rules) into buffers the plan owns; thb_attn_dplan then
+ * launches attention over a fixed grid whose slots past the call's groups or
+ * a group's partitions do nothing.  Neither allocates, uploads or reads
+ * anything on the host, so both can be captured; a replay computes each
+ * (group, partition) as thb_attn does, bit for bit, at the row meta's
+ * positions of that replay.  Chunks of four or more groups (prefill) run on
+ * the decode kernel (correct, slower: use thb_attn).  A row whose sequence's
+ * pages do not cover its keys reads nothing (its output is NaN) and the
+ * first such row is reported by thb_pool_status ("pages must cover the
+ * chunk: ...").  A plan serves calls of up to max_m rows and q_heads query
+ * heads; build it after the row meta it plans (stream order), and rebuild it
+ * when the rows, the spec or the pages change.  One plan is one set of
+ * buffers: calls that use it must not overlap. */
+typedef struct thb_dplan thb_dplan;
+int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan** out);
+void thb_dplan_destroy(thb_dplan* plan);
+int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* rows, void* stream);
+int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_dplan* plan,
+                   void* stream);
 
 /* No reference counterpart.  Copies tokens [t0, t0 + n) of seq, layer
  * `layer`, into contiguous k_dst/v_dst [kv_heads, n, head_dim] in the KV type
