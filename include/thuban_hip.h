@@ -408,8 +408,10 @@ int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_
  * the decode kernel (correct, slower: use thb_attn).  A row whose sequence's
  * pages do not cover its keys reads nothing (its output is NaN) and the
  * first such row is reported by thb_pool_status ("pages must cover the
- * chunk: ...").  A plan serves calls of up to max_m rows and q_heads query
- * heads; build it after the row meta it plans (stream order), and rebuild it
+ * chunk: ...").  A plan serves calls of up to max_m rows (at most 4096) and
+ * q_heads query heads; its grid holds max_m x (partitions of the pool's
+ * longest sequence) x kv_heads workgroups, the unused ones returning at
+ * once.  Build it after the row meta it plans (stream order), and rebuild it
  * when the rows, the spec or the pages change.  One plan is one set of
  * buffers: calls that use it must not overlap. */
 typedef struct thb_dplan thb_dplan;
