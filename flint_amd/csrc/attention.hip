@@ -171,6 +171,60 @@ __device__ inline void load_q8(const AttnArgs& a, uint64_t qbase, uint32_t d0, f
     }
 }
 
+// The lane's KS chunks of 8 query elements as f32 (load_q8 for every k-step):
+// every load is issued before the first conversion, from the query's first
+// element where a chunk is out of range (then zeroed), so the KS round trips
+// overlap instead of each waiting behind a branch.
+template <int KS, bool FULL>
+__device__ inline void load_q_all(const AttnArgs& a, bool con, uint64_t qbase, uint32_t a4, float (&x)[KS][8]) {
+    const uint32_t hd = a.head_dim;
+    bool ok[KS];
+    uint64_t off[KS];
+#pragma unroll
+    for (int j = 0; j < KS; j++) {
+        const uint32_t d0 = 32u * j + 8u * a4;
+        ok[j] = con && d0 < hd;
+        off[j] = ok[j] ? qbase + d0 : 0u;
+    }
+    if (a.q_dt == THB_DT_F16) {
+        f16x8 w[KS];
+#pragma unroll
+        for (int j = 0; j < KS; j++) w[j] = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.q) + off[j]);
+#pragma unroll
+        for (int j = 0; j < KS; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[j][e] = ok[j] ? static_cast<float>(w[j][e]) : 0.0f;
+    } else if (FULL && a.q_dt == THB_DT_BF16) {
+        uint4 w[KS];
+#pragma unroll
+        for (int j = 0; j < KS; j++) w[j] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + off[j]);
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const uint32_t ws[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x[j][2 * e] = ok[j] ? __uint_as_float(ws[e] << 16) : 0.0f;
+                x[j][2 * e + 1] = ok[j] ? __uint_as_float(ws[e] & 0xffff0000u) : 0.0f;
+            }
+        }
+    } else {
+        f32x4 u[KS][2];
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + off[j]);
+            u[j][0] = p[0];
+            u[j][1] = p[1];
+        }
+#pragma unroll
+        for (int j = 0; j < KS; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x[j][e] = ok[j] ? u[j][0][e] : 0.0f;
+                x[j][4 + e] = ok[j] ? u[j][1][e] : 0.0f;
+            }
+    }
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float tanh_approx(float x) {
@@ -358,19 +412,13 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
     const uint64_t qbase = (static_cast<uint64_t>(row) * a.q_heads + head) * (FULL ? a.q_stride : hd);
     const bool rope = FULL && a.rope_on;
     if (!rope) {
+        float x[KS][8];
+        load_q_all<KS, FULL>(a, con, qbase, a4, x);
 #pragma unroll
         for (int j = 0; j < KS; j++) {
-            const uint32_t d0 = 32u * j + 8u * a4;
-            float x[8];
-            if (con && d0 < hd) {
-                load_q8<FULL>(a, qbase, d0, x);
-            } else {
 #pragma unroll
-                for (int e = 0; e < 8; e++) x[e] = 0.0f;
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e++) x[e] *= pre;
-            O::split8(x, qh[j], ql[j]);
+            for (int e = 0; e < 8; e++) x[j][e] *= pre;
+            O::split8(x[j], qh[j], ql[j]);
         }
         return;
     }
@@ -378,16 +426,7 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
     const RopeDev& r = a.qrope;
     const uint32_t pos = con ? a.meta[8 * row] : 0u;
     float x[KS][8];
-#pragma unroll
-    for (int j = 0; j < KS; j++) {
-        const uint32_t d0 = 32u * j + 8u * a4;
-        if (con && d0 < hd) {
-            load_q8<FULL>(a, qbase, d0, x[j]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; e++) x[j][e] = 0.0f;
-        }
-    }
+    load_q_all<KS, FULL>(a, con, qbase, a4, x);
     float inv = 1.0f;
     if (r.w) {
         float ss = 0.0f;
