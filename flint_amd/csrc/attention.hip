@@ -58,6 +58,13 @@ constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units)
 constexpr float kFloor = -1.0e30f;    // initial running max (finite on purpose)
 constexpr uint32_t kGroupWords = 11;  // r0, R, h0, H, seq, lo, hi, n_parts, base, plen, item0
 constexpr uint32_t kMaxPartPages = 1024;
+// Raw buffer resources (decode tile loads): word 3 of a gfx9 descriptor
+// with a 32-bit data format (untyped loads need a nonzero one), the
+// non-temporal cache-policy bit of a buffer load, and an offset that is out
+// of range of every resource the kernels build (loads there return zeros).
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kBufferNt = 2;
+constexpr uint32_t kBufferOob = 0xFFFFFFF0u;
 constexpr uint32_t kMaxParts = 512;   // partitions of one group the merge kernel takes
 constexpr uint32_t kCols = 16;        // query vectors per group (MFMA N)
 constexpr uint32_t kMergeWords = 8;   // merge record: r0, R, h0, H, n_parts, item0, 0, 0
@@ -476,27 +483,44 @@ __device__ inline void load_q(const AttnArgs& a, bool con, uint32_t row, uint32_
     }
 }
 
+// The query operand in LDS (head_dim 512 only: QLDS), else nothing.
+template <typename T, int KS, bool QLDS>
+struct DecodeQLds {
+    T q[KS][2][64];
+};
+template <typename T, int KS>
+struct DecodeQLds<T, KS, false> {};
+
+// LDS of one decode workgroup.  The W waves' states are merged in one step
+// (every state in LDS, each wave merging and storing its own 16-dimension
+// tiles) up to head_dim 256 (128 KiB at 8 waves); head_dim 512 uses a fixed
+// tree over W / 2 states.
+template <int HD, bool F16, int W>
+struct DecodeLds : DecodeQLds<typename Ops<F16>::in8, HD / 32, q_in_lds(HD)> {
+    static constexpr bool FLAT = HD <= 256;
+    static constexpr int NSTATE = FLAT ? W : (W / 2 > 0 ? W / 2 : 1);
+    uint32_t page[kMaxPartPages];
+    f32x4 o[NSTATE][HD / 16][64];
+    float m[NSTATE][64];
+    float l[NSTATE][64];
+};
+
 // One (group, partition, KV head) per workgroup of W waves.  NB tiles of
 // loads are kept in flight per wave: tile i + NB is requested as soon as
 // tile i has been consumed.
 template <int HD, bool F16, int W, int NB, bool FULL>
-__device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
+__device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, DecodeLds<HD, F16, W>& L) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
     typedef typename O::in4 in4;
     constexpr int KS = HD / 32;  // QK k-steps of 32 dimensions
     constexpr int MT = HD / 16;  // PV tiles of 16 dimensions
-    // The W waves' states are merged in one step (every state in LDS, each
-    // wave merging and storing its own 16-dimension tiles) where they fit:
-    // up to head_dim 128 beside the prefill body of attn_mixed, at 256 (128
-    // KiB, never in attn_mixed) alone; head_dim 512 uses a fixed tree.
-    constexpr bool FLAT = HD <= 256;
-    constexpr int NSTATE = FLAT ? W : (W / 2 > 0 ? W / 2 : 1);
-
-    __shared__ uint32_t s_page[kMaxPartPages];
-    __shared__ f32x4 s_o[NSTATE][MT][64];
-    __shared__ float s_m[NSTATE][64];
-    __shared__ float s_l[NSTATE][64];
+    constexpr bool FLAT = DecodeLds<HD, F16, W>::FLAT;
+    constexpr int NSTATE = DecodeLds<HD, F16, W>::NSTATE;
+    auto& s_page = L.page;
+    auto& s_o = L.o;
+    auto& s_m = L.m;
+    auto& s_l = L.l;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -545,7 +569,6 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     // Q^T operand: lane (a4, c) holds q[c][32j + 8a4 .. +8], split hi/lo; at
     // head_dim 512 in LDS (wave 0 writes it before the barrier below).
     constexpr bool QLDS = q_in_lds(HD);
-    __shared__ in8 s_q[QLDS ? KS : 1][2][64];
     [[maybe_unused]] in8 qh[QLDS ? 1 : KS], ql[QLDS ? 1 : KS];
     if constexpr (QLDS) {
         if (wave == 0) {
@@ -553,8 +576,8 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
             load_q<KS, O, FULL>(a, con, row, head, a4, th, tl);
 #pragma unroll
             for (int j = 0; j < KS; j++) {
-                s_q[j][0][lane] = th[j];
-                s_q[j][1][lane] = tl[j];
+                L.q[j][0][lane] = th[j];
+                L.q[j][1][lane] = tl[j];
             }
         }
     } else {
@@ -573,10 +596,9 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     // hi - 1 of the row, and the only wave that ever loads it is the wave
     // whose run holds that position.  That wave encodes and stores the row's
     // K and V of this KV head (exactly as kv_store) before its first tile
-    // load: the first item of each lane before the workgroup barrier (whose
-    // wait covers the stores), further items (more than 64) after it, where
-    // one wave's accesses to an address are ordered.  Work item t of the
-    // group: row t / (2 cpr), K or V, 8-element chunk.
+    // load; one wave's accesses to an address are ordered, so its tile loads
+    // read the stored token.  Work item t of the group: row t / (2 cpr), K or
+    // V, 8-element chunk.
     const uint32_t cpr = hd >> 3;
     const uint32_t app_items = a.k_src != nullptr ? R * 2 * cpr : 0u;
     constexpr uint32_t KVE = F16 ? THB_KV_F16_RNE : THB_KV_BF16_TRUNC;
@@ -607,28 +629,20 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     };
     uint32_t app_pos = 0, app_d = 0;
     uint64_t app_e = 0;
-    bool app_v = false, app_own = false, app_late = false;
-    uint4 app_w = make_uint4(0u, 0u, 0u, 0u);
+    bool app_v = false, app_own = false;
+    Raw8 app_raw{};
     const bool rope = FULL && a.rope_on;
-    // First item of each lane: which lane owns one is known before the
-    // barrier (its position load runs beside the query loads), but its
-    // source is loaded after it, so the barrier's wait does not take a second
-    // round trip.  The source load then completes beside the first tile
-    // loads.  When the token lies beyond the wave's first NB tiles, the store
-    // is issued in the tile loop, right before the load of the token's tile:
-    // a wave's waits for loads issued after a store also wait for the store,
-    // which is acknowledged long after it is issued.  Otherwise it is stored
-    // before any tile load.
-    if (lane < app_items && !rope) app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
-    __syncthreads();
-    if (app_own) {
-        app_w = load_encode8_rt<KVE>(a.src_dtype, app_v ? a.v_src : a.k_src, app_e);
-        app_late = app_pos >= ws + 16u * NB;
-        if (!app_late) {
-            app_store(app_pos, app_v, app_d, app_w);
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        }
+    // First item of each lane: its position and its source (whose address
+    // does not depend on the position) are loaded beside the query loads in
+    // every wave, before the barrier, so no wave waits a second round trip;
+    // the owning lane encodes and stores it after the barrier, before the
+    // first tile load.  The tile loop then holds no store.
+    if (lane < app_items && !rope) {
+        app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
+        app_raw = load_raw8_rt(a.src_dtype, app_v ? a.v_src : a.k_src, app_e);
     }
+    __syncthreads();
+    if (app_own) app_store(app_pos, app_v, app_d, encode8_rt<KVE>(a.src_dtype, app_raw));
     if (rope) {
         if (app_items != 0) {
             // Rotary append: the key head of each row this wave owns, one chunk
@@ -676,37 +690,67 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
     const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
     const uint32_t last = te > 0 ? te - 1 : 0;
+    const uint32_t page_elems = hd << pshift;
 
-    // Loads one 16-token tile.  Tokens outside [tb, te) are clamped into
-    // it (their scores are masked), so every address is inside a page of
-    // the sequence.
+    // Loads one 16-token tile with buffer loads.  Tokens outside [tb, te)
+    // are clamped into it (their scores are masked).  The tile's tokens lie
+    // in the pages of its first and last clamped token (one page unless
+    // page_len is 8); the buffer resource starts at the lower of the two, so
+    // every lane's byte offset is non-negative (below 4 GiB: the pool checks
+    // the plane size for page_len 8).  A tile past the wave's run gets a
+    // resource of size 0 and a lane past head_dim an offset beyond the size:
+    // such loads return zeros without touching memory (K dims past head_dim
+    // must be zeros: the query is zero there).  Every load is thus
+    // issued unconditionally, and the compiler's wait counts stay exact
+    // through the tile loop (a skipped load would force a full drain).
     // K pages hold 32-dimension groups ([hd/32][page_len][32]): for a fixed
     // k-step j the 64 lanes read 16 tokens x 64 bytes, 1 KiB contiguous.  V
     // pages hold 4-slot groups ([page_len/4][hd][4]): a lane's 4 slots of one
     // dim are 8 bytes, and 16 lanes read 128 contiguous bytes.  The loads are
-    // non-temporal: every byte is read once.
+    // non-temporal (every byte is read once).
+    struct TileRes {
+        __amdgpu_buffer_rsrc_t k, v;
+        uint32_t pa, pb, pmin, first_lp;
+    };
+    auto tile_res = [&](uint32_t t0) {
+        TileRes r;
+        const bool on = t0 < we;  // then tb <= tf <= tl <= last: pages of the partition
+        const uint32_t tf = min(max(t0, tb), last), tl = min(max(t0 + 15u, tb), last);
+        r.first_lp = tf >> pshift;
+        r.pa = __builtin_amdgcn_readfirstlane(s_page[on ? r.first_lp - (pbeg >> pshift) : 0u]);
+        r.pb = __builtin_amdgcn_readfirstlane(s_page[on ? (tl >> pshift) - (pbeg >> pshift) : 0u]);
+        r.pmin = min(r.pa, r.pb);
+        const uint32_t nrec = on ? (max(r.pa, r.pb) - r.pmin + 1u) * 2u * page_elems : 0u;
+        const uint64_t off = static_cast<uint64_t>(r.pmin) * page_elems;
+        r.k = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kplane + off), 0, nrec, kBufferFlags);
+        r.v = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vplane + off), 0, nrec, kBufferFlags);
+        return r;
+    };
+    // Byte offset of token t's page from the resource base.
+    auto page_bytes_off = [&](const TileRes& r, uint32_t t) {
+        return ((t >> pshift) == r.first_lp ? r.pa - r.pmin : r.pb - r.pmin) * 2u * page_elems;
+    };
     auto load_k = [&](uint32_t t0, u32x4 (&kr)[KS]) {
+        const TileRes r = tile_res(t0);
         const uint32_t tk = min(max(t0 + c, tb), last);
-        const uint32_t kpage = s_page[(tk - pbeg) >> pshift];
-        const uint16_t* kbase = kplane + (static_cast<uint64_t>(kpage) * hd << pshift);
+        const uint32_t base = page_bytes_off(r, tk);
 #pragma unroll
         for (int j = 0; j < KS; j++) {
             const uint32_t d0 = 32u * j + 8u * a4;
-            kr[j] = d0 < hd ? __builtin_nontemporal_load(
-                                  reinterpret_cast<const u32x4*>(kbase + k_off(tk & pmask, d0, hd, pshift)))
-                            : u32x4{0u, 0u, 0u, 0u};
+            const uint32_t off = d0 < hd ? base + 2u * k_off(tk & pmask, d0, hd, pshift) : kBufferOob;
+            kr[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r.k, off, 0, kBufferNt));
         }
     };
     auto load_v = [&](uint32_t t0, u32x2 (&vr)[MT]) {
+        const TileRes r = tile_res(t0);
         const uint32_t tv = min(max(t0 + 4u * a4, tb & ~3u), last & ~3u);
-        const uint32_t vpage = s_page[(tv - pbeg) >> pshift];
-        const uint16_t* vbase = vplane + (static_cast<uint64_t>(vpage) * hd << pshift) + v_off(tv & pmask, 0, hd);
+        const uint32_t base = page_bytes_off(r, tv) + 2u * v_off(tv & pmask, 0, hd);
+        // Dims past head_dim read whatever lies there (or zeros): each PV
+        // output row is one dim, so they only reach outputs never stored.
 #pragma unroll
-        for (int i = 0; i < MT; i++) {
-            const uint32_t d = 16u * i + c;
-            vr[i] = d < hd ? __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vbase + 4u * d))
-                           : u32x2{0u, 0u};
-        }
+        for (int i = 0; i < MT; i++)
+            vr[i] = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(r.v, base + 8u * (16u * i + c), 0, kBufferNt));
     };
     auto load = [&](uint32_t t0, u32x4 (&kr)[KS], u32x2 (&vr)[MT]) {
         load_k(t0, kr);
@@ -721,8 +765,8 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
 #pragma unroll
         for (int j = 0; j < KS; j++) {
             if constexpr (QLDS) {
-                s = O::qk(kr[j], s_q[j][0][lane], s);
-                s = O::qk(kr[j], s_q[j][1][lane], s);
+                s = O::qk(kr[j], L.q[j][0][lane], s);
+                s = O::qk(kr[j], L.q[j][1][lane], s);
             } else {
                 s = O::qk(kr[j], qh[j], s);
                 s = O::qk(kr[j], ql[j], s);
@@ -769,44 +813,25 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
     };
 
     {
+        // NB tiles in flight per wave.  Loads of tiles past the run are
+        // issued too (they read nothing), so every iteration issues the same
+        // loads and only the products are skipped.
         u32x4 kr[NB][KS];
         u32x2 vr[NB][MT];
 #pragma unroll
-        for (int b = 0; b < NB; b++)
-            if (ws + 16u * b < we) load(ws + 16u * b, kr[b], vr[b]);
+        for (int b = 0; b < NB; b++) load(ws + 16u * b, kr[b], vr[b]);
         for (uint32_t t0 = ws; t0 < we; t0 += 16u * NB) {
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                const uint32_t t = t0 + 16u * b;
-                if (t < we) {
-                    const uint32_t tn = t + 16u * NB;
-                    // The token lies beyond tile NB of this wave: it is
-                    // stored just before the load of its own tile, so only
-                    // the waits for that tile (whose load latency covers
-                    // the store's) also wait for the store.
-                    auto store_late = [&]() {
-                        if (app_late && app_pos - tn < 16u) {
-                            app_store(app_pos, app_v, app_d, app_w);
-                            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                        }
-                    };
-                    if constexpr (NB == 1) {
-                        // One tile in flight: the next tile's K goes out as soon
-                        // as this tile's K is consumed, its V after the PV.
-                        compute(t, kr[b], vr[b], [&]() {
-                            if (tn < we) {
-                                store_late();
-                                load_k(tn, kr[b]);
-                            }
-                        });
-                        if (tn < we) load_v(tn, vr[b]);
-                    } else {
-                        compute(t, kr[b], vr[b], []() {});
-                        if (tn < we) {
-                            store_late();
-                            load(tn, kr[b], vr[b]);
-                        }
-                    }
+                const uint32_t t = t0 + 16u * b, tn = t + 16u * NB;
+                if constexpr (NB == 1) {
+                    // One tile in flight: the next tile's K goes out as soon
+                    // as this tile's K is consumed, its V after the PV.
+                    compute(t, kr[b], vr[b], [&]() { load_k(tn, kr[b]); });
+                    load_v(tn, vr[b]);
+                } else {
+                    if (t < we) compute(t, kr[b], vr[b], []() {});
+                    load(tn, kr[b], vr[b]);
                 }
             }
         }
@@ -903,7 +928,8 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid) {
 
 template <int HD, bool F16, int W, int NB, bool FULL>
 __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
-    decode_wg<HD, F16, W, NB, FULL>(a, blockIdx.x);
+    __shared__ DecodeLds<HD, F16, W> lds;
+    decode_wg<HD, F16, W, NB, FULL>(a, blockIdx.x, lds);
 }
 
 // Merges the partitions of every group that has more than one, in
@@ -1231,8 +1257,17 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
 #ifndef THB_PREFILL_NCG
 #define THB_PREFILL_NCG 2
 #endif
+// LDS of one prefill workgroup: the double-buffered K and V tiles and the
+// partition's page list.
+template <int HD>
+struct PrefillLds {
+    u32x4 k[2][THB_PREFILL_TILE * HD / 8];
+    u32x4 v[2][THB_PREFILL_TILE / 32 * HD * 4];
+    uint32_t page[kMaxPartPages];
+};
+
 template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
-__device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid) {
+__device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid, PrefillLds<HD>& L) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
     constexpr int KS = HD / 32;
@@ -1248,9 +1283,10 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
     constexpr int KPT = (KU + NT - 1) / NT;
     constexpr int VPT = (VP + NT - 1) / NT;
 
-    __shared__ u32x4 s_k[2][KU];
-    __shared__ u32x4 s_v[2][VE];
-    __shared__ uint32_t s_page[kMaxPartPages];
+    static_assert(sizeof(L.k[0]) == KU * 16 && sizeof(L.v[0]) == VE * 16, "prefill LDS tiles");
+    auto& s_k = L.k;
+    auto& s_v = L.v;
+    auto& s_page = L.page;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1632,7 +1668,8 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid)
 
 template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
 __global__ __launch_bounds__(64 * W, W >= 8 ? W / 4 : 1) void attn_prefill_wide(AttnArgs a) {
-    prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, blockIdx.x);
+    __shared__ PrefillLds<HD> lds;
+    prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, blockIdx.x, lds);
 }
 
 // A call with decode items and prefill blocks (a continuous batch) as one
@@ -1641,16 +1678,24 @@ __global__ __launch_bounds__(64 * W, W >= 8 ? W / 4 : 1) void attn_prefill_wide(
 // The host interleaves the two kinds, so that workgroups streaming KV from
 // HBM and workgroups busy on the matrix cores run side by side on different
 // CUs instead of one kernel after the other.  Each workgroup runs exactly
-// the code (and arithmetic) of its own kernel.
+// the code (and arithmetic) of its own kernel.  The two bodies' LDS
+// overlay each other.
+template <int HD, bool F16, int W>
+union MixedLds {
+    DecodeLds<HD, F16, W> d;
+    PrefillLds<HD> p;
+};
+
 template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
 __global__ __launch_bounds__(64 * W, 2) void attn_mixed(AttnArgs a) {
+    __shared__ MixedLds<HD, F16, W> lds;
     const uint32_t rec = blockIdx.x / a.n_kvh, kvh = blockIdx.x - rec * a.n_kvh;
     const uint32_t w = a.order[rec];
     const uint32_t bid = (w & 0x7FFFFFFFu) * a.n_kvh + kvh;
     if (w >> 31)
-        prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, bid);
+        prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, bid, lds.p);
     else
-        decode_wg<HD, F16, W, ring_for(HD), FULL>(a, bid);
+        decode_wg<HD, F16, W, ring_for(HD), FULL>(a, bid, lds.d);
 }
 
 // ---------------------------------------------------- device-side planning
@@ -2195,7 +2240,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     // arithmetic.
     const bool mixed = n_items > 0 && n_bitems > 0 && wide && THB_ATTN_WAVES == THB_PREFILL_WAVES;
     if (mixed) {
-        constexpr double kHbmBytesPerUs = 6.2e6, kCuBytesPerUs = 3.7e4;
+        constexpr double kHbmBytesPerUs = 6.2e6, kCuBytesPerUs = 3.7e4 * THB_PREFILL_WAVES / 8;
         const uint32_t n_kvh = pool->kv_heads;
         std::vector<std::pair<double, uint32_t>> dec, pre;  // (bytes per workgroup | us, record)
         dec.reserve(n_items);
@@ -2217,7 +2262,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         };
         std::stable_sort(dec.begin(), dec.end(), longest_first);
         std::stable_sort(pre.begin(), pre.end(), longest_first);
-        const uint32_t slots = std::max<uint32_t>(2, pool->cus / n_kvh);
+        const uint32_t slots = std::max<uint32_t>(2, pool->cus * (8 / THB_PREFILL_WAVES) / n_kvh);
         std::vector<uint32_t> order, best;
         double best_t = INFINITY;
         const uint32_t step = std::max<uint32_t>(1, slots / 32);  // at most ~32 simulations

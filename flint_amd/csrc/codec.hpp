@@ -103,6 +103,47 @@ __device__ inline uint4 load_encode8(const void* src, uint64_t e) {
     return out;
 }
 
+// 8 source elements as loaded (f32: 32 bytes in a, b; 16-bit types: 16
+// bytes in a), so the load can be issued long before the encoding.
+struct Raw8 {
+    uint4 a, b;
+};
+
+__device__ inline Raw8 load_raw8_rt(uint32_t src_dtype, const void* src, uint64_t e) {
+    Raw8 r{};
+    if (src_dtype == THB_DT_F32) {
+        const float* p = static_cast<const float*>(src) + e;
+        r.a = ld_stream16(p);
+        r.b = ld_stream16(p + 4);
+    } else {
+        r.a = ld_stream16(static_cast<const uint16_t*>(src) + e);
+    }
+    return r;
+}
+
+// The encoding of load_encode8 applied to loaded words.
+template <uint32_t KV>
+__device__ inline uint4 encode8_rt(uint32_t src_dtype, const Raw8& r) {
+    uint4 out;
+    if (src_dtype == THB_DT_F32) {
+        out.x = conv32<KV>(r.a.x) | (conv32<KV>(r.a.y) << 16);
+        out.y = conv32<KV>(r.a.z) | (conv32<KV>(r.a.w) << 16);
+        out.z = conv32<KV>(r.b.x) | (conv32<KV>(r.b.y) << 16);
+        out.w = conv32<KV>(r.b.z) | (conv32<KV>(r.b.w) << 16);
+    } else if (src_dtype == THB_DT_F16) {
+        auto c2 = [](uint32_t w) {
+            return conv16<THB_DT_F16, KV>(w & 0xffffu) | (conv16<THB_DT_F16, KV>(w >> 16) << 16);
+        };
+        out = make_uint4(c2(r.a.x), c2(r.a.y), c2(r.a.z), c2(r.a.w));
+    } else {
+        auto c2 = [](uint32_t w) {
+            return conv16<THB_DT_BF16, KV>(w & 0xffffu) | (conv16<THB_DT_BF16, KV>(w >> 16) << 16);
+        };
+        out = make_uint4(c2(r.a.x), c2(r.a.y), c2(r.a.z), c2(r.a.w));
+    }
+    return out;
+}
+
 // Runtime source type, compile-time KV encoding.
 template <uint32_t KV>
 __device__ inline uint4 load_encode8_rt(uint32_t src_dtype, const void* src, uint64_t e) {

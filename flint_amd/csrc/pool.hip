@@ -312,6 +312,12 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
         uint64_t off = 0;
         for (uint32_t l = 0; l < d->layers; l++) {
             uint32_t hd = d->head_dims ? d->head_dims[l] : d->head_dim;
+            // A decode tile of 16 tokens spans two pages at page_len 8, read
+            // through one buffer resource with 32-bit offsets between them.
+            if (d->page_len < 16 && pool_len * hd * 2 > 0xFFFF0000ull)
+                return fail(THB_ERR_CONFIG, "page_len " + std::to_string(d->page_len) + " holds at most 4 GiB per KV-head plane (layer " +
+                                                std::to_string(l) + " needs " + std::to_string(pool_len * hd * 2) +
+                                                " bytes); use page_len >= 16");
             uint64_t plane = (static_cast<uint64_t>(d->kv_heads) * pool_len * hd * 2 + 255) & ~uint64_t(255);
             p->geom.push_back({hd, off, off + plane});
             off += 2 * plane;
