@@ -126,6 +126,10 @@ struct AttnArgs {
     uint32_t src_dtype;
     float* part_o;   // [n_items][n_kvh][16][hd_t]
     float* part_ml;  // [n_items][n_kvh][16][2]
+    // Arrival counters of the decode groups of several partitions, one per
+    // (first item, KV head), zero between launches; null: attn_merge combines
+    // every group's partitions after the launch.
+    uint32_t* merge_cnt;
     uint64_t plane;  // 16-bit elements per head plane
     uint32_t max_pages, page_shift, q_heads, nq_per_kv, head_dim, part_len, n_kvh;
     float qscale;  // scale * log2(e), or scale / softcap
@@ -491,6 +495,126 @@ struct DecodeQLds {
 template <typename T, int KS>
 struct DecodeQLds<T, KS, false> {};
 
+// ------------------------------------------------ split-K partition merge
+// A group whose keys span several partitions has one partial result (m, l,
+// o) per partition.  The partials are written with relaxed agent-scope
+// atomic stores and read with relaxed agent-scope atomic loads (coherent
+// across the XCDs' L2 caches: the stores reach the device's coherence point,
+// the loads do not hit a stale copy), so a workgroup of the same launch can
+// read another's partial once that partial's stores have completed.
+__device__ inline void publish_o(float* p, const f32x4& v) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(p);
+    __hip_atomic_store(q, (uint64_t(__float_as_uint(v[1])) << 32) | __float_as_uint(v[0]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, (uint64_t(__float_as_uint(v[3])) << 32) | __float_as_uint(v[2]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void publish_ml(float* p, float m, float l) {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), (uint64_t(__float_as_uint(l)) << 32) | __float_as_uint(m),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool COH>
+__device__ inline uint64_t load_u64(const float* p) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    if constexpr (COH)
+        return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        return *q;
+}
+template <bool COH>
+__device__ inline f32x4 load_o(const float* p) {
+    const uint64_t lo = load_u64<COH>(p), hi = load_u64<COH>(p + 2);
+    return f32x4{__uint_as_float(static_cast<uint32_t>(lo)), __uint_as_float(static_cast<uint32_t>(lo >> 32)),
+                 __uint_as_float(static_cast<uint32_t>(hi)), __uint_as_float(static_cast<uint32_t>(hi >> 32))};
+}
+
+// Combines the partitions of one (group, KV head) in partition order.  Each
+// of NT threads owns 4-dimension units of the group's outputs (unit u:
+// column u / q4, dims 4 (u % q4) .. + 4) and reads its column's (m, l)
+// itself; up to U partitions are requested at once, (m, l) and o together.
+// The arithmetic does not depend on NT or on where it runs (the merge
+// kernel, or the workgroup of the group's last partition), so neither does
+// the output.
+template <int HD, bool FULL, int NT, bool COH>
+__device__ __forceinline__ void merge_group(const AttnArgs& a, uint32_t r0, uint32_t R, uint32_t h0, uint32_t H,
+                                            uint32_t n_parts, uint32_t item0, uint32_t kvh, uint32_t tid) {
+    const uint32_t ncols = R * H, hd = a.head_dim, q4 = hd >> 2;
+    const uint64_t base = static_cast<uint64_t>(item0) * a.n_kvh + kvh;  // partition pi: base + pi * n_kvh
+    const uint64_t mstep = 2 * static_cast<uint64_t>(a.n_kvh) * kCols;   // (m, l) of the next partition
+    const uint64_t ostep = static_cast<uint64_t>(a.n_kvh) * kCols * HD;  // o of the next partition
+    constexpr uint32_t U = 8, NU = (kCols * HD / 4 + NT - 1) / NT;
+    for (uint32_t u0 = 0; u0 < NU; u0++) {
+        const uint32_t u = tid + NT * u0;
+        if (u >= ncols * q4) break;
+        const uint32_t c = u / q4, d = 4u * (u - c * q4);
+        const float* ml = a.part_ml + 2 * (base * kCols + c);
+        const float* op = a.part_o + (base * kCols + c) * HD + d;
+        float M = kFloor;
+        if (n_parts > U) {  // long merges: the maximum first
+            for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
+                float mv[U];
+#pragma unroll
+                for (uint32_t k = 0; k < U; k++)
+                    mv[k] = p0 + k < n_parts ? __uint_as_float(static_cast<uint32_t>(load_u64<COH>(ml + (p0 + k) * mstep)))
+                                             : kFloor;
+#pragma unroll
+                for (uint32_t k = 0; k < U; k++) M = fmaxf(M, mv[k]);
+            }
+        }
+        float L = 0.0f;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
+            float mv[U], lv[U];
+            f32x4 ov[U];
+#pragma unroll
+            for (uint32_t k = 0; k < U; k++) {
+                const bool in = p0 + k < n_parts;
+                const uint64_t w = in ? load_u64<COH>(ml + (p0 + k) * mstep) : 0ull;
+                mv[k] = in ? __uint_as_float(static_cast<uint32_t>(w)) : kFloor;
+                lv[k] = in ? __uint_as_float(static_cast<uint32_t>(w >> 32)) : 0.0f;
+                ov[k] = in ? load_o<COH>(op + (p0 + k) * ostep) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            if (n_parts <= U) {
+#pragma unroll
+                for (uint32_t k = 0; k < U; k++) M = fmaxf(M, mv[k]);
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < U; k++) {
+                if (p0 + k >= n_parts) break;
+                const float w = fast_exp2(mv[k] - M);
+                L += w * lv[k];
+                acc += w * ov[k];
+            }
+        }
+        const float inv = 1.0f / L;
+        const float yv[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        const uint32_t rr = c / H, hh = c - rr * H;
+        store_y<4, FULL>(a, r0 + rr, kvh * a.nq_per_kv + h0 + hh, d, yv);
+    }
+}
+
+// Run by every thread of a decode workgroup of a group with several
+// partitions once its partial is published: the workgroup that finishes
+// the group's last partition combines them all (merge_group) and clears the
+// group's counter for the next launch.  Each thread waits until its partial
+// stores have completed before the barrier, the counter add (relaxed, agent
+// scope) is issued after it, and the combining loads only after the add has
+// returned, so the last workgroup's loads find every partition's stores
+// done.  No workgroup waits for another.
+template <int HD, bool FULL, int NT>
+__device__ __forceinline__ void merge_if_last(const AttnArgs& a, uint32_t& s_arrived, uint32_t r0, uint32_t R,
+                                              uint32_t h0, uint32_t H, uint32_t n_parts, uint32_t item0,
+                                              uint32_t kvh, uint32_t tid) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    uint32_t* cnt = a.merge_cnt + static_cast<uint64_t>(item0) * a.n_kvh + kvh;
+    if (tid == 0) s_arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived + 1u != n_parts) return;
+    merge_group<HD, FULL, NT, true>(a, r0, R, h0, H, n_parts, item0, kvh, tid);
+    if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // LDS of one decode workgroup.  The W waves' states are merged in one step
 // (every state in LDS, each wave merging and storing its own 16-dimension
 // tiles) up to head_dim 256 (128 KiB at 8 waves); head_dim 512 uses a fixed
@@ -503,6 +627,7 @@ struct DecodeLds : DecodeQLds<typename Ops<F16>::in8, HD / 32, q_in_lds(HD)> {
     f32x4 o[NSTATE][HD / 16][64];
     float m[NSTATE][64];
     float l[NSTATE][64];
+    uint32_t arrived;  // partitions of the group finished before this one
 };
 
 // One (group, partition, KV head) per workgroup of W waves.  NB tiles of
@@ -516,11 +641,11 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
     constexpr int KS = HD / 32;  // QK k-steps of 32 dimensions
     constexpr int MT = HD / 16;  // PV tiles of 16 dimensions
     constexpr bool FLAT = DecodeLds<HD, F16, W>::FLAT;
-    constexpr int NSTATE = DecodeLds<HD, F16, W>::NSTATE;
     auto& s_page = L.page;
     auto& s_o = L.o;
     auto& s_m = L.m;
     auto& s_l = L.l;
+    auto& s_arrived = L.arrived;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -531,7 +656,7 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
 
     const uint32_t* G = a.items + static_cast<uint64_t>(item) * kItemWords;
     const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3], seq = G[4];
-    const uint32_t glo = G[5], ghi = G[6], n_parts = G[7], gbase = G[8], P = G[9];
+    const uint32_t glo = G[5], ghi = G[6], n_parts = G[7], gbase = G[8], P = G[9], item0 = G[10];
     // A device-planned call's fixed grid holds slots past a group's last
     // partition (and groups past the call's last): they do nothing.
     if (G[kGroupWords] >= n_parts) return;
@@ -867,15 +992,14 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
                 const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
                 store_y<4, FULL>(a, row, head, d, v4);
             } else {
-                // several partitions: publish this one's (m, l, o); the
-                // merge kernel combines them after this kernel has finished
-                *reinterpret_cast<f32x4*>(a.part_o + pb * HD + d) = acc;
+                // several partitions: publish this one's (m, l, o) for the
+                // workgroup of the last partition (or the merge kernel)
+                publish_o(a.part_o + pb * HD + d, acc);
             }
         }
-        if (n_parts > 1 && wave == 0 && con && a4 == 0) {
-            a.part_ml[2 * pb] = M;
-            a.part_ml[2 * pb + 1] = L;
-        }
+        if (n_parts > 1 && wave == 0 && con && a4 == 0) publish_ml(a.part_ml + 2 * pb, M, L);
+        if (n_parts > 1 && a.merge_cnt)
+            merge_if_last<HD, FULL, 64 * W>(a, s_arrived, r0, R, h0, H, n_parts, item0, kvh, tid);
         return;
     }
 
@@ -900,30 +1024,28 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
         }
         __syncthreads();
     }
-    if (wave != 0 || !con) return;
-
-    if (n_parts == 1) {
-        const float inv = 1.0f / l;
+    if (wave == 0 && con) {
+        if (n_parts == 1) {
+            const float inv = 1.0f / l;
 #pragma unroll
-        for (int i = 0; i < MT; i++) {
-            const uint32_t d = 16u * i + 4u * a4;
-            if (d >= hd) continue;
-            const f32x4 yv = o[i] * inv;
-            const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
-            store_y<4, FULL>(a, row, head, d, v4);
+            for (int i = 0; i < MT; i++) {
+                const uint32_t d = 16u * i + 4u * a4;
+                if (d >= hd) continue;
+                const f32x4 yv = o[i] * inv;
+                const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
+                store_y<4, FULL>(a, row, head, d, v4);
+            }
+        } else {
+            // Several partitions: publish this one's (m, l, o) for the
+            // workgroup of the last partition (or the merge kernel).
+            const uint64_t pb = (static_cast<uint64_t>(item) * a.n_kvh + kvh) * kCols + c;
+#pragma unroll
+            for (int i = 0; i < MT; i++) publish_o(a.part_o + pb * HD + 16u * i + 4u * a4, o[i]);
+            if (a4 == 0) publish_ml(a.part_ml + 2 * pb, m, l);
         }
-        return;
     }
-    // Several partitions: publish this one's (m, l, o); the merge kernel
-    // combines them after this kernel has finished.
-    const uint64_t pb = (static_cast<uint64_t>(item) * a.n_kvh + kvh) * kCols + c;
-#pragma unroll
-    for (int i = 0; i < MT; i++)
-        *reinterpret_cast<f32x4*>(a.part_o + pb * HD + 16u * i + 4u * a4) = o[i];
-    if (a4 == 0) {
-        a.part_ml[2 * pb] = m;
-        a.part_ml[2 * pb + 1] = l;
-    }
+    if (n_parts > 1 && a.merge_cnt)
+        merge_if_last<HD, FULL, 64 * W>(a, s_arrived, r0, R, h0, H, n_parts, item0, kvh, tid);
 }
 
 template <int HD, bool F16, int W, int NB, bool FULL>
@@ -941,63 +1063,9 @@ __global__ __launch_bounds__(256) void attn_merge(AttnArgs a) {
     // Merge record (kMergeWords): the group's r0, R, h0, H, n_parts, item0,
     // so the partials are requested one round trip after the launch.
     const uint32_t* E = a.merge_groups + static_cast<uint64_t>(blockIdx.x) * kMergeWords;
-    const uint32_t kvh = blockIdx.y, tid = threadIdx.x;
-    const uint32_t r0 = E[0], R = E[1], h0 = E[2], H = E[3], n_parts = E[4], item0 = E[5];
+    const uint32_t n_parts = E[4];
     if (n_parts <= 1) return;  // a device-planned call's slot of a one-partition group (or none)
-    const uint32_t ncols = R * H, hd = a.head_dim, q4 = hd >> 2;
-    const uint64_t base = static_cast<uint64_t>(item0) * a.n_kvh + kvh;  // partition pi: base + pi * n_kvh
-    const uint64_t mstep = 2 * static_cast<uint64_t>(a.n_kvh) * kCols;   // (m, l) of the next partition
-    const uint64_t ostep = static_cast<uint64_t>(a.n_kvh) * kCols * HD;  // o of the next partition
-    // Each thread owns 4-dimension units of the group's outputs (unit u:
-    // column u / q4, dims 4 (u % q4) .. + 4) and reads its column's (m, l)
-    // itself.  Up to U partitions are requested at once, (m, l) and o
-    // together; the sums run in partition order.
-    constexpr uint32_t U = 8, NU = (kCols * HD / 4 + 255) / 256;
-    for (uint32_t u0 = 0; u0 < NU; u0++) {
-        const uint32_t u = tid + 256u * u0;
-        if (u >= ncols * q4) break;
-        const uint32_t c = u / q4, d = 4u * (u - c * q4);
-        const float* ml = a.part_ml + 2 * (base * kCols + c);
-        const f32x4* op = reinterpret_cast<const f32x4*>(a.part_o + (base * kCols + c) * HD + d);
-        float M = kFloor;
-        if (n_parts > U) {  // long merges: the maximum first
-            for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
-                float mv[U];
-#pragma unroll
-                for (uint32_t k = 0; k < U; k++) mv[k] = p0 + k < n_parts ? ml[(p0 + k) * mstep] : kFloor;
-#pragma unroll
-                for (uint32_t k = 0; k < U; k++) M = fmaxf(M, mv[k]);
-            }
-        }
-        float L = 0.0f;
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t p0 = 0; p0 < n_parts; p0 += U) {
-            float mv[U], lv[U];
-            f32x4 ov[U];
-#pragma unroll
-            for (uint32_t k = 0; k < U; k++) {
-                const bool in = p0 + k < n_parts;
-                mv[k] = in ? ml[(p0 + k) * mstep] : kFloor;
-                lv[k] = in ? ml[(p0 + k) * mstep + 1] : 0.0f;
-                ov[k] = in ? op[(p0 + k) * ostep / 4] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-            if (n_parts <= U) {
-#pragma unroll
-                for (uint32_t k = 0; k < U; k++) M = fmaxf(M, mv[k]);
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < U; k++) {
-                if (p0 + k >= n_parts) break;
-                const float w = fast_exp2(mv[k] - M);
-                L += w * lv[k];
-                acc += w * ov[k];
-            }
-        }
-        const float inv = 1.0f / L;
-        const float yv[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-        const uint32_t rr = c / H, hh = c - rr * H;
-        store_y<4, FULL>(a, r0 + rr, kvh * a.nq_per_kv + h0 + hh, d, yv);
-    }
+    merge_group<HD, FULL, 256, false>(a, E[0], E[1], E[2], E[3], n_parts, E[5], blockIdx.y, threadIdx.x);
 }
 
 // Chunked prefill (and any sequence chunk that needs more than one group).
@@ -2304,12 +2372,19 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         }
         blob.insert(blob.end(), best.begin(), best.end());
     }
-    // The groups the merge kernel combines (more than one partition).
+    // The groups of more than one partition: decode groups first (their
+    // last partition's workgroup combines them where the launch has merge
+    // counters), then the prefill blocks' groups (always the merge kernel).
     const size_t merge_off = blob.size();
-    for (uint32_t gi = 0; gi < n_groups; gi++) {
-        const uint32_t* G = groups.data() + static_cast<size_t>(gi) * kGroupWords;
-        if (G[7] > 1) blob.insert(blob.end(), {G[0], G[1], G[2], G[3], G[7], G[10], 0u, 0u});
-    }
+    uint32_t n_merge_dec = 0;
+    for (int blk = 0; blk < 2; blk++)
+        for (uint32_t gi = 0; gi < n_groups; gi++) {
+            const uint32_t* G = groups.data() + static_cast<size_t>(gi) * kGroupWords;
+            if (G[7] > 1 && in_block[gi] == (blk == 1)) {
+                blob.insert(blob.end(), {G[0], G[1], G[2], G[3], G[7], G[10], 0u, 0u});
+                n_merge_dec += blk == 0;
+            }
+        }
     const uint32_t n_merge = static_cast<uint32_t>((blob.size() - merge_off) / kMergeWords);
     plan.blob.swap(blob);
     plan.uploaded = false;
@@ -2320,6 +2395,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     plan.n_slots = n_slots;
     plan.split = any_split;
     plan.n_merge = n_merge;
+    plan.n_merge_dec = n_merge_dec;
     plan.merge_off = static_cast<uint32_t>(merge_off);
     plan.hd_t = hd_t;
     plan.wide = wide;
@@ -2433,11 +2509,15 @@ uint64_t partial_bytes(const thb_pool* pool, const AttnPlan& plan, uint64_t* o_b
 
 // Launches attention (and, when app is set, the fused append) for a plan
 // whose blob is at `blob` on the device, with the split-K partial results
-// (when the plan splits) at `part`.  With rope set, the query is rotated as
-// it is loaded (and the fused append rotates the key); meta is the row meta
-// of the call's first row.
+// (when the plan splits) at `part`.  With merge_cnt (zeroed counters, one
+// per decode item and KV head, left zero again), each split decode group is
+// combined by the workgroup of its last partition; without, by the merge
+// kernel after the launch.  With rope set, the query is rotated as it is
+// loaded (and the fused append rotates the key); meta is the row meta of
+// the call's first row.
 void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const thb_attn_spec& sp, const AttnPlan& plan,
-                 bool fused_append, const uint32_t* meta, const uint32_t* blob, uint8_t* part, hipStream_t s) {
+                 bool fused_append, const uint32_t* meta, const uint32_t* blob, uint8_t* part, uint32_t* merge_cnt,
+                 hipStream_t s) {
     const thb_rope* rope = io.rope;
     const uint32_t hd = pool->geom[layer].head_dim;
     const uint32_t hd_t = plan.hd_t;
@@ -2467,6 +2547,7 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.src_dtype = fused_append ? io.src_dtype : 0u;
     a.part_o = part_o;
     a.part_ml = part_ml;
+    a.merge_cnt = plan.split ? merge_cnt : nullptr;
     a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
     a.max_pages = pool->arena.a.max_pages();
     a.page_shift = pool->page_shift;
@@ -2510,8 +2591,10 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
         launch_prefill(hd_t, f16, dim3(static_cast<uint32_t>(n_pwg)), a, s);
         THB_HIP(hipGetLastError());
     }
-    if (plan.split) {
-        launch_merge(hd_t, dim3(plan.n_merge, pool->kv_heads), a, s);
+    const uint32_t m0 = a.merge_cnt ? plan.n_merge_dec : 0u;  // records the launch above combined
+    if (plan.split && plan.n_merge > m0) {
+        a.merge_groups = blob + plan.merge_off + static_cast<size_t>(m0) * kMergeWords;
+        launch_merge(hd_t, dim3(plan.n_merge - m0, pool->kv_heads), a, s);
         THB_HIP(hipGetLastError());
     }
 }
@@ -2575,8 +2658,11 @@ int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_a
         uint64_t o_bytes = 0;
         const uint64_t pb = partial_bytes(pool, *plan, &o_bytes);
         uint8_t* part = pb ? static_cast<uint8_t*>(pool->partials.reserve(pb, false)) : nullptr;
+        uint32_t* cnt = plan->n_merge_dec ? static_cast<uint32_t*>(pool->merge_cnt.reserve(
+                                                static_cast<size_t>(plan->n_items) * pool->kv_heads * 4, true))
+                                          : nullptr;
         if (!append) {
-            launch_plan(pool, layer, *io, *spec, *plan, false, meta, blob, part, s);
+            launch_plan(pool, layer, *io, *spec, *plan, false, meta, blob, part, cnt, s);
             return THB_OK;
         }
         // The row meta's sequence must be the one the append uses: a fixed
@@ -2586,7 +2672,7 @@ int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_a
             for (uint32_t r = spec->row_off; r < spec->row_off + spec->m && fuse; r++)
                 fuse = rows->host[8 * r + 1] == spec->seq;
         if (fuse) {
-            launch_plan(pool, layer, *io, *spec, *plan, true, meta, blob, part, s);
+            launch_plan(pool, layer, *io, *spec, *plan, true, meta, blob, part, cnt, s);
             return THB_OK;
         }
         const int rc = rope ? thb_kv_store_rope(pool, layer, io->k_src_dev, io->v_src_dev, io->src_dtype, rope, rows,
@@ -2594,7 +2680,7 @@ int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_a
                             : thb_kv_store(pool, layer, io->k_src_dev, io->v_src_dev, io->src_dtype, rows,
                                            spec->row_off, spec->m, stream);
         if (rc) return rc;
-        launch_plan(pool, layer, *io, *spec, *plan, false, meta, blob, part, s);
+        launch_plan(pool, layer, *io, *spec, *plan, false, meta, blob, part, cnt, s);
         return THB_OK;
     });
 }
@@ -2721,7 +2807,7 @@ extern "C" int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q, v
         const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
         const uint32_t* meta = rows->dev + 8 * static_cast<size_t>(spec->row_off);
         launch_plan(pool, layer, io, *spec, *plan, false, meta, reinterpret_cast<const uint32_t*>(scr),
-                    scr + THB_NOALLOC_PLAN_BYTES, s);
+                    scr + THB_NOALLOC_PLAN_BYTES, nullptr, s);
         return THB_OK;
     });
 }
@@ -2736,6 +2822,7 @@ struct thb_dplan {
     thb_attn_spec spec{};
     const thb_rows* rows = nullptr;
     thb::DevBuf blob, part;
+    thb::DevBuf cnt;  // merge counters (one per item slot and KV head), zero between launches
 };
 
 namespace {
@@ -2756,6 +2843,7 @@ void dplan_shape(const thb_dplan* p, uint32_t hd, AttnPlan& a) {
     a.hd_t = template_hd(hd);
     a.split = p->pmax > 1;
     a.n_merge = p->gmax;
+    a.n_merge_dec = p->gmax;
     a.merge_off = p->merge_off;
 }
 
@@ -2799,7 +2887,10 @@ int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan
         dplan_shape(p.get(), p->hd_max, shape);
         uint64_t o_bytes = 0;
         const uint64_t pb = partial_bytes(pool, shape, &o_bytes);
-        if (pb) p->part.reserve(pb, false);
+        if (pb) {
+            p->part.reserve(pb, false);
+            p->cnt.reserve(static_cast<size_t>(shape.n_items) * pool->kv_heads * 4, true);
+        }
         *out = p.release();
         return THB_OK;
     });
@@ -2874,7 +2965,7 @@ int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q, void* y, const
         const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
         const uint32_t* meta = plan->rows->dev + 8 * static_cast<size_t>(plan->spec.row_off);
         launch_plan(pool, layer, io, plan->spec, shape, false, meta, static_cast<const uint32_t*>(plan->blob.get()),
-                    static_cast<uint8_t*>(plan->part.get()), s);
+                    static_cast<uint8_t*>(plan->part.get()), static_cast<uint32_t*>(plan->cnt.get()), s);
         return THB_OK;
     });
 }

@@ -40,6 +40,7 @@ struct AttnPlan {
     bool mixed = false;  // decode items and prefill blocks run as one launch (attn_mixed)
     bool split = false;  // some group spans several partitions: merge kernel runs
     uint32_t n_merge = 0, merge_off = 0;  // groups of several partitions: count, blob offset (words)
+    uint32_t n_merge_dec = 0;             // of those, decode groups (listed first)
     bool fusable = false;  // an append of the call's rows can run inside the launch
     std::vector<uint32_t> blob;  // [groups | items | row ranges | prefill items | order | merge list]
     DevBuf dev;                  // blob on the device, when uploaded
@@ -104,6 +105,7 @@ struct thb_pool {
     thb::DevBuf copy_buf;            // copy triples
     thb::DevBuf geom_buf;            // per-layer DevLayer records
     thb::DevBuf partials;            // split-K partial results
+    thb::DevBuf merge_cnt;           // arrival counters of split decode groups (zero between launches)
     thb::DevBuf run_buf;             // append runs of the last row meta the append cut into runs
     thb::DevBuf range_buf;           // work items and range records of a batched gather / scatter
     std::vector<uint32_t> range_key; // what range_buf holds

@@ -247,6 +247,64 @@ def test_invariants_bit_exact(torch_cuda):
     assert torch.equal(again, ya), "repeatable"
 
 
+SPLIT_CASES = [
+    # name, nq, nkv, hd, kv, lens, part_len, window, softcap
+    ("hd128-32-partitions", 32, 8, 128, "f16", [1100, 700, 64, 300], 64, 0, 0.0),
+    ("hd256-window-softcap", 16, 8, 256, "f16", [2100, 900], 256, 1000, 50.0),
+    ("hd512-tree-merge", 8, 2, 512, "f16", [900, 400], 128, 0, 0.0),
+    ("g32-head-split-bf16", 32, 1, 128, "bf16", [800, 333], 128, 0, 0.0),
+]
+
+
+def _attn_noalloc(torch, pool, q, y, spec):
+    import ctypes
+
+    from flint_amd import _lib, ops
+    from flint_amd.pool import _stream_ptr
+
+    c = ops._spec_c(spec, q, y)
+    rc = _lib.lib().thb_attn_noalloc(pool.handle, 0, q.data_ptr(), y.data_ptr(), ctypes.byref(c), spec.args.handle,
+                                     _stream_ptr(None))
+    assert rc == 0, _lib.lib().thb_last_error().decode()
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_split_groups_combined_in_launch(torch_cuda, case):
+    """Decode groups split over many partitions are combined by the
+    workgroup of each group's last partition (thb_attn): parity with the
+    oracle, and bit-identical to the combination by the merge kernel after
+    the launch (thb_attn_noalloc), over calls of different shapes in a row
+    (the arrival counters are left at zero for the next call)."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    name, nq, nkv, hd, kv, lens, part_len, window, cap = case
+    say("split groups", name)
+    rng = random.Random(zlib.crc32(name.encode()))
+    pool = make_pool(lens, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype=kv, extra_pages=7, part_len=part_len)
+    scattered_alloc(pool, lens, rng, 16)
+    rows = RowMeta(256)
+    fill(torch, pool, rows, lens, seed=41)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(41)
+    n = len(lens)
+    calls = [(list(range(n)), [x - 1 for x in lens]),
+             ([0, 0, 0, 0], [lens[0] - 4 + i for i in range(4)]),  # a 4-row verify chunk
+             ([n - 1, 0], [lens[-1] // 2, lens[0] - 1]),
+             (list(range(n)), [x - 1 for x in lens])]
+    for i, (seqs, positions) in enumerate(calls):
+        m = len(seqs)
+        q = torch.randn(m, nq, hd, device="cuda", generator=g)
+        y = check_parity(torch, pool, rows, q, positions, seqs, f"{name} call {i}", window=window, softcap=cap)
+        spec = ops.AttnSpec(q_heads=nq, window=window, scale=1.0 / math.sqrt(hd), m=m, causal=True, seq=None,
+                            args=rows, softcap=cap)
+        y2 = torch.full_like(y, float("nan"))
+        _attn_noalloc(torch, pool, q, y2, spec)
+        assert torch.equal(y, y2), (name, i, float((y - y2).abs().max()))
+
+
 def test_llama3_full_shape_sampled(torch_cuda):
     """BASELINE config 2 at full size (B=32, ctx 4096, 32q/8kv/hd128, f16 KV,
     scattered block tables): the oracle checks 3 sequences in full, and every
