@@ -752,22 +752,33 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
     auto app_store = [&](uint32_t pos, bool is_v, uint32_t d, const uint4& w) {
         app_store_at(s_page[(pos - pbeg) >> pshift], pos, is_v, d, w);
     };
-    uint32_t app_pos = 0, app_d = 0;
-    uint64_t app_e = 0;
-    bool app_v = false, app_own = false;
-    Raw8 app_raw{};
+    // The first kAppLane items of each lane (items lane + 64 k): their
+    // positions, and the sources of the items this wave owns, are loaded
+    // beside the query loads, before the barrier (the source loads overlap
+    // the page-table round trips the barrier waits for); the owning lanes
+    // encode and store them after the barrier, before the first tile load.
+    // A 4-row verify chunk at head_dim 256 (256 items, all in one wave's
+    // run) thus costs one round trip instead of four in a row.  The tile
+    // loop then holds no store.
+    constexpr int kAppLane = 4;
+    uint32_t app_pos[kAppLane], app_d[kAppLane];
+    uint64_t app_e[kAppLane];
+    bool app_v[kAppLane], app_own[kAppLane];
+    Raw8 app_raw[kAppLane];
     const bool rope = FULL && a.rope_on;
-    // First item of each lane: its position and its source (whose address
-    // does not depend on the position) are loaded beside the query loads in
-    // every wave, before the barrier, so no wave waits a second round trip;
-    // the owning lane encodes and stores it after the barrier, before the
-    // first tile load.  The tile loop then holds no store.
-    if (lane < app_items && !rope) {
-        app_own = app_decode(lane, app_pos, app_v, app_d, app_e);
-        app_raw = load_raw8_rt(a.src_dtype, app_v ? a.v_src : a.k_src, app_e);
+#pragma unroll
+    for (int k = 0; k < kAppLane; k++) {
+        const uint32_t t = lane + 64u * k;
+        app_own[k] = false;
+        if (t < app_items && !rope) {
+            app_own[k] = app_decode(t, app_pos[k], app_v[k], app_d[k], app_e[k]);
+            if (app_own[k]) app_raw[k] = load_raw8_rt(a.src_dtype, app_v[k] ? a.v_src : a.k_src, app_e[k]);
+        }
     }
     __syncthreads();
-    if (app_own) app_store(app_pos, app_v, app_d, encode8_rt<KVE>(a.src_dtype, app_raw));
+#pragma unroll
+    for (int k = 0; k < kAppLane; k++)
+        if (app_own[k]) app_store(app_pos[k], app_v[k], app_d[k], encode8_rt<KVE>(a.src_dtype, app_raw[k]));
     if (rope) {
         if (app_items != 0) {
             // Rotary append: the key head of each row this wave owns, one chunk
@@ -797,8 +808,8 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
             }
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         }
-    } else if (app_items > 64) {
-        for (uint32_t t = lane + 64; t < app_items; t += 64) {
+    } else if (app_items > 64u * kAppLane) {
+        for (uint32_t t = lane + 64u * kAppLane; t < app_items; t += 64) {
             uint32_t pos2, d2;
             uint64_t e2;
             bool v2;
