@@ -20,9 +20,10 @@
 //    weight byte is read once (non-temporal), x comes from L2.  The 8 waves'
 //    partial sums are added through LDS in wave order: one launch, no
 //    atomics, deterministic.
-//  * gemm_split + gemm_merge (rows 17..64): K in slices of 1024, x's slice
-//    staged once per workgroup in LDS, partial sums merged in slice order
-//    by a second kernel (the reference's split-K merge_gemm.wgsl order).
+//  * gemm_split (rows 17..64): K in slices of 1024, x's slice staged once
+//    per workgroup in LDS; the workgroup that finishes a column block's last
+//    slice adds the block's partial sums in slice order (the reference's
+//    split-K merge_gemm.wgsl order), in the same launch.
 //  * gemm_tile (rows > 64, prefill): 128 x 128 output tiles, 4 waves of
 //    64 x 64, k-tiles of 64 staged in double-buffered LDS (rows of 144
 //    bytes: conflict-free 16-byte operand reads), the next tile's loads in
@@ -320,13 +321,34 @@ __global__ __launch_bounds__(256) void gemm_tile(GemmArgs a) {
 // did not overlap the 7.5 us weight stream; split: 12.2 us + the merge,
 // against 16.3 us in one pass).  Wave w: n-tile
 // w % 4, half w / 4 of the slice's k-steps, every weight load issued before
-// the first product.  Partial sums go to part[q][m][n]; gemm_merge adds them
-// in slice order.
+// the first product.  Partial sums go to part[q][m][n] (agent-scope
+// atomic stores, coherent across the XCDs' L2 caches); the workgroup that
+// finishes the column block's last slice (an arrival counter per block,
+// relaxed agent-scope add after every thread's stores have completed) adds
+// the block's slices in order, y = (acc ? y : 0) + part[0] + part[1] + ...,
+// and clears the counter for the next call.  No workgroup waits for
+// another.
 struct SplitArgs {
     GemmArgs g;
-    float* part;  // [S][m][n]
+    float* part;    // [S][m][n]
+    uint32_t* cnt;  // [n / 64] arrival counters, zero between launches
     uint32_t S, m16;
 };
+
+__device__ inline void publish4(float* p, const f32x4& v) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(p);
+    __hip_atomic_store(q, (uint64_t(__float_as_uint(v[1])) << 32) | __float_as_uint(v[0]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, (uint64_t(__float_as_uint(v[3])) << 32) | __float_as_uint(v[2]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline f32x4 coherent4(const float* p) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return f32x4{__uint_as_float(static_cast<uint32_t>(lo)), __uint_as_float(static_cast<uint32_t>(lo >> 32)),
+                 __uint_as_float(static_cast<uint32_t>(hi)), __uint_as_float(static_cast<uint32_t>(hi >> 32))};
+}
 
 template <uint32_t XT, bool WF16, int MT>
 __global__ __launch_bounds__(512) void gemm_split(SplitArgs sa) {
@@ -430,29 +452,37 @@ __global__ __launch_bounds__(512) void gemm_split(SplitArgs sa) {
             const uint32_t row = 16u * t + c;
             if (row < a.m) {
                 const f32x4 s = d[t] + red[(nt * MT + t) * 64u + lane];
-                *reinterpret_cast<f32x4*>(sa.part + (static_cast<uint64_t>(q) * a.m + row) * a.n + n0 + 4u * g) = s;
+                publish4(sa.part + (static_cast<uint64_t>(q) * a.m + row) * a.n + n0 + 4u * g, s);
             }
         }
     }
-}
-
-// y = (acc ? y : 0) + part[0] + part[1] + ... in slice order, as the
-// reference's merge_gemm.wgsl adds its segments; 4 columns per thread.
-__global__ __launch_bounds__(256) void gemm_merge(const float* part, float* y, uint32_t mn4, uint32_t S, uint32_t acc) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= mn4) return;
-    const f32x4* p = reinterpret_cast<const f32x4*>(part) + i;
-    f32x4 s = acc ? reinterpret_cast<const f32x4*>(y)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t q0 = 0; q0 < S; q0 += 8) {  // 8 slices requested at once, added in order
-        f32x4 v[8];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
+    __shared__ uint32_t s_arrived;
+    __syncthreads();
+    uint32_t* cnt = sa.cnt + blockIdx.x;
+    if (tid == 0) s_arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived + 1u != sa.S) return;
+    // The block's last slice: y[row][64 blockIdx.x + 4 u .. + 4] for every
+    // row, 8 slices requested at once and added in slice order.
+    const uint64_t mn = static_cast<uint64_t>(a.m) * a.n;
+    for (uint32_t u = tid; u < a.m * 16u; u += 512u) {
+        const uint32_t row = u >> 4;
+        const uint64_t idx = static_cast<uint64_t>(row) * a.n + 64u * blockIdx.x + 4u * (u & 15u);
+        f32x4* yp = reinterpret_cast<f32x4*>(a.y + idx);
+        f32x4 acc = a.acc ? *yp : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t q0 = 0; q0 < sa.S; q0 += 8) {
+            f32x4 v[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (q0 + j < S) v[j] = p[static_cast<uint64_t>(q0 + j) * mn4];
+            for (int j = 0; j < 8; j++)
+                if (q0 + j < sa.S) v[j] = coherent4(sa.part + (q0 + j) * mn + idx);
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (q0 + j < S) s += v[j];
+            for (int j = 0; j < 8; j++)
+                if (q0 + j < sa.S) acc += v[j];
+        }
+        *yp = acc;
     }
-    reinterpret_cast<f32x4*>(y)[i] = s;
+    if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // k-steps of 32 per slice of the split kernel (half that with a low part).
@@ -464,6 +494,7 @@ __global__ __launch_bounds__(256) void gemm_merge(const float* part, float* y, u
 // reference's backend keeps gemm_partial the same way, matmul.rs:9-18).
 constexpr int kMaxDev = 64;
 DevBuf g_part[kMaxDev];
+DevBuf g_cnt[kMaxDev];  // split kernel's arrival counters (zero between launches)
 std::mutex g_part_mu;
 
 template <uint32_t XT, bool WF16>
@@ -505,13 +536,16 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     THB_HIP(hipGetDevice(&dev));
     if (dev < 0 || dev >= kMaxDev) throw HipError{hipErrorInvalidDevice, "gemm partial buffer"};
     float* part;
+    uint32_t* cnt;
     {
         std::lock_guard<std::mutex> lock(g_part_mu);
         part = static_cast<float*>(g_part[dev].reserve(static_cast<size_t>(S) * a.m * a.n * 4, false));
+        cnt = static_cast<uint32_t*>(g_cnt[dev].reserve(static_cast<size_t>(a.n / 64) * 4, true));
     }
     SplitArgs sa;
     sa.g = a;
     sa.part = part;
+    sa.cnt = cnt;
     sa.S = S;
     sa.m16 = m16;
     const dim3 grid(a.n / 64, S);
@@ -524,8 +558,6 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     else
         hipLaunchKernelGGL((gemm_split<XT, WF16, 4>), grid, dim3(512), lds, s, sa);
     THB_HIP(hipGetLastError());
-    const uint32_t mn4 = a.m * a.n / 4;
-    hipLaunchKernelGGL(gemm_merge, dim3((mn4 + 255) / 256), dim3(256), 0, s, part, a.y, mn4, S, a.acc);
 }
 
 template <bool WF16>
