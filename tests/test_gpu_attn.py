@@ -368,6 +368,11 @@ FUSE_CASES = [
     # workgroups, and both store the row's token (the same bytes)
     ("decode-mqa32-two-groups", 32, 1, 128, "f16", "f16", 1, True),
     ("prefill40-fallback", 8, 2, 128, "f16", "bf16", 40, False),
+    # verify chunks of 8 rows (two groups of 4 query heads per row), and of
+    # 16 rows at head_dim 256: 1024 append items per group, more than the
+    # first pass over the wave's lanes takes
+    ("verify8-g2-f32src", 16, 8, 128, "f16", "f32", 8, True, [704, 1496, 41]),
+    ("verify16-hd256", 8, 8, 256, "f16", "f16", 16, True, [512, 1200, 47]),
 ]
 
 
@@ -379,9 +384,9 @@ def test_fused_append_matches_separate_calls(torch_cuda, case):
     from flint_amd import ops
     from flint_amd.pool import RowMeta
 
-    name, nq, nkv, hd, kv, src, rps, _ = case
+    name, nq, nkv, hd, kv, src, rps, _ = case[:8]
     say("fused append", name)
-    lens = [700, 1500, 33]  # tokens already in the cache
+    lens = case[8] if len(case) > 8 else [700, 1500, 33]  # tokens already in the cache
     budget = [n + rps for n in lens]
     pools = []
     for _ in range(2):
