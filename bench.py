@@ -265,7 +265,7 @@ def time_o_proj(torch, ops, dev, B, nq, hd, layers=32, reps=5):
             "bytes_per_call": nbytes,
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                          "frac": round(gbps / PEAK_HBM_GBPS, 4)},
-            "note": f"thb_gemm_acc (gemm_skinny): y[{B}, {hidden}] += x[{B}, {hidden}] bf16 . W[{hidden}, {hidden}]^T "
+            "note": f"thb_gemm_acc (gemm_split at 17-64 rows): y[{B}, {hidden}] += x[{B}, {hidden}] bf16 . W[{hidden}, {hidden}]^T "
                     f"bf16, acc into f32, distinct W per layer, graph of {layers} calls; bytes = W + x + y read/write"}
 
 
