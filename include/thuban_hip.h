@@ -261,11 +261,15 @@ typedef struct thb_attn_spec {
 /* ops::attn (ops/attn.rs:18-51) / attn.wgsl:53-365.  q, y: [m, q_heads,
  * head_dim], 16-byte aligned.  Key ranges per row follow attn.wgsl:78-88,169
  * exactly.  One launch covers every row (batched over sequences), as a
- * split-K pass with a deterministic log-sum-exp merge (a second kernel when a
- * row's keys span several part_len partitions): output is independent of
- * physical page placement and of the other rows in the batch.  Products on
- * the matrix cores with q and p split into high and low halves, f32
- * accumulation; within 2e-3 of an exact softmax. */
+ * split-K pass with a deterministic log-sum-exp merge when a row's keys span
+ * several part_len partitions (in the same launch, by the workgroup that
+ * finishes the group's last partition; a second kernel for prefill blocks):
+ * output is independent of physical page placement and of the other rows in
+ * the batch.  Products on the matrix cores with q and p split into high and
+ * low halves, f32 accumulation; within 2e-3 of an exact softmax.  The pool
+ * holds the split-K partial results and the merge counters: calls on one
+ * pool run in stream order, and calls on one pool from several streams at
+ * once race. */
 int thb_attn(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
              const thb_rows* rows, void* stream);
 
@@ -374,7 +378,9 @@ int thb_check_gemm_dims(uint32_t n, uint32_t k);
  * THB_DT_F16; y: f32; all 16-byte aligned; n and k as thb_check_gemm_dims.
  * Products on the matrix cores in f32 accumulation; an x wider than the
  * weight type is split into high and low parts (f32-grade products).
- * Deterministic: the same inputs give the same bits. */
+ * Deterministic: the same inputs give the same bits.  At 17-64 rows the
+ * split-K partial sums and their merge counters live in one buffer per
+ * device: calls on one device from several streams at once race. */
 int thb_gemm_acc(const void* x_dev, uint32_t x_dtype, const void* w_dev, uint32_t w_dtype, float* y_dev,
                  uint32_t rows, uint32_t n, uint32_t k, uint32_t acc, void* stream);
 
