@@ -710,11 +710,20 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
     }
 
 
-    // This wave's run of 16-token tiles inside [tb, te).
+    // This wave's run of 16-token tiles inside [tb, te).  For groups of
+    // several rows, and with the rotary embedding, runs are handed out last
+    // key first: wave 0 takes the run that ends at te, which holds the rows'
+    // new tokens, so a fused append's stores (~3.5 us for a 4-row verify
+    // chunk at head_dim 256) delay the older wave of its SIMD pair, which
+    // the SIMD's issue arbiter favours (over equal runs the younger waves
+    // 4-7 take 9-14% longer).  The order depends on the group and the call's
+    // kind only, not on whether the append is fused, so fused and separate
+    // calls stay bit-identical.
     const uint32_t tb16 = tb & ~15u;
     const uint32_t span = te > tb16 ? te - tb16 : 0u;
     const uint32_t run = ((span + W - 1) / W + 15u) & ~15u;
-    const uint32_t ws = tb16 + wave * run;
+    const bool last_first = R > 1 || (FULL && a.rope_on);
+    const uint32_t ws = tb16 + (last_first ? W - 1u - wave : wave) * run;
     const uint32_t we = min(ws + run, te);
 
     // Fused append (thb_attn_append).  A row's new token sits at position
