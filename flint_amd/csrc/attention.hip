@@ -58,6 +58,20 @@ constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units)
 constexpr float kFloor = -1.0e30f;    // initial running max (finite on purpose)
 constexpr uint32_t kGroupWords = 11;  // r0, R, h0, H, seq, lo, hi, n_parts, base, plen, item0
 constexpr uint32_t kMaxPartPages = 1024;
+
+// Partitions of a key span (a function of the span only, so a group's
+// arithmetic does not depend on the rest of the call): ceil(span / PL)
+// rounded up to a power of two, as n_parts equal pieces of plen keys (a
+// multiple of align), the last one shorter.  Rounding down instead (pieces
+// up to ~2 PL) measured faster on Gemma-2's global layers and slower on the
+// ragged Qwen3 batch and the 131072-token Qwen2.5 contexts.
+__host__ __device__ inline void part_split(uint64_t span, uint32_t PL, uint32_t align, uint32_t& n_parts,
+                                           uint32_t& plen) {
+    uint32_t n = static_cast<uint32_t>((span + PL - 1) / PL);
+    if (n > 1) n = 1u << (32 - __builtin_clz(n - 1));
+    plen = static_cast<uint32_t>(((span + n - 1) / n + align - 1) / align * align);
+    n_parts = static_cast<uint32_t>((span + plen - 1) / plen);
+}
 // Raw buffer resources (decode tile loads): word 3 of a gfx9 descriptor
 // with a 32-bit data format (untyped loads need a nonzero one), the
 // non-temporal cache-policy bit of a buffer load, and an offset that is out
@@ -1820,11 +1834,7 @@ __device__ inline void dplan_partition(uint32_t& lo, uint32_t& hi, uint32_t PL, 
         return;
     }
     base = lo & ~(align - 1);
-    const uint64_t span = uint64_t(hi) - base;
-    n_parts = static_cast<uint32_t>((span + PL - 1) / PL);
-    if (n_parts > 1) n_parts = 1u << (32 - __builtin_clz(n_parts - 1));
-    plen = static_cast<uint32_t>(((span + n_parts - 1) / n_parts + align - 1) / align * align);
-    n_parts = static_cast<uint32_t>((span + plen - 1) / plen);
+    part_split(uint64_t(hi) - base, PL, align, n_parts, plen);
 }
 
 // Inclusive sum over the workgroup; *total gets the sum.  Every thread calls it.
@@ -2197,10 +2207,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
             base = lo & ~(align - 1);
             const uint64_t span = uint64_t(hi) - base;
             max_span = std::max(max_span, span);
-            n_parts = static_cast<uint32_t>((span + PL - 1) / PL);
-            if (n_parts > 1) n_parts = 1u << (32 - __builtin_clz(n_parts - 1));
-            plen = static_cast<uint32_t>(((span + n_parts - 1) / n_parts + align - 1) / align * align);
-            n_parts = static_cast<uint32_t>((span + plen - 1) / plen);
+            part_split(span, PL, align, n_parts, plen);
         }
         max_parts = std::max(max_parts, n_parts);
         any_split = any_split || n_parts > 1;
