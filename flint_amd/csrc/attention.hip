@@ -13,7 +13,8 @@
 //    size) is cut into n equal partitions, n = ceil(span / part_len) rounded
 //    up to a power of two (so that groups of similar spans tile the 256 CUs
 //    evenly: 3 partitions per group on 128 groups leave half the CUs idle
-//    for the last third of the launch, 4 do not).  One
+//    for the last third of the launch, 4 do not; a span a few keys over
+//    k * part_len, k >= 2, takes k slightly longer partitions).  One
 //    workgroup of W waves handles one (group, partition, KV head); the waves
 //    split the partition into W contiguous runs of 16-token tiles.  All
 //    boundaries depend only on the group's own key range, so a row's
@@ -48,6 +49,7 @@
 
 #include "codec.hpp"
 #include "layout.hpp"
+#include "partition.hpp"
 #include "pool.hpp"
 #include "rope.hpp"
 
@@ -58,20 +60,10 @@ constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units)
 constexpr float kFloor = -1.0e30f;    // initial running max (finite on purpose)
 constexpr uint32_t kGroupWords = 11;  // r0, R, h0, H, seq, lo, hi, n_parts, base, plen, item0
 constexpr uint32_t kMaxPartPages = 1024;
+// Longest part_len in pages: its partitions, up to part_len + part_len / 64
+// rounded up to the alignment, fit kMaxPartPages pages.
+constexpr uint32_t kMaxPartLenPages = kMaxPartPages - kMaxPartPages / 64;
 
-// Partitions of a key span (a function of the span only, so a group's
-// arithmetic does not depend on the rest of the call): ceil(span / PL)
-// rounded up to a power of two, as n_parts equal pieces of plen keys (a
-// multiple of align), the last one shorter.  Rounding down instead (pieces
-// up to ~2 PL) measured faster on Gemma-2's global layers and slower on the
-// ragged Qwen3 batch and the 131072-token Qwen2.5 contexts.
-__host__ __device__ inline void part_split(uint64_t span, uint32_t PL, uint32_t align, uint32_t& n_parts,
-                                           uint32_t& plen) {
-    uint32_t n = static_cast<uint32_t>((span + PL - 1) / PL);
-    if (n > 1) n = 1u << (32 - __builtin_clz(n - 1));
-    plen = static_cast<uint32_t>(((span + n - 1) / n + align - 1) / align * align);
-    n_parts = static_cast<uint32_t>((span + plen - 1) / plen);
-}
 // Raw buffer resources (decode tile loads): word 3 of a gfx9 descriptor
 // with a 32-bit data format (untyped loads need a nonzero one), the
 // non-temporal cache-policy bit of a buffer load, and an offset that is out
@@ -2185,9 +2177,9 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
 
     // Partitions of a group (or of a prefill block) start at its first key
     // (rounded down to the page and tile size) and split its span into
-    // n equal parts, n = ceil(span / part_len) rounded up to a power of two
-    // (then lowered if the aligned part length leaves trailing parts empty):
-    // a function of its own key range only.
+    // n equal parts (part_split: n = ceil(span / part_len) rounded up to a
+    // power of two, then lowered if the aligned part length leaves trailing
+    // parts empty): a function of its own key range only.
     std::vector<uint32_t> groups, items, blocks, bitems;
     const uint32_t PL = pool->part_len;
     const uint32_t align = std::max<uint32_t>(pool->page_len, 16);
@@ -2473,8 +2465,8 @@ int check_attn_call(thb_pool* pool, uint32_t layer, const void* q, void* y, cons
     if (sp.seq != THB_SEQ_PER_ROW && sp.seq >= pool->arena.a.seqs())
         return fail(THB_ERR_INVALID, "sequence " + std::to_string(sp.seq) + " out of range");
     if (!(sp.softcap >= 0.0f)) return fail(THB_ERR_INVALID, "softcap must be >= 0");
-    if (pool->part_len >> pool->page_shift > kMaxPartPages)
-        return fail(THB_ERR_CONFIG, "part_len / page_len must be at most " + std::to_string(kMaxPartPages));
+    if (pool->part_len >> pool->page_shift > kMaxPartLenPages)
+        return fail(THB_ERR_CONFIG, "part_len / page_len must be at most " + std::to_string(kMaxPartLenPages));
     return THB_OK;
 }
 
@@ -2887,8 +2879,8 @@ int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan
     if (q_heads == 0 || q_heads % pool->kv_heads != 0)
         return fail(THB_ERR_CONFIG, "q_heads " + std::to_string(q_heads) + " must be a positive multiple of kv_heads " +
                                         std::to_string(pool->kv_heads));
-    if (pool->part_len >> pool->page_shift > kMaxPartPages)
-        return fail(THB_ERR_CONFIG, "part_len / page_len must be at most " + std::to_string(kMaxPartPages));
+    if (pool->part_len >> pool->page_shift > kMaxPartLenPages)
+        return fail(THB_ERR_CONFIG, "part_len / page_len must be at most " + std::to_string(kMaxPartLenPages));
     return guarded([&]() -> int {
         auto p = std::make_unique<thb_dplan>();
         p->pool = pool;

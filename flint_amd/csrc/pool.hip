@@ -290,9 +290,12 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
     if (d->page_len < 8 || d->page_len > 256 || (d->page_len & (d->page_len - 1)))
         return fail(THB_ERR_CONFIG, "page_len " + std::to_string(d->page_len) + " must be a power of two in [8, 256]");
     uint32_t part = d->part_len ? d->part_len : 4096;
-    if (part % 16 != 0 || part % d->page_len != 0 || part / d->page_len > 1024)
+    // At most 1008 pages: a partition may run part_len / 64 longer (a span a
+    // few keys over a multiple of part_len), and the kernels stage at most
+    // 1024 page numbers of one partition.
+    if (part % 16 != 0 || part % d->page_len != 0 || part / d->page_len > 1008)
         return fail(THB_ERR_CONFIG, "part_len " + std::to_string(part) +
-                                        " must be a multiple of 16 and of page_len, at most 1024 pages");
+                                        " must be a multiple of 16 and of page_len, at most 1008 pages");
     for (uint32_t l = 0; l < d->layers; l++) {
         uint32_t hd = d->head_dims ? d->head_dims[l] : d->head_dim;
         if (int rc = thb_backend_head_dim(hd)) return rc;

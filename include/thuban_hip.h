@@ -145,7 +145,7 @@ typedef struct thb_pool_desc {
     int64_t pages;              /* ArenaSpec.pages; < 0 = None */
     uint32_t part_len;          /* split-K partition in tokens (0 = 4096);
                                    multiple of 16 and of page_len, at most
-                                   1024 pages */
+                                   1008 pages */
     void* arena_dev;            /* optional caller-owned device memory */
     uint64_t arena_bytes;       /* its size; 0 = let the pool hipMalloc */
 } thb_pool_desc;

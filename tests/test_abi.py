@@ -118,3 +118,49 @@ def test_page_offsets_match_the_kernels_layout(tmp_path):
         assert np.array_equal(got[i:i + n, 1], v.reshape(-1)), (P, hd)
         assert np.array_equal(np.sort(k.reshape(-1)), np.arange(n)) and np.array_equal(np.sort(v.reshape(-1)), np.arange(n))
         i += n
+
+
+def test_partition_rule(tmp_path):
+    """thb::part_split (flint_amd/csrc/partition.hpp, what both planners use):
+    known answers at part_len 4096 (a span a few keys over 2 or 32 pieces
+    keeps 2 or 32; one key more than PL / 64 per piece goes to the next power
+    of two; a span just over one piece keeps two), and for every span of a
+    sweep: pieces are aligned, cover the span with no empty trailing piece, are
+    at most part_len + part_len / 64 (rounded up to the alignment) long, never
+    outnumber ceil(span / part_len) rounded up to a power of two, and at the
+    longest part_len the pool accepts (1008 pages) fit the kernels' 1024 staged
+    page numbers."""
+    import subprocess
+
+    known = {  # span -> (n_parts, plen) at part_len 4096, align 16
+        1: (1, 16), 4096: (1, 4096), 4099: (2, 2064), 8192: (2, 4096), 8196: (2, 4112), 8320: (2, 4160),
+        8321: (4, 2096), 12288: (4, 3072), 20000: (8, 2512), 131072: (32, 4096), 131073: (32, 4112),
+        131072 + 2048: (32, 4160), 131072 + 2049: (64, 2096),
+    }
+    cases = [(s, 4096, 16) for s in known]
+    for pl, align in ((64, 16), (512, 32), (4096, 16), (4096, 256), (1008 * 16, 16), (1008 * 8, 16), (1008 * 256, 256)):
+        for s in list(range(1, 3 * pl, max(1, pl // 61))) + [k * pl + d for k in range(2, 40) for d in (0, 1, pl // 64 * k,
+                                                                                                      pl // 64 * k + 1)]:
+            cases.append((s, pl, align))
+    src = tmp_path / "parts.cpp"
+    src.write_text('#include <cstdio>\n#include "partition.hpp"\nint main() {\n'
+                   f"static const unsigned long long c[][3] = {{{','.join(f'{{{s},{p},{a}}}' for s, p, a in cases)}}};\n"
+                   "for (const auto& x : c) { uint32_t n, plen; thb::part_split(x[0], (uint32_t)x[1], (uint32_t)x[2], n, plen);"
+                   ' std::printf("%u %u\\n", n, plen); }\nreturn 0; }\n')
+    exe = tmp_path / "parts"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-D__host__=", "-D__device__=", "-I",
+                    os.path.join(ROOT, "flint_amd", "csrc"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    got = [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(len(cases))]
+    for s, np_ in zip(known, got):
+        assert np_ == known[s], (s, np_)
+    for (s, pl, align), (n, plen) in zip(cases, got):
+        assert plen % align == 0 and (n - 1) * plen < s <= n * plen, (s, pl, align, n, plen)
+        assert plen <= -(-(pl + pl // 64) // align) * align, (s, pl, align, plen)
+        n_ceil = -(-s // pl)
+        assert n <= (1 << (n_ceil - 1).bit_length()), (s, pl, n)
+        if s <= pl:
+            assert n == 1
+        if pl % 1008 == 0:
+            page = pl // 1008
+            assert plen // page <= 1024, (s, pl, plen)

@@ -253,6 +253,9 @@ SPLIT_CASES = [
     ("hd256-window-softcap", 16, 8, 256, "f16", [2100, 900], 256, 1000, 50.0),
     ("hd512-tree-merge", 8, 2, 512, "f16", [900, 400], 128, 0, 0.0),
     ("g32-head-split-bf16", 32, 1, 128, "bf16", [800, 333], 128, 0, 0.0),
+    # spans a few keys over 2 and 4 pieces of 1024 (2 and 4 longer partitions) and one key past
+    # that tolerance (4 partitions)
+    ("hd128-span-tolerance", 32, 8, 128, "f16", [2050, 2081, 2080, 4100], 1024, 0, 0.0),
 ]
 
 
