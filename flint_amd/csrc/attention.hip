@@ -975,9 +975,13 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
 #pragma unroll
             for (int b = 0; b < NB; b++) {
                 const uint32_t t = t0 + 16u * b, tn = t + 16u * NB;
-                if constexpr (NB == 1) {
+                if constexpr (NB == 1 && HD < 512) {
                     // One tile in flight: the next tile's K goes out as soon
-                    // as this tile's K is consumed, its V after the PV.
+                    // as this tile's K is consumed, its V after the PV.  (At
+                    // head_dim 512 the next K beside this tile's V and the
+                    // 128 output registers spilled ~90 registers: 246 us for
+                    // a 16 x 4096-token decode, against 106 us with the whole
+                    // next tile requested after the PV, below.)
                     compute(t, kr[b], vr[b], [&]() { load_k(tn, kr[b]); });
                     load_v(tn, vr[b]);
                 } else {
