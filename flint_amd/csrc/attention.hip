@@ -138,6 +138,7 @@ struct AttnArgs {
     uint32_t* merge_cnt;
     uint64_t plane;  // 16-bit elements per head plane
     uint32_t max_pages, page_shift, q_heads, nq_per_kv, head_dim, part_len, n_kvh;
+    uint32_t pages;  // pages of the pool
     float qscale;  // scale * log2(e), or scale / softcap
     float cap2;    // softcap * log2(e), 0 = no soft-cap
     // attn_prefill_wide: the query carries qpre = the sign of qscale (an exact
@@ -606,7 +607,10 @@ __device__ __forceinline__ void merge_group(const AttnArgs& a, uint32_t r0, uint
 // stores have completed before the barrier, the counter add (relaxed, agent
 // scope) is issued after it, and the combining loads only after the add has
 // returned, so the last workgroup's loads find every partition's stores
-// done.  No workgroup waits for another.
+// done.  No workgroup waits for another.  Every partial store and merge load
+// is an agent-scope atomic (sc1 on gfx950: not held in an XCD's L2), so this
+// is the memory model's agent-scope release/acquire sequence without the L2
+// write-back and invalidate, which only plain accesses need.
 template <int HD, bool FULL, int NT>
 __device__ __forceinline__ void merge_if_last(const AttnArgs& a, uint32_t& s_arrived, uint32_t r0, uint32_t R,
                                               uint32_t h0, uint32_t H, uint32_t n_parts, uint32_t item0,
@@ -680,7 +684,8 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
         for (uint32_t i = tid; i < npg; i += 64 * W) {
             const uint32_t lp = lp0 + i;
             const bool used = tb < te && (lp << pshift) < te && ((lp + 1) << pshift) > tb;
-            s_page[i] = used ? trow[lp] : 0u;
+            const uint32_t pg = used ? trow[lp] : 0u;
+            s_page[i] = pg < a.pages ? pg : 0u;  // block_pages: a page outside the pool reads page 0
         }
     }
 
@@ -1154,7 +1159,8 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
         for (uint32_t i = tid; i < npg; i += NT) {
             const uint32_t lp = lp0 + i;
             const bool used = tb < te && (lp << pshift) < te && ((lp + 1) << pshift) > tb;
-            s_page[i] = used ? trow[lp] : 0u;
+            const uint32_t pg = used ? trow[lp] : 0u;
+            s_page[i] = pg < a.pages ? pg : 0u;  // block_pages: a page outside the pool reads page 0
         }
     }
 
@@ -1409,7 +1415,8 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
         for (uint32_t i = tid; i < npg; i += NT) {
             const uint32_t lp = lp0 + i;
             const bool used = tb < te && (lp << pshift) < te && ((lp + 1) << pshift) > tb;
-            s_page[i] = used ? trow[lp] : 0u;
+            const uint32_t pg = used ? trow[lp] : 0u;
+            s_page[i] = pg < a.pages ? pg : 0u;  // block_pages: a page outside the pool reads page 0
         }
     }
 
@@ -2477,7 +2484,7 @@ int check_attn_call(thb_pool* pool, uint32_t layer, const void* q, void* y, cons
 // Copies a plan's blob to its own device buffer (once per plan).
 void upload_plan(thb_pool* pool, AttnPlan& plan, hipStream_t s) {
     if (plan.uploaded) return;
-    void* dev = plan.dev.reserve(plan.blob.size() * 4, false);
+    void* dev = plan.dev.reserve_rewrite(plan.blob.size() * 4, false, s);
     pool->stager.upload(dev, plan.blob.data(), plan.blob.size() * 4, s);
     plan.uploaded = true;
 }
@@ -2573,6 +2580,7 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.merge_cnt = plan.split ? merge_cnt : nullptr;
     a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
     a.max_pages = pool->arena.a.max_pages();
+    a.pages = pool->arena.a.pages();
     a.page_shift = pool->page_shift;
     a.q_heads = sp.q_heads;
     a.nq_per_kv = sp.q_heads / pool->kv_heads;
@@ -2634,6 +2642,13 @@ namespace {
 int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_attn_spec* spec, const thb_rows* rows,
               void* stream) {
     if (!pool || !io || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, io, spec or rows");
+    // The plan is made on the host from the row meta last written and cached
+    // in buffers that later calls reuse: a replay could not follow the rows.
+    if (capturing(as_stream(stream)))
+        return fail(THB_ERR_INVALID, "not capturable: thb_attn plans each call on the host; capture "
+                                     "thb_dplan_build + thb_attn_dplan (planned on the device at every replay) or "
+                                     "thb_attn_noalloc (the plan travels in the graph)");
+    if (int rc = sync_mirror(pool, as_stream(stream))) return rc;
     if (spec->m == 0)
         return layer < pool->layers ? THB_OK : check_attn_call(pool, layer, io->q_dev, io->y_dev, *spec, rows);
     if (int rc = check_attn_call(pool, layer, io->q_dev, io->y_dev, *spec, rows)) return rc;
@@ -2680,9 +2695,9 @@ int step_impl(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_a
         const uint32_t* blob = static_cast<const uint32_t*>(plan->dev.get());
         uint64_t o_bytes = 0;
         const uint64_t pb = partial_bytes(pool, *plan, &o_bytes);
-        uint8_t* part = pb ? static_cast<uint8_t*>(pool->partials.reserve(pb, false)) : nullptr;
+        uint8_t* part = pb ? static_cast<uint8_t*>(pool->partials.reserve(pb, false, s)) : nullptr;
         uint32_t* cnt = plan->n_merge_dec ? static_cast<uint32_t*>(pool->merge_cnt.reserve(
-                                                static_cast<size_t>(plan->n_items) * pool->kv_heads * 4, true))
+                                                static_cast<size_t>(plan->n_items) * pool->kv_heads * 4, true, s))
                                           : nullptr;
         if (!append) {
             launch_plan(pool, layer, *io, *spec, *plan, false, meta, blob, part, cnt, s);
@@ -2801,6 +2816,7 @@ extern "C" int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q, v
     if (!pool || !spec || !rows) return fail(THB_ERR_INVALID, "null pool, spec or rows");
     if (int rc = check_attn_call(pool, layer, q, y, *spec, rows)) return rc;
     if (spec->m == 0) return THB_OK;
+    if (int rc = sync_mirror(pool, as_stream(stream))) return rc;
     const uint32_t hd = pool->geom[layer].head_dim;
     return guarded([&]() -> int {
         int device = -1;
@@ -2905,14 +2921,14 @@ int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan
         for (const auto& g : pool->geom) p->hd_max = std::max(p->hd_max, template_hd(g.head_dim));
         dplan_layout(p.get());
         const size_t words = static_cast<size_t>(p->merge_off) + static_cast<size_t>(p->gmax) * kMergeWords;
-        p->blob.reserve(words * 4, true);
+        p->blob.reserve(words * 4, true, nullptr);
         AttnPlan shape;
         dplan_shape(p.get(), p->hd_max, shape);
         uint64_t o_bytes = 0;
         const uint64_t pb = partial_bytes(pool, shape, &o_bytes);
         if (pb) {
-            p->part.reserve(pb, false);
-            p->cnt.reserve(static_cast<size_t>(shape.n_items) * pool->kv_heads * 4, true);
+            p->part.reserve(pb, false, nullptr);
+            p->cnt.reserve(static_cast<size_t>(shape.n_items) * pool->kv_heads * 4, true, nullptr);
         }
         *out = p.release();
         return THB_OK;

@@ -24,6 +24,24 @@ struct HipError {
     std::string where;
 };
 
+// A call refused because its stream is capturing a graph and the call
+// cannot be replayed correctly from a capture (THB_ERR_INVALID).
+struct CaptureRefused {
+    std::string what;
+};
+
+// True while `stream` captures a graph (also when the capture has been
+// invalidated, or when another stream captures in global mode and `stream`
+// is the legacy default stream).
+bool capturing(hipStream_t stream);
+
+// Writes `bytes` of host data to device `dst` inside the graph `stream` is
+// capturing: the data travel in the arguments of copy kernels, so the graph
+// owns them and every replay writes the same bytes.  Up to
+// kGraphUploadMax bytes; more throws CaptureRefused.
+constexpr size_t kGraphUploadMax = 256u << 10;
+void upload_in_graph(void* dst, const void* src, size_t bytes, hipStream_t stream);
+
 #define THB_HIP(call)                                                              \
     do {                                                                           \
         hipError_t thb_e_ = (call);                                                \
@@ -37,6 +55,8 @@ int guarded(F&& body) {
         return body();
     } catch (const HipError& e) {
         return fail(THB_ERR_GPU, std::string("HIP error ") + hipGetErrorString(e.err) + " in " + e.where);
+    } catch (const CaptureRefused& e) {
+        return fail(THB_ERR_INVALID, "not capturable: " + e.what);
     } catch (const std::bad_alloc&) {
         return fail(THB_ERR_GPU, "host out of memory");
     }
@@ -46,7 +66,9 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // Pinned host staging for host->device copies.  A ring of slots; a slot is
 // reused only after the event recorded behind its last copy has completed,
-// so the host never overwrites bytes a pending copy still reads.
+// so the host never overwrites bytes a pending copy still reads.  On a
+// capturing stream the bytes go into the graph instead (upload_in_graph): a
+// captured copy from a slot would read the slot's contents at replay time.
 class Stager {
 public:
     Stager() = default;
@@ -70,7 +92,8 @@ private:
 
 // Pinned host staging of a fixed size, allocated once (init) and never
 // grown: two slots, each reused after the event behind its last copy.
-// upload() allocates nothing.
+// upload() allocates nothing; on a capturing stream it writes through
+// upload_in_graph, which allocates nothing either.
 class FixedStager {
 public:
     FixedStager() = default;
@@ -92,21 +115,31 @@ private:
 };
 
 // Device buffer that grows on demand (hipMalloc outside the hot path: only
-// when a larger size than ever before is requested).
+// when a larger size than ever before is requested).  A buffer handed out
+// while `stream` captures a graph may be read by every replay of that graph,
+// so it is never freed before the DevBuf is destroyed: growth after a capture
+// keeps the old allocation alive, and growth during a capture is refused.
 class DevBuf {
 public:
     DevBuf() = default;
     DevBuf(const DevBuf&) = delete;
     DevBuf& operator=(const DevBuf&) = delete;
     ~DevBuf();
-    // Ensures capacity; newly grown memory is zero-filled when `zero`.
-    void* reserve(size_t bytes, bool zero);
+    // Ensures capacity for work queued on `stream`; newly grown memory is
+    // zero-filled when `zero`.
+    void* reserve(size_t bytes, bool zero, hipStream_t stream);
+    // reserve() for a caller about to overwrite the contents from the host:
+    // outside a capture, a buffer a graph has used is replaced by a new
+    // allocation (the graph keeps reading the old contents).
+    void* reserve_rewrite(size_t bytes, bool zero, hipStream_t stream);
     void* get() const { return ptr_; }
     size_t size() const { return cap_; }
 
 private:
     void* ptr_ = nullptr;
     size_t cap_ = 0;
+    bool captured_ = false;        // ptr_ was handed to a capture
+    std::vector<void*> retired_;   // earlier allocations a graph may still read
 };
 
 }  // namespace thb

@@ -539,8 +539,8 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     uint32_t* cnt;
     {
         std::lock_guard<std::mutex> lock(g_part_mu);
-        part = static_cast<float*>(g_part[dev].reserve(static_cast<size_t>(S) * a.m * a.n * 4, false));
-        cnt = static_cast<uint32_t*>(g_cnt[dev].reserve(static_cast<size_t>(a.n / 64) * 4, true));
+        part = static_cast<float*>(g_part[dev].reserve(static_cast<size_t>(S) * a.m * a.n * 4, false, s));
+        cnt = static_cast<uint32_t*>(g_cnt[dev].reserve(static_cast<size_t>(a.n / 64) * 4, true, s));
     }
     SplitArgs sa;
     sa.g = a;

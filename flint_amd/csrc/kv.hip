@@ -28,6 +28,7 @@ struct StoreArgs {
     const uint32_t* table;  // [seqs * max_pages]
     uint64_t plane;         // elements per head plane
     uint32_t max_pages, page_shift, head_dim, chunks;  // chunks = kv_heads * head_dim / 8
+    uint32_t pages, seqs;   // a row outside them, or on a page not held, stores nothing
 };
 
 // kv_store.wgsl:24-46 with one lane per 8 elements.  Grid: (ceil(2 *
@@ -40,7 +41,11 @@ __global__ __launch_bounds__(256) void kv_store_kernel(StoreArgs a) {
     const bool is_v = c >= a.chunks;
     if (is_v) c -= a.chunks;
     const uint32_t pos = a.meta[8 * row], seq = a.meta[8 * row + 1];
+    // The host checks every row's pages before an eager call; a captured
+    // call replays with the row meta of its own time, so the device checks.
+    if (seq >= a.seqs || (pos >> a.page_shift) >= a.max_pages) return;
     const uint32_t page = a.table[static_cast<uint64_t>(seq) * a.max_pages + (pos >> a.page_shift)];
+    if (page >= a.pages) return;
     const uint32_t cph = a.head_dim >> 3;
     const uint32_t h = c / cph, d = (c - h * cph) << 3;
     const uint64_t src_e = (static_cast<uint64_t>(row) * a.chunks + c) << 3;
@@ -329,6 +334,7 @@ struct GatherArgs {
     const uint32_t* table_row;  // the sequence's block-table row
     uint64_t plane;
     uint32_t page_shift, head_dim, n, t0;
+    uint32_t pages;  // pages of the pool: a table entry outside them moves nothing
     uint32_t tile;   // tokens per LDS tile of V (min(page_len, 64))
     uint32_t heads;  // KV heads per workgroup
     // Batched calls (null otherwise): work item x = (range, page of the
@@ -420,7 +426,9 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs args) {
     const uint32_t ja = max(a.t0, p0) - p0;
     const uint32_t jb = static_cast<uint32_t>(
         min(static_cast<uint64_t>(a.t0) + a.n, static_cast<uint64_t>(p0) + (1u << shift)) - p0);
-    const uint64_t pbase0 = (static_cast<uint64_t>(a.table_row[pi]) * hd) << shift;
+    const uint32_t phys = a.table_row[pi];
+    if (phys >= a.pages) return;  // whole workgroup: a page not held (a replay after the pages changed)
+    const uint64_t pbase0 = (static_cast<uint64_t>(phys) * hd) << shift;
     auto pbase = [&](uint32_t hh) { return static_cast<uint64_t>(h0 + hh) * a.plane + pbase0; };
     // flat row of page slot j of head h: h * n + p0 + j - t0 (j >= ja keeps it >= h * n)
     auto flat_off = [&](uint32_t hh, uint32_t j, uint32_t c) {
@@ -579,32 +587,19 @@ struct CopyArgs {
     uint8_t* mem;
     const DevLayer* layers;
     const uint32_t* triples;  // device (src_page, dst_page, tokens) list, or null: the inline list
+    const uint32_t* count;    // device length of `triples` (workgroups walk it), or null: one triple per x
     uint64_t pool_len;
     uint32_t kv_heads, page_shift;
     uint32_t inl[3 * kInlineCopies];
 };
 
 // Copy of slots [0, ntok) of one (page, head, K or V) plane of one layer.
-// Grid: (n_triples, layers * 2 * kv_heads), plane fastest.  Every access is
-// a 16-byte vector: a whole page is one contiguous run (4 vectors in flight
-// per lane); of a partial page, each K group moves the 16-byte pieces of its
-// first ntok slots, and V its first ceil(ntok / 4) 4-slot groups, the group
-// that ntok cuts merged slot by slot.
-__global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
-    const uint32_t planes = 2 * a.kv_heads;
-    const uint32_t layer = blockIdx.y / planes, plane = blockIdx.y - layer * planes;
-    const uint32_t which = plane >= a.kv_heads, h = plane - which * a.kv_heads;
-    const DevLayer L = a.layers[layer];
-    uint32_t src, dst, ntok;
-    if (a.triples) {
-        src = a.triples[3 * blockIdx.x];
-        dst = a.triples[3 * blockIdx.x + 1];
-        ntok = a.triples[3 * blockIdx.x + 2];
-    } else {
-        src = a.inl[3 * blockIdx.x];
-        dst = a.inl[3 * blockIdx.x + 1];
-        ntok = a.inl[3 * blockIdx.x + 2];
-    }
+// Every access is a 16-byte vector: a whole page is one contiguous run (4
+// vectors in flight per lane); of a partial page, each K group moves the
+// 16-byte pieces of its first ntok slots, and V its first ceil(ntok / 4)
+// 4-slot groups, the group that ntok cuts merged slot by slot.
+__device__ void copy_page_plane(const CopyArgs& a, const DevLayer& L, uint32_t which, uint32_t h, uint32_t src,
+                                uint32_t dst, uint32_t ntok) {
     const uint32_t shift = a.page_shift, P = 1u << shift, hd = L.head_dim;
     const uint32_t vecs = (hd << shift) >> 3;  // 16-byte vectors per page plane
     const uint64_t page_elems = static_cast<uint64_t>(L.head_dim) << shift;
@@ -635,6 +630,27 @@ __global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
             if (4u * q < ntok) merge_v16(dp + e, sp + e, 0, ntok - 4u * q);
         }
     }
+}
+
+// Grid: (x, layers * 2 * kv_heads), plane fastest.  Without a count,
+// workgroup x copies triple x; with one, the x workgroups of a plane walk
+// the *count triples of the device list (a launch sized without the host).
+__global__ __launch_bounds__(256) void block_copy_kernel(CopyArgs a) {
+    const uint32_t planes = 2 * a.kv_heads;
+    const uint32_t layer = blockIdx.y / planes, plane = blockIdx.y - layer * planes;
+    const uint32_t which = plane >= a.kv_heads, h = plane - which * a.kv_heads;
+    const DevLayer L = a.layers[layer];
+    if (a.count) {
+        const uint32_t n = *a.count;
+        for (uint32_t t = blockIdx.x; t < n; t += gridDim.x)
+            copy_page_plane(a, L, which, h, a.triples[3 * t], a.triples[3 * t + 1], a.triples[3 * t + 2]);
+        return;
+    }
+    if (a.triples)
+        copy_page_plane(a, L, which, h, a.triples[3 * blockIdx.x], a.triples[3 * blockIdx.x + 1],
+                        a.triples[3 * blockIdx.x + 2]);
+    else
+        copy_page_plane(a, L, which, h, a.inl[3 * blockIdx.x], a.inl[3 * blockIdx.x + 1], a.inl[3 * blockIdx.x + 2]);
 }
 
 template <uint32_t SRC>
@@ -682,6 +698,11 @@ uint32_t make_runs(const uint32_t* meta, uint32_t m, uint32_t max_run, std::vect
 // row kernel instead.
 const uint32_t* device_runs(thb_pool* p, const thb_rows* rows, uint32_t row_off, uint32_t m, uint32_t max_run,
                             hipStream_t s, uint32_t* n_runs) {
+    // Under capture a new cut is uploaded inside the graph and not kept as
+    // the cache (the buffer holds it only once the graph has run); a cached
+    // cut that a capture uses stays in its buffer (reserve_rewrite moves
+    // later uploads to a new one).
+    const bool cap = capturing(s);
     if (p->runs_rows != rows || p->runs_version != rows->version || p->runs_off != row_off || p->runs_m != m ||
         p->runs_max != max_run) {
         std::vector<uint32_t> runs;
@@ -689,14 +710,19 @@ const uint32_t* device_runs(thb_pool* p, const thb_rows* rows, uint32_t row_off,
         p->runs_n = static_cast<uint32_t>(runs.size() / 4);
         p->runs_rows = nullptr;  // invalid until the upload below is queued
         if (2 * static_cast<uint64_t>(p->runs_long) >= m) {
-            void* dev = p->run_buf.reserve(runs.size() * 4, false);
+            void* dev = cap ? p->run_buf.reserve(runs.size() * 4, false, s)
+                            : p->run_buf.reserve_rewrite(runs.size() * 4, false, s);
             p->stager.upload(dev, runs.data(), runs.size() * 4, s);
         }
-        p->runs_rows = rows;
-        p->runs_version = rows->version;
-        p->runs_off = row_off;
-        p->runs_m = m;
-        p->runs_max = max_run;
+        if (!cap) {
+            p->runs_rows = rows;
+            p->runs_version = rows->version;
+            p->runs_off = row_off;
+            p->runs_m = m;
+            p->runs_max = max_run;
+        }
+    } else if (2 * static_cast<uint64_t>(p->runs_long) >= m) {
+        p->run_buf.reserve(static_cast<size_t>(p->runs_n) * 16, false, s);  // marks it as used by a capture
     }
     *n_runs = p->runs_n;
     return 2 * static_cast<uint64_t>(p->runs_long) >= m ? static_cast<const uint32_t*>(p->run_buf.get()) : nullptr;
@@ -787,7 +813,7 @@ void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_
         std::copy(triples, triples + 3 * static_cast<size_t>(n), a.inl);
         a.triples = nullptr;
     } else {
-        void* dev = p->copy_buf.reserve(static_cast<size_t>(n) * 12, false);
+        void* dev = p->copy_buf.reserve_rewrite(static_cast<size_t>(n) * 12, false, stream);
         p->stager.upload(dev, triples, static_cast<size_t>(n) * 12, stream);
         a.triples = static_cast<const uint32_t*>(dev);
     }
@@ -800,6 +826,14 @@ void launch_block_copy_dev(thb_pool* p, const uint32_t* triples_dev, uint32_t n,
     CopyArgs a = copy_args(p);
     a.triples = triples_dev;
     launch_copy_grid(a, n, p->layers, stream);
+}
+
+void launch_block_copy_counted(thb_pool* p, const uint32_t* triples_dev, const uint32_t* count_dev, uint32_t grid_x,
+                               hipStream_t stream) {
+    CopyArgs a = copy_args(p);
+    a.triples = triples_dev;
+    a.count = count_dev;
+    launch_copy_grid(a, std::max<uint32_t>(grid_x, 1), p->layers, stream);
 }
 
 }  // namespace thb
@@ -816,12 +850,21 @@ int thb_kv_store(thb_pool* pool, uint32_t layer, const void* k_src, const void* 
     if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
     if (src_dtype > THB_DT_BF16) return fail(THB_ERR_INVALID, "unknown src_dtype " + std::to_string(src_dtype));
     if (!aligned16(k_src) || !aligned16(v_src)) return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
-    if (static_cast<uint64_t>(row_off) + m > rows->m)
-        return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(rows->m) + " rows, call needs " +
-                                         std::to_string(static_cast<uint64_t>(row_off) + m));
-    for (uint32_t r = row_off; r < row_off + m; r++) {
-        uint32_t pos = rows->host[8 * r], seq = rows->host[8 * r + 1];
-        if (int rc = check_cover(pool, seq, static_cast<uint64_t>(pos) + 1)) return rc;
+    // Under capture in graph mode (after a captured thb_pool_alloc_rows) the
+    // call follows the row meta of each replay on the row kernel, its pages
+    // checked on the device: the host mirror cannot know them.
+    const bool cap = capturing(as_stream(stream));
+    const bool follow = cap && pool->graph_mode;
+    if (static_cast<uint64_t>(row_off) + m > (follow ? rows->max_m : rows->m))
+        return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(follow ? rows->max_m : rows->m) +
+                                         " rows, call needs " + std::to_string(static_cast<uint64_t>(row_off) + m));
+    if (!follow) {
+        if (!cap)
+            if (int rc = sync_mirror(pool, as_stream(stream))) return rc;
+        for (uint32_t r = row_off; r < row_off + m; r++) {
+            uint32_t pos = rows->host[8 * r], seq = rows->host[8 * r + 1];
+            if (int rc = check_cover(pool, seq, static_cast<uint64_t>(pos) + 1)) return rc;
+        }
     }
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
@@ -839,11 +882,16 @@ int thb_kv_store(thb_pool* pool, uint32_t layer, const void* k_src, const void* 
         a.page_shift = pool->page_shift;
         a.head_dim = g.head_dim;
         a.chunks = pool->kv_heads * g.head_dim / 8;
+        a.pages = pool->arena.a.pages();
+        a.seqs = pool->arena.a.seqs();
         const size_t esize = src_dtype == THB_DT_F32 ? 4 : 2;
         // Mostly long runs (prefill chunks): the run kernel writes whole V
         // page rows; otherwise (decode) one lane per 8 elements of a row.
+        // The runs are cut on the host from the row meta's host mirror, so
+        // a call that follows the replays' rows never takes them (a captured
+        // call outside graph mode replays the captured runs).
         uint32_t n_runs = 0;
-        if (const uint32_t* dev = device_runs(pool, rows, row_off, m, kRunTokens, s, &n_runs)) {
+        if (const uint32_t* dev = follow ? nullptr : device_runs(pool, rows, row_off, m, kRunTokens, s, &n_runs)) {
             RunArgs ra;
             ra.k_src = k_src;
             ra.v_src = v_src;
@@ -928,6 +976,7 @@ static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t 
     if (n == 0) return THB_OK;
     if (!k || !v) return fail(THB_ERR_INVALID, "null buffer");
     if (!aligned16(k) || !aligned16(v)) return fail(THB_ERR_INVALID, "buffers must be 16-byte aligned");
+    if (int rc = sync_mirror(pool, as_stream(stream))) return rc;
     if (int rc = check_cover(pool, seq, static_cast<uint64_t>(t0) + n)) return rc;
     if (!to_flat)
         if (int rc = check_unshared(pool, seq, t0, n)) return rc;
@@ -944,6 +993,7 @@ static int gather_common(thb_pool* pool, uint32_t layer, uint32_t seq, uint32_t 
         a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * g.head_dim;
         a.page_shift = pool->page_shift;
         a.head_dim = g.head_dim;
+        a.pages = pool->arena.a.pages();
         a.n = n;
         a.t0 = t0;
         size_t lds = 0;
@@ -969,6 +1019,7 @@ static int gather_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t cou
     if (!ranges) return fail(THB_ERR_INVALID, "ranges is null");
     if (!k || !v) return fail(THB_ERR_INVALID, "null buffer");
     if (!aligned16(k) || !aligned16(v)) return fail(THB_ERR_INVALID, "buffers must be 16-byte aligned");
+    if (int rc = sync_mirror(pool, as_stream(stream))) return rc;
     uint32_t hd = 0;
     for (uint32_t i = 0; i < count; i++) {
         const thb_kv_range& r = ranges[i];
@@ -1021,11 +1072,20 @@ static int gather_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t cou
         const size_t items_words = blob.size();
         blob.insert(blob.end(), recs.begin(), recs.end());
         // Uploaded only when the ranges change: repeating a call (or
-        // capturing it in a graph after a first call) moves nothing.
+        // capturing it in a graph after a first call) moves nothing.  Under
+        // capture a new list is uploaded inside the graph and not kept as
+        // the cache; a cached list that a capture uses stays in its buffer.
+        const bool cap = capturing(s);
         if (blob != pool->range_key) {
-            void* d = pool->range_buf.reserve(blob.size() * 4, false);
+            void* d = cap ? pool->range_buf.reserve(blob.size() * 4, false, s)
+                          : pool->range_buf.reserve_rewrite(blob.size() * 4, false, s);
             pool->stager.upload(d, blob.data(), blob.size() * 4, s);
-            pool->range_key.swap(blob);
+            if (cap)
+                pool->range_key.clear();
+            else
+                pool->range_key.swap(blob);
+        } else {
+            pool->range_buf.reserve(blob.size() * 4, false, s);  // marks it as used by a capture
         }
         const uint32_t* dev = static_cast<const uint32_t*>(pool->range_buf.get());
         GatherArgs a{};
@@ -1037,6 +1097,7 @@ static int gather_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t cou
         a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
         a.page_shift = pool->page_shift;
         a.head_dim = hd;
+        a.pages = pool->arena.a.pages();
         a.items = dev;
         a.ranges = dev + items_words;
         size_t lds = 0;
@@ -1075,6 +1136,7 @@ int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* st
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
     if (n == 0) return THB_OK;
     if (!triples) return fail(THB_ERR_INVALID, "triples is null");
+    if (int rc = sync_mirror(pool, as_stream(stream))) return rc;
     const uint32_t pages = pool->arena.a.pages();
     uint32_t max_tok = 0;
     std::vector<uint32_t> srcs, dsts;
@@ -1116,6 +1178,9 @@ int thb_rope_rows(void* x, uint32_t dtype, uint32_t m, uint32_t heads, uint32_t 
     if (dtype != THB_DT_F32 && dtype != THB_DT_F16)
         return fail(THB_ERR_INVALID, "rope rows take f32 or f16 (dtype " + std::to_string(dtype) + ")");
     if (int rc = thb_backend_head_dim(head_dim)) return rc;
+    if (capturing(as_stream(stream)))
+        return fail(THB_ERR_INVALID, "not capturable: thb_rope_rows checks the rows' positions against the rotary "
+                                     "tables on the host");
     if (int rc = check_rope(rope, head_dim, rows, row_off, m)) return rc;
     if (!aligned16(norm_w)) return fail(THB_ERR_INVALID, "norm weight must be 16-byte aligned");
     const uint64_t waves = static_cast<uint64_t>(m) * heads;
@@ -1152,6 +1217,10 @@ int thb_kv_store_rope(thb_pool* pool, uint32_t layer, const void* k_src, const v
         return fail(THB_ERR_INVALID, "rotary append takes f32 or f16 sources (src_dtype " +
                                          std::to_string(src_dtype) + ")");
     if (!aligned16(k_src) || !aligned16(v_src)) return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
+    if (capturing(as_stream(stream)))
+        return fail(THB_ERR_INVALID, "not capturable: thb_kv_store_rope checks the rows' positions against the "
+                                     "rotary tables on the host");
+    if (int rc = sync_mirror(pool, as_stream(stream))) return rc;
     if (int rc = check_rope(rope, pool->geom[layer].head_dim, rows, row_off, m)) return rc;
     for (uint32_t r = row_off; r < row_off + m; r++) {
         uint32_t pos = rows->host[8 * r], seq = rows->host[8 * r + 1];

@@ -20,10 +20,13 @@
 //
 // Device state (u32 words, one allocation):
 //   header [64]: free-stack top, status (first failure since the last
-//                thb_pool_status: code + 3 arguments), copy count
+//                thb_pool_status: code + 3 arguments), copy count, epoch of
+//                the last alloc-rows call
 //   free [pages] | refs [pages] | npages [seqs] | budgets [seqs] |
 //   copies [pages x 3]: (src page, dst page, tokens) of the copy-on-write
-//   copies made since the list was last reset (a flush resets it per batch).
+//   copies made since the list was last reset (a flush resets it per batch) |
+//   keys [seqs] (64-bit, 8-byte aligned): per sequence, the epoch and first
+//   row of the last alloc-rows call that saw it head a run of rows.
 #include <algorithm>
 #include <string>
 
@@ -39,9 +42,19 @@ enum : uint32_t {
     kStForkTarget = 3,
     kStForkCover = 4,
     kStBadSeq = kPageStBadSeq,
-    kStCover = kPageStCover
+    kStCover = kPageStCover,
+    kStDupSeq = 7
 };
-enum : uint32_t { kHdrTop = 0, kHdrStatus = 1, kHdrA = 2, kHdrB = 3, kHdrC = 4, kHdrCopies = 5, kHdrWords = 64 };
+enum : uint32_t {
+    kHdrTop = 0,
+    kHdrStatus = 1,
+    kHdrA = 2,
+    kHdrB = 3,
+    kHdrC = 4,
+    kHdrCopies = kPageHdrCopies,
+    kHdrEpoch = 6,
+    kHdrWords = 64
+};
 static_assert(kHdrStatus == kPageHdrStatus, "status word shared with the attention planner");
 
 constexpr uint32_t kOpsPerLaunch = 64;  // page ops passed in one launch's arguments
@@ -56,7 +69,7 @@ struct PageOpArgs {
     uint32_t* table;       // [seqs * max_pages]
     const uint32_t* meta;  // row meta of an alloc-rows op (at its first row)
     uint32_t pages, seqs, max_pages, shift;
-    uint32_t free_off, refs_off, npages_off, lens_off, copies_off;
+    uint32_t free_off, refs_off, npages_off, lens_off, copies_off, keys_off;
     uint32_t n_ops, reset_copies;
     uint32_t ops[4 * kOpsPerLaunch];  // (kind, a, b, c)
 };
@@ -68,6 +81,7 @@ struct St {
     uint32_t* npages;
     const uint32_t* lens;
     uint32_t* copies;
+    unsigned long long* keys;
     uint32_t* table;
     uint32_t pages, seqs, mp, shift;
     __device__ uint32_t* row(uint32_t seq) const { return table + static_cast<uint64_t>(seq) * mp; }
@@ -80,6 +94,7 @@ struct Lds {
     uint32_t cnt[kT], pre[kT], base[kT], nnew[kT];
     uint32_t red[kT / 64];
     uint32_t top, ncopy, first_fail, shared;
+    uint32_t epoch, bad, reset;
 };
 
 // Inclusive scan (sum, or max when MAX) over the workgroup; *total gets the
@@ -267,13 +282,67 @@ __device__ bool alloc_chunks(const St& st, uint32_t n, Lds& L) {
     return ff != kNone;
 }
 
+// Validates an alloc-rows call before anything is allocated, as the host
+// does: every row's sequence in range, and no sequence heading two runs of
+// rows (two runs allocated in one parallel round would write the same
+// table slots).  The first offending row (in row order) is recorded and the
+// call returns false.  A sequence's key (epoch << 32 inverted, | row) keeps,
+// by atomicMin, the first row heading one of its runs in this call: older
+// calls' epochs give larger keys.  When the epoch counter wraps, every key
+// is reset first.
+__device__ bool check_rows(const St& st, const uint32_t* meta, uint32_t m, Lds& L) {
+    const uint32_t tid = threadIdx.x;
+    if (tid == 0) {
+        uint32_t e = st.hdr[kHdrEpoch] + 1u;
+        L.reset = e == 0u;
+        if (e == 0u) e = 1u;
+        st.hdr[kHdrEpoch] = e;
+        L.epoch = e;
+        L.bad = kNone;
+    }
+    __syncthreads();
+    if (L.reset) {
+        for (uint32_t s = tid; s < st.seqs; s += blockDim.x) st.keys[s] = ~0ull;
+        __syncthreads();
+    }
+    const unsigned long long hi = static_cast<unsigned long long>(~L.epoch) << 32;
+    for (uint32_t r = tid; r < m; r += blockDim.x) {
+        const uint32_t seq = meta[8u * r + 1];
+        if (seq >= st.seqs)
+            atomicMin(&L.bad, r);
+        else if (r == 0 || meta[8u * (r - 1) + 1] != seq)
+            atomicMin(&st.keys[seq], hi | r);
+    }
+    __syncthreads();
+    for (uint32_t r = tid; r < m; r += blockDim.x) {
+        const uint32_t seq = meta[8u * r + 1];
+        if (seq < st.seqs && (r == 0 || meta[8u * (r - 1) + 1] != seq)) {
+            const unsigned long long k = atomicAdd(&st.keys[seq], 0ull);  // read at the cache the atomics used
+            if (static_cast<uint32_t>(k) != r) atomicMin(&L.bad, r);
+        }
+    }
+    __syncthreads();
+    const uint32_t bad = L.bad;
+    if (bad == kNone) return true;
+    if (tid == 0) {
+        const uint32_t seq = meta[8u * bad + 1];
+        if (seq >= st.seqs)
+            record(st, kStBadSeq, seq, st.seqs, 0);
+        else
+            record(st, kStDupSeq, seq, 0, 0);
+    }
+    __syncthreads();
+    return false;
+}
+
 // Chunks of rows [0, m) of the row meta, in row order: maximal runs of rows
 // of one sequence, each allocated as KvArena::alloc(seq, position of its
-// first row, rows in the run).  Rows are read in tiles of one row per lane;
+// first row, rows in the run), after check_rows.  Rows are read in tiles of one row per lane;
 // the chunks that end in a tile are allocated before the next tile is read,
 // and a failure ends the call.
 __device__ void alloc_rows(const St& st, const uint32_t* meta, uint32_t m, Lds& L) {
     const uint32_t tid = threadIdx.x;
+    if (!check_rows(st, meta, m, L)) return;
     uint32_t open = 0;  // 1 + first row of the chunk still open at the end of the last tile
     for (uint32_t t0 = 0; t0 < m; t0 += blockDim.x) {
         const uint32_t r = t0 + tid;
@@ -404,6 +473,7 @@ __global__ __launch_bounds__(kT) void page_ops_kernel(PageOpArgs a) {
     st.npages = a.state + a.npages_off;
     st.lens = a.state + a.lens_off;
     st.copies = a.state + a.copies_off;
+    st.keys = reinterpret_cast<unsigned long long*>(a.state + a.keys_off);
     st.table = a.table;
     st.pages = a.pages;
     st.seqs = a.seqs;
@@ -461,6 +531,7 @@ PageOpArgs op_args(const thb_pool* p) {
     a.npages_off = p->state.npages_off;
     a.lens_off = p->state.lens_off;
     a.copies_off = p->state.copies_off;
+    a.keys_off = p->state.keys_off;
     return a;
 }
 
@@ -489,6 +560,8 @@ std::string status_message(const uint32_t* hdr) {
         case kStForkCover:
             return "fork source " + std::to_string(a) + " does not cover " + std::to_string(b) + " tokens";
         case kStBadSeq: return "sequence " + std::to_string(a) + " out of range (" + std::to_string(b) + " sequences)";
+        case kStDupSeq:
+            return "sequence " + std::to_string(a) + " heads two runs of rows in one call (one run per sequence)";
         case kStCover:
             return "pages must cover the chunk: sequence " + std::to_string(a) + " holds " + std::to_string(b) +
                    " slots, a row reads " + std::to_string(hdr[kHdrC]);
@@ -507,8 +580,10 @@ void init_page_state(thb_pool* p) {
     L.npages_off = L.refs_off + pages;
     L.lens_off = L.npages_off + seqs;
     L.copies_off = L.lens_off + seqs;
-    L.words = static_cast<size_t>(L.copies_off) + 3ull * pages;
+    L.keys_off = (L.copies_off + 3u * pages + 1u) & ~1u;  // 8-byte aligned 64-bit keys
+    L.words = static_cast<size_t>(L.keys_off) + 2ull * seqs;
     std::vector<uint32_t> h(L.words, 0u);
+    std::fill(h.begin() + L.keys_off, h.end(), ~0u);
     h[kHdrTop] = pages;
     for (uint32_t i = 0; i < pages; i++) h[L.free_off + i] = ar.free_list()[i];
     for (uint32_t s = 0; s < seqs; s++) h[L.lens_off + s] = ar.seq_len(s);
@@ -528,6 +603,10 @@ void queue_page_op(thb_pool* p, uint32_t kind, uint32_t a, uint32_t b, uint32_t 
 void pool_flush(thb_pool* p, hipStream_t stream) {
     auto& ops = p->page_ops;
     if (ops.empty()) return;
+    if (capturing(stream))
+        throw CaptureRefused{"page-API calls queued on the host (thb_pool_alloc, _free_seq, _truncate, _fork) "
+                             "must run before the capture starts (thb_pool_sync): a graph would repeat them on "
+                             "every replay"};
     const auto& copies = p->arena.a.copies();
     auto emit = [&](size_t i0, size_t i1) {
         for (size_t k = i0; k < i1; k += kOpsPerLaunch) {
@@ -578,6 +657,26 @@ void pool_flush(thb_pool* p, hipStream_t stream) {
     p->arena.a.copies().clear();
 }
 
+int sync_mirror(thb_pool* p, hipStream_t stream) {
+    if (!p->graph_mode) return THB_OK;
+    return guarded([&]() -> int {
+        if (capturing(stream) || capturing(nullptr))
+            throw CaptureRefused{"in graph mode the host mirror is reloaded from the device first, which waits "
+                                 "for the device"};
+        THB_HIP(hipDeviceSynchronize());  // replays on any stream
+        pool_flush(p, nullptr);
+        THB_HIP(hipDeviceSynchronize());
+        std::vector<uint32_t> h(p->state.words);
+        THB_HIP(hipMemcpy(h.data(), p->state_dev, p->state.words * 4, hipMemcpyDeviceToHost));
+        Arena& ar = p->arena.a;
+        std::vector<uint32_t> table(static_cast<size_t>(ar.seqs()) * ar.max_pages());
+        THB_HIP(hipMemcpy(table.data(), p->table_dev, table.size() * 4, hipMemcpyDeviceToHost));
+        ar.load_state(h.data() + p->state.free_off, h[kHdrTop], h.data() + p->state.refs_off,
+                      h.data() + p->state.npages_off, table.data());
+        return THB_OK;
+    });
+}
+
 }  // namespace thb
 
 using namespace thb;
@@ -586,6 +685,7 @@ namespace {
 
 // Reads the device page state into host arrays after the stream's work.
 void read_state(thb_pool* p, hipStream_t s, std::vector<uint32_t>& h) {
+    if (capturing(s)) throw CaptureRefused{"reading the device allocator's state waits for the stream"};
     pool_flush(p, s);
     THB_HIP(hipStreamSynchronize(s));
     h.resize(p->state.words);
@@ -599,6 +699,34 @@ extern "C" {
 int thb_pool_alloc_rows(thb_pool* pool, const thb_rows* rows, uint32_t row_off, uint32_t m, void* stream) {
     if (!pool || !rows) return fail(THB_ERR_INVALID, "null pool or rows");
     if (m == 0) return THB_OK;
+    hipStream_t s = as_stream(stream);
+    if (capturing(s)) {
+        // Under capture the call is the device allocator alone: replays read
+        // the row meta of their own time, validate it (bad or repeated
+        // sequences are recorded for thb_pool_status) and size the
+        // copy-on-write launch from the device's own copy count.  The host
+        // mirror cannot follow the replays: the pool enters graph mode.
+        if (static_cast<uint64_t>(row_off) + m > rows->max_m)
+            return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(rows->max_m) + " rows, call needs " +
+                                             std::to_string(static_cast<uint64_t>(row_off) + m));
+        return guarded([&]() -> int {
+            pool_flush(pool, s);  // refuses queued host page ops
+            PageOpArgs a = op_args(pool);
+            a.meta = rows->dev + 8 * static_cast<size_t>(row_off);
+            a.n_ops = 1;
+            a.reset_copies = 1;
+            a.ops[0] = kPageOpAllocRows;
+            a.ops[1] = m;
+            launch_ops(a, s);
+            // A run of t rows writes into at most t pages, so the call makes
+            // at most m copies; 4 workgroups per plane walk them.
+            launch_block_copy_counted(pool, pool->state_dev + pool->state.copies_off, pool->state_dev + kHdrCopies,
+                                      std::min<uint32_t>(m, 4), s);
+            pool->graph_mode = true;
+            return THB_OK;
+        });
+    }
+    if (int rc = sync_mirror(pool, s)) return rc;
     if (static_cast<uint64_t>(row_off) + m > rows->m)
         return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(rows->m) + " rows, call needs " +
                                          std::to_string(static_cast<uint64_t>(row_off) + m));
@@ -626,7 +754,6 @@ int thb_pool_alloc_rows(thb_pool* pool, const thb_rows* rows, uint32_t row_off, 
         chunks.push_back({seq, meta[8 * r], 1});
     }
     return guarded([&]() -> int {
-        hipStream_t s = as_stream(stream);
         pool_flush(pool, s);  // queued page ops first
         std::string err;
         for (const Chunk& c : chunks) {  // the host mirror, chunk by chunk
@@ -656,7 +783,7 @@ int thb_pool_status(thb_pool* pool, void* stream) {
         const std::string msg = status_message(h.data());
         const uint32_t zero[4] = {0, 0, 0, 0};
         THB_HIP(hipMemcpy(pool->state_dev + kHdrStatus, zero, sizeof(zero), hipMemcpyHostToDevice));
-        return fail(h[kHdrStatus] == kStBadSeq ? THB_ERR_INVALID : THB_ERR_MODEL, msg);
+        return fail(h[kHdrStatus] == kStBadSeq || h[kHdrStatus] == kStDupSeq ? THB_ERR_INVALID : THB_ERR_MODEL, msg);
     });
 }
 

@@ -30,6 +30,52 @@ int fail(int code, const std::string& msg) {
 
 void clear_error() { g_error.clear(); }
 
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(stream, &st);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return e == hipErrorStreamCaptureImplicit;
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
+namespace {
+
+// Payload of one in-graph upload launch: 3968 bytes of data beside the
+// destination and the word count (a 4 KiB kernel-argument block).
+constexpr uint32_t kGraphChunkWords = 992;
+struct GraphChunk {
+    uint32_t* dst;
+    uint32_t n;
+    uint32_t w[kGraphChunkWords];
+};
+
+__global__ __launch_bounds__(256) void graph_upload_kernel(GraphChunk a) {
+    for (uint32_t i = threadIdx.x; i < a.n; i += 256) a.dst[i] = a.w[i];
+}
+
+}  // namespace
+
+void upload_in_graph(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return;
+    if (bytes > kGraphUploadMax)
+        throw CaptureRefused{"an upload of " + std::to_string(bytes) + " bytes under capture exceeds the " +
+                             std::to_string(kGraphUploadMax) + " bytes a graph carries in kernel arguments"};
+    if ((reinterpret_cast<uintptr_t>(dst) & 3u) || (bytes & 3u))
+        throw CaptureRefused{"an upload under capture must be whole, aligned 32-bit words"};
+    const uint32_t words = static_cast<uint32_t>(bytes / 4);
+    const auto* from = static_cast<const uint32_t*>(src);
+    for (uint32_t w0 = 0; w0 < words; w0 += kGraphChunkWords) {
+        GraphChunk c;
+        c.dst = static_cast<uint32_t*>(dst) + w0;
+        c.n = std::min(kGraphChunkWords, words - w0);
+        std::memcpy(c.w, from + w0, static_cast<size_t>(c.n) * 4);
+        hipLaunchKernelGGL(graph_upload_kernel, dim3(1), dim3(256), 0, stream, c);
+        THB_HIP(hipGetLastError());
+    }
+}
+
 Stager::~Stager() {
     for (auto& s : slots_) {
         if (s.done) {
@@ -42,6 +88,10 @@ Stager::~Stager() {
 
 void Stager::upload(void* dst, const void* src, size_t bytes, hipStream_t stream) {
     if (bytes == 0) return;
+    if (capturing(stream)) {
+        upload_in_graph(dst, src, bytes, stream);
+        return;
+    }
     Slot& s = slots_[next_];
     next_ = (next_ + 1) % kSlots;
     if (s.pending) {
@@ -83,6 +133,10 @@ void FixedStager::init(size_t bytes) {
 void FixedStager::upload(void* dst, const void* src, size_t bytes, hipStream_t stream) {
     if (bytes == 0) return;
     if (bytes > cap_) throw HipError{hipErrorInvalidValue, "fixed staging upload larger than its slots"};
+    if (capturing(stream)) {
+        upload_in_graph(dst, src, bytes, stream);
+        return;
+    }
     const int i = next_;
     next_ = (next_ + 1) % kSlots;
     if (pending_[i]) {
@@ -95,23 +149,48 @@ void FixedStager::upload(void* dst, const void* src, size_t bytes, hipStream_t s
     pending_[i] = true;
 }
 
+void* DevBuf::reserve_rewrite(size_t bytes, bool zero, hipStream_t stream) {
+    if (captured_ && !capturing(stream)) {
+        retired_.push_back(ptr_);
+        ptr_ = nullptr;
+        const size_t cap = std::max(bytes, cap_);
+        cap_ = 0;
+        captured_ = false;
+        return reserve(cap, zero, stream);
+    }
+    return reserve(bytes, zero, stream);
+}
+
 DevBuf::~DevBuf() {
-    if (ptr_) {
+    if (ptr_ || !retired_.empty()) {
         (void)hipDeviceSynchronize();
-        (void)hipFree(ptr_);
+        if (ptr_) (void)hipFree(ptr_);
+        for (void* p : retired_) (void)hipFree(p);
     }
 }
 
-void* DevBuf::reserve(size_t bytes, bool zero) {
-    if (bytes <= cap_) return ptr_;
+void* DevBuf::reserve(size_t bytes, bool zero, hipStream_t stream) {
+    const bool cap_now = capturing(stream);
+    if (bytes <= cap_) {
+        captured_ = captured_ || cap_now;
+        return ptr_;
+    }
+    if (cap_now)
+        throw CaptureRefused{"a device buffer of the library must grow to " + std::to_string(bytes) +
+                             " bytes (run the call once outside the capture first)"};
     size_t cap = std::max<size_t>(bytes, cap_ * 2);
     cap = (cap + 255) & ~size_t(255);
     if (ptr_) {
-        // The old buffer may still be read by queued kernels.
-        THB_HIP(hipDeviceSynchronize());
-        THB_HIP(hipFree(ptr_));
+        if (captured_) {
+            retired_.push_back(ptr_);  // a graph may still read it
+        } else {
+            // The old buffer may still be read by queued kernels.
+            THB_HIP(hipDeviceSynchronize());
+            THB_HIP(hipFree(ptr_));
+        }
         ptr_ = nullptr;
         cap_ = 0;
+        captured_ = false;
     }
     THB_HIP(hipMalloc(&ptr_, cap));
     if (zero) THB_HIP(hipMemset(ptr_, 0, cap));
@@ -355,7 +434,7 @@ int thb_pool_create(const thb_pool_desc* d, thb_pool** out) {
         p->fixed_stager.init(THB_NOALLOC_PLAN_BYTES);
         std::vector<DevLayer> dl;
         for (const auto& g : p->geom) dl.push_back({g.k_off, g.v_off, g.head_dim, 0});
-        void* gd = p->geom_buf.reserve(dl.size() * sizeof(DevLayer), false);
+        void* gd = p->geom_buf.reserve(dl.size() * sizeof(DevLayer), false, nullptr);
         THB_HIP(hipMemcpy(gd, dl.data(), dl.size() * sizeof(DevLayer), hipMemcpyHostToDevice));
         THB_HIP(hipDeviceSynchronize());
         *out = p.release();
@@ -377,6 +456,7 @@ void thb_pool_destroy(thb_pool* pool) {
 // device allocator; pool_flush replays the queue before the next kernel.
 int thb_pool_alloc(thb_pool* pool, uint32_t seq, uint32_t pos, uint32_t tokens) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (int rc = sync_mirror(pool, nullptr)) return rc;
     const uint64_t v = pool->arena.a.version();
     const size_t c = pool->arena.a.copies().size();
     if (int rc = thb_arena_alloc(&pool->arena, seq, pos, tokens)) return rc;
@@ -386,6 +466,7 @@ int thb_pool_alloc(thb_pool* pool, uint32_t seq, uint32_t pos, uint32_t tokens) 
 
 int thb_pool_free_seq(thb_pool* pool, uint32_t seq) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (int rc = sync_mirror(pool, nullptr)) return rc;
     const uint64_t v = pool->arena.a.version();
     const size_t c = pool->arena.a.copies().size();
     if (int rc = thb_arena_free_seq(&pool->arena, seq)) return rc;
@@ -395,6 +476,7 @@ int thb_pool_free_seq(thb_pool* pool, uint32_t seq) {
 
 int thb_pool_truncate(thb_pool* pool, uint32_t seq, uint32_t keep_tokens) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (int rc = sync_mirror(pool, nullptr)) return rc;
     const uint64_t v = pool->arena.a.version();
     const size_t c = pool->arena.a.copies().size();
     if (int rc = thb_arena_truncate(&pool->arena, seq, keep_tokens)) return rc;
@@ -404,6 +486,7 @@ int thb_pool_truncate(thb_pool* pool, uint32_t seq, uint32_t keep_tokens) {
 
 int thb_pool_fork(thb_pool* pool, uint32_t src, uint32_t dst, uint32_t tokens) {
     if (!pool) return fail(THB_ERR_INVALID, "pool is null");
+    if (int rc = sync_mirror(pool, nullptr)) return rc;
     const size_t c = pool->arena.a.copies().size();
     if (int rc = thb_arena_fork(&pool->arena, src, dst, tokens)) return rc;
     queue_page_op(pool, kPageOpFork, src, dst, tokens, c);

@@ -55,6 +55,7 @@ enum : uint32_t { kPageOpAlloc = 1, kPageOpFree = 2, kPageOpTruncate = 3, kPageO
 // attention call records for a row its sequence's pages do not cover
 // (arguments: sequence, slots held, keys the row reads).
 constexpr uint32_t kPageHdrStatus = 1;
+constexpr uint32_t kPageHdrCopies = 5;  // copy-on-write copies in the device list
 constexpr uint32_t kPageStBadSeq = 5;
 constexpr uint32_t kPageStCover = 6;
 
@@ -67,7 +68,7 @@ struct PageOp {
 
 // Word offsets of the device page state (one allocation).
 struct PageStateLayout {
-    uint32_t free_off, refs_off, npages_off, lens_off, copies_off;
+    uint32_t free_off, refs_off, npages_off, lens_off, copies_off, keys_off;
     size_t words;
 };
 
@@ -100,6 +101,11 @@ struct thb_pool {
     uint32_t* state_dev = nullptr;
     thb::PageStateLayout state;
     std::vector<thb::PageOp> page_ops;  // queued for the device
+    // Set for good once thb_pool_alloc_rows is captured in a graph: its
+    // replays change the device allocator without the host, so every later
+    // call that reads the host arena reloads it from the device first
+    // (sync_mirror).
+    bool graph_mode = false;
     thb::Stager stager;
     thb::FixedStager fixed_stager;   // plan uploads of thb_attn_noalloc (never grows)
     thb::DevBuf copy_buf;            // copy triples
@@ -131,6 +137,16 @@ void init_page_state(thb_pool* p);
 // Launches the block-copy kernel over n triples already on the device.
 void launch_block_copy_dev(thb_pool* p, const uint32_t* triples_dev, uint32_t n, uint32_t max_tokens,
                            hipStream_t stream);
+// Launches the block-copy kernel over the triples of a device list whose
+// length the kernel reads from count_dev when it runs: grid_x workgroups
+// per plane walk the list (a launch whose size does not depend on host
+// state, for graphs).
+void launch_block_copy_counted(thb_pool* p, const uint32_t* triples_dev, const uint32_t* count_dev, uint32_t grid_x,
+                               hipStream_t stream);
+// In graph mode, waits for the device and reloads the host mirror from the
+// device allocator (thb_pool_pull); otherwise nothing.  Call before reading
+// the host arena; refuses (THB_ERR_INVALID) while `stream` captures.
+int sync_mirror(thb_pool* p, hipStream_t stream);
 // Validates a thb_rope for rows [row_off, row_off + m) of head_dim vectors.
 int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint32_t row_off, uint32_t m);
 // Launches the block-copy kernel for n non-chaining host triples (passed in

@@ -13,6 +13,27 @@
  * stream).  Device work of one pool is ordered on the stream the caller
  * passes; a pool, like the reference's Backend (thuban_backend/src/lib.rs
  * :57-69), has one owner and is not thread-safe.
+ *
+ * HIP graph capture (no reference counterpart).  On a capturing stream:
+ *  - thb_pool_alloc_rows, thb_kv_store, thb_dplan_build and thb_attn_dplan
+ *    read everything a step changes (row meta, page counts, block table)
+ *    from device memory, so a graph of them replays correctly while the
+ *    rows move and pages are forked, truncated or freed between replays.
+ *    Once thb_pool_alloc_rows has been captured the pool is in graph mode
+ *    for good: every later call that reads the host arena (page API,
+ *    thb_attn, gather, ...) first waits for the device and reloads the host
+ *    arena from the device allocator, as thb_pool_pull does.
+ *  - Other entry points that can be captured replay the captured call: the
+ *    host data they upload travels in the graph's own kernel arguments (up
+ *    to 256 KiB per upload), and a library buffer a graph uses is not freed
+ *    before its pool.  Such a replay is valid while what the call read on
+ *    the host at capture time (positions, pages) still holds.
+ *  - These refuse with THB_ERR_INVALID: thb_attn and its variants (host
+ *    plans), thb_kv_store_rope and thb_rope_rows (host position checks),
+ *    thb_pool_status / _read_state / _pull (they wait for the stream), any
+ *    call while page-API calls queued on the host have not run (flush with
+ *    thb_pool_sync before capturing), and any call that would have to grow
+ *    a library buffer (run it once outside the capture first).
  */
 #ifndef THUBAN_HIP_H
 #define THUBAN_HIP_H
@@ -195,7 +216,12 @@ typedef struct thb_rows thb_rows;
  * order, with copy-on-write of shared pages the write touches.  Each
  * sequence may head one run only (THB_ERR_INVALID).  A failing run (context
  * limit, arena exhausted) ends the call with the reference's message; the
- * runs before it keep their pages, as the engine's loop does. */
+ * runs before it keep their pages, as the engine's loop does.  Captured in a
+ * graph, each replay validates its own rows on the device (a bad or
+ * repeated sequence allocates nothing and is reported by thb_pool_status
+ * with the message above) and copies shared pages it writes into (copy on
+ * write) over a launch sized by the device's own copy count; the pool enters
+ * graph mode (see the top of this file). */
 int thb_pool_alloc_rows(thb_pool* pool, const thb_rows* rows, uint32_t row_off, uint32_t m, void* stream);
 /* First failure the device allocator met since the last call (THB_OK if
  * none), with the reference's message; clears it.  Synchronises stream. */
@@ -208,7 +234,8 @@ int thb_pool_status(thb_pool* pool, void* stream);
 int thb_pool_read_state(thb_pool* pool, void* stream, uint32_t* free_list, size_t free_cap, uint32_t* n_free,
                         uint32_t* refs, size_t refs_cap, uint32_t* table, size_t table_n);
 /* Reloads the host mirror from the device allocator (after changes the host
- * did not see, such as replays of a captured thb_pool_alloc_rows). */
+ * did not see, such as replays of a captured thb_pool_alloc_rows; in graph
+ * mode every call that reads the host arena does this first). */
 int thb_pool_pull(thb_pool* pool, void* stream);
 /* The pool's allocator (queries; mutate through thb_pool_* instead). */
 const thb_arena* thb_pool_arena(const thb_pool* pool);
@@ -395,7 +422,10 @@ int thb_gemm_acc(const void* x_dev, uint32_t x_dtype, const void* w_dev, uint32_
  * needing more returns THB_ERR_INVALID.  Results are bit-identical to
  * thb_attn.  Every call on a device shares the array: calls that overlap on
  * one device (other streams, other threads) race.  The pool's device must be
- * current. */
+ * current.  It can be captured in a graph: the plan then travels in the
+ * graph's own kernel arguments and every replay writes it into the array
+ * before the attention launch, so a replay recomputes the captured call (at
+ * its captured positions) whatever other calls left in the array. */
 #define THB_NOALLOC_SCRATCH_BYTES (32u << 20)
 #define THB_NOALLOC_PLAN_BYTES (256u << 10)
 int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_attn_spec* spec,
