@@ -20,7 +20,10 @@ keep the GPU busy).  traffic = HBM bytes per launch from the committed rocprofv3
 counter summary.  cpu_baseline = the CPU oracle (restatement of the
 reference's f32 online-softmax algorithm) on layer 0 of the same step.
 gather / scatter / block_copy = the page-move kernels at the same shape
-(secondary fields of the same line).
+(secondary fields of the same line).  hbm_ceiling = the device's achievable
+linear read and copy rates (thb_hbm_stream over 1 GiB), against which every
+fraction is also stated.  c1_* / c3_* / c4_* / c5_* = the other BASELINE
+configurations measured in the same run (C1 with its CPU baseline).
 
 --config selects one of the other BASELINE configurations instead (C1
 qwen2-0.5b, C3 qwen3-8b, C4 gemma2-9b, C5 qwen2.5-32b).  Those are parity-
@@ -99,6 +102,63 @@ def time_append_graph(torch, ops, pool, rows, k, v, layer, m, launches=50, repla
     except Exception as exc:  # capture refused: report no figure rather than a host-bound one
         log(f"append graph timing unavailable: {exc}")
         return None
+
+
+def time_hbm_ceiling(torch, dev, mib=1024, reps=5):
+    """The device's achievable linear HBM rate, measured next to the 8 TB/s
+    specification: thb_hbm_stream over `mib` MiB with 16-byte non-temporal
+    accesses (the attention and page-move kernels' access kind), read-only
+    and copy, the best of a sweep of workgroup counts (median of `reps`
+    launches each, HIP events on the launch stream); and torch's own
+    device copy of the same buffers for comparison.  Copy rates count the
+    bytes read plus the bytes written."""
+    import ctypes
+
+    from flint_amd import _lib
+    from flint_amd.pool import _stream_ptr
+
+    nbytes = mib << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    src.random_(0, 255)
+    dst = torch.empty_like(src)
+    L = _lib.lib()
+    stream = _stream_ptr(None)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e-3)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    best = {}
+    for mode, name in ((0, "read"), (1, "copy")):
+        for wg in (256, 512, 1024, 2048, 4096):
+            def run(mode=mode, wg=wg):
+                _lib.check(L.thb_hbm_stream(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                                            nbytes, mode, wg, stream))
+            t = timed(run)
+            moved = nbytes * (2 if mode else 1)
+            gbps = moved / t / 1e9
+            if gbps > best.get(name, (0.0, 0))[0]:
+                best[name] = (gbps, wg)
+    t_torch = timed(lambda: dst.copy_(src))
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"read_GBps": round(best["read"][0], 1), "read_workgroups": best["read"][1],
+            "copy_GBps": round(best["copy"][0], 1), "copy_workgroups": best["copy"][1],
+            "torch_copy_GBps": round(2 * nbytes / t_torch / 1e9, 1), "bytes": nbytes,
+            "read_frac_of_spec": round(best["read"][0] / PEAK_HBM_GBPS, 4),
+            "copy_frac_of_spec": round(best["copy"][0] / PEAK_HBM_GBPS, 4),
+            "note": f"thb_hbm_stream over {mib} MiB, linear 16-byte non-temporal accesses, 512-lane workgroups "
+                    f"(best of 256-4096), median of {reps} launches; copy = read + write bytes"}
 
 
 def time_gather_copy(torch, ops, pool, layer, B, ctx, nkv, hd, pl, dev, reps=3):
@@ -498,6 +558,31 @@ def measure_secondary(name, args):
         sp = spec(rows, nq, hd, B)
         us = _time_steps(torch, lambda: ops.kv_store_attn(k, v, q, pool, 0, y, sp), args.steps, args.warmup)
         byts = sum(c + 1 for c in ctx) * nkv * hd * 2 * 2
+        # the same step as a serving loop replays it: kv_store + device-planned attention captured
+        # once in a HIP graph (thb_attn plans on the host and cannot be captured); 20 steps per graph
+        plan = ops.DevicePlan(pool, max_m=B, q_heads=nq)
+        yg = torch.empty_like(q)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(20):
+                    ops.kv_store(k, v, pool, 0, B, rows)
+                    plan.build(sp, q, yg)
+                    plan.attn(0, q, yg)
+        torch.cuda.current_stream().wait_stream(side)
+        gus = _time_steps(torch, graph.replay, max(1, args.steps // 5), 2) / 20
+        ops.kv_store_attn(k, v, q, pool, 0, y, sp)
+        torch.cuda.synchronize()
+        same = bool(torch.equal(y, yg))
+        del graph
+        plan.close()
+        out["graph_step"] = {"us_per_step": round(gus, 2), "GBps": round(byts / (gus * 1e-6) / 1e9, 1),
+                             "bit_identical_to_eager": same,
+                             "note": "kv_store + thb_dplan_build + thb_attn_dplan captured in a HIP graph (20 "
+                                     "steps per graph), replayed; the eager line above is one fused launch per "
+                                     "step issued from Python"}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = c1_cpu_baseline(torch, pool, rows, k, v, q, y, ctx, nq, hd, byts,
                                                   min(args.cpu_seconds, 3.0))
@@ -671,7 +756,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the C3 (qwen3-8b) and C4 (gemma2-9b) fields of the default line")
+                    help="skip the C1, C3, C4 and C5 fields of the default line")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the timed steps, run 3 device copies of this many MiB (scale factor for the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -795,6 +880,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
                      "kernel": "attn_mfma<128,f16,8 waves,ring 2> with fused append",
+                     "traffic_source": "profiles/attn_mfma_llama3-8b-decode_traffic.json: rocprofv3 FETCH_SIZE and "
+                                       "WRITE_SIZE passes of this kernel (committed), scaled by a 256 MiB copy; "
+                                       "not counted in this run",
                      "algorithmic_bytes": fused_bytes, "launches_timed": len(timed) * per_run},
         "cpu_baseline": None,
     }
@@ -811,9 +899,18 @@ def main():
         "note": "the same fused append + decode with every sequence on consecutive pages vs pages scattered "
                 "at random (thuban_bench probes/attn.rs:97-133 compares identity and shuffled tables)"}
     out["o_proj"] = time_o_proj(torch, ops, dev, B, nq, hd, layers=L)
+    ceiling = time_hbm_ceiling(torch, dev)
+    out["hbm_ceiling"] = ceiling
+    log(f"hbm ceiling: read {ceiling['read_GBps']} GB/s, copy {ceiling['copy_GBps']} GB/s")
+    rd, cp = ceiling["read_GBps"], ceiling["copy_GBps"]
+    out["roofline"]["frac_of_ceiling"] = round(achieved / rd, 4)
+    out["decode"]["frac_of_read_ceiling"] = round(achieved / rd, 4)
+    out["o_proj"]["frac_of_read_ceiling"] = round(out["o_proj"]["GBps"] / rd, 4)
     log(f"o_proj: {out['o_proj']['us_per_call']} us/call, {out['o_proj']['GBps']} GB/s")
     moves = time_gather_copy(torch, ops, pool, 1 % L, B, ctx, nkv, hd, pl, dev)
     log("gather/scatter/copy: " + ", ".join(f"{k} {v['us_per_call']} us {v['GBps']} GB/s" for k, v in moves.items()))
+    for rec in moves.values():
+        rec["frac_of_copy_ceiling"] = round(rec["GBps"] / cp, 4)
     out.update(moves)
     if args.calibrate_copy_mib:
         src = torch.empty(args.calibrate_copy_mib << 20, dtype=torch.uint8, device=dev)
@@ -829,17 +926,21 @@ def main():
             f"layer 0 of the step (decode of {B} seqs x {nq} heads x {ctx} keys), median of {runs} runs after 3 "
             f"warm-ups, {med * 1e3:.1f} ms/run, max |cpu-gpu| {err:.1e}")
     if not args.no_secondary:
-        # C3 and C4 on the same box, in the driver's line (their own lines: --config)
+        # C1, C3, C4 and C5 on the same box, in the driver's line (their own lines: --config)
         pool.close()
         del q, y, k_new, v_new
         torch.cuda.empty_cache()
         sec = argparse.Namespace(**vars(args))
         sec.steps, sec.warmup, sec.no_cpu_baseline = min(args.steps, 10), min(args.warmup, 3), True
-        for name, key in (("qwen3-8b", "c3_qwen3_8b"), ("gemma2-9b", "c4_gemma2_9b")):
+        for name, key in (("qwen2-0.5b", "c1_qwen2_0_5b"), ("qwen3-8b", "c3_qwen3_8b"),
+                          ("gemma2-9b", "c4_gemma2_9b"), ("qwen2.5-32b", "c5_qwen2_5_32b")):
+            sec.no_cpu_baseline = name != "qwen2-0.5b" or args.no_cpu_baseline
             rec = measure_secondary(name, sec)
             out[key] = {k: rec[k] for k in ("value", "unit", "us_per_layer_step", "pct_of_peak", "bytes_per_layer_step",
-                                            "prefill", "norm_rope_step", "window_layer", "global_layer")
-                        if k in rec}
+                                            "prefill", "norm_rope_step", "window_layer", "global_layer",
+                                            "gemma_prefill", "graph_step", "arena_bytes", "cpu_baseline")
+                        if k in rec and rec[k] is not None}
+            out[key]["pct_of_read_ceiling"] = round(100 * rec["value"] / rd, 1)
             out[key]["workload"] = rec["config"]["workload"]
             log(f"{name}: {rec['us_per_layer_step']} us/layer, {rec['value']} GB/s ({rec['pct_of_peak']}%)")
             torch.cuda.empty_cache()

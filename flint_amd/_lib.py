@@ -179,6 +179,7 @@ SIGNATURES = [
     ("thb_kv_gather_batch", _int, [_vp, ctypes.POINTER(KvRangeC), _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter_batch", _int, [_vp, ctypes.POINTER(KvRangeC), _u32, _vp, _vp, _vp]),
     ("thb_block_copy", _int, [_vp, _pu32, _u32, _vp]),
+    ("thb_hbm_stream", _int, [_vp, _vp, ctypes.c_uint64, _u32, _u32, _vp]),
 ]
 
 _lib = None

@@ -498,6 +498,17 @@ int thb_kv_scatter_batch(thb_pool* pool, const thb_kv_range* ranges, uint32_t co
  * destination). */
 int thb_block_copy(thb_pool* pool, const uint32_t* triples, uint32_t n, void* stream);
 
+/* ----------------------------------------------------------- measurement */
+
+/* No reference counterpart: a measurement aid.  Streams `bytes` of src_dev
+ * with 16-byte non-temporal loads (mode 0, read: folds them into registers
+ * and writes workgroups x 2 KiB of dst_dev) or copies them to dst_dev (mode
+ * 1), each of `workgroups` workgroups of 512 lanes taking one contiguous
+ * slab.  The benchmark times it to state the device's achievable linear
+ * HBM rate next to the specification's. */
+int thb_hbm_stream(const void* src_dev, void* dst_dev, uint64_t bytes, uint32_t mode, uint32_t workgroups,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

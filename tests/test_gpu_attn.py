@@ -310,8 +310,8 @@ def test_split_groups_combined_in_launch(torch_cuda, case):
 
 def test_llama3_full_shape_sampled(torch_cuda):
     """BASELINE config 2 at full size (B=32, ctx 4096, 32q/8kv/hd128, f16 KV,
-    scattered block tables): the oracle checks 3 sequences in full, and every
-    output is a convex combination of V (|y| <= max |V|)."""
+    scattered block tables): the oracle checks all 32 sequences in full, and
+    every output is a convex combination of V (|y| <= max |V|)."""
     torch = torch_cuda
     from flint_amd import ops
     from flint_amd.pool import RowMeta
@@ -331,13 +331,12 @@ def test_llama3_full_shape_sampled(torch_cuda):
     y = run_attn(torch, pool, rows, q, [ctx - 1] * B, list(range(B)))
     assert float(y.abs().max()) <= float(v.view(torch.float16).abs().max()) + 1e-3
     ref = oracle_layer(torch, pool)
-    for s in (0, 17, 31):
-        want = ref.attn(q[s:s + 1].cpu().numpy(), oracle.row_meta([ctx - 1], [s]), 1, 32, 1 / math.sqrt(128))
-        err = float(np.max(np.abs(y[s:s + 1].cpu().numpy() - want)))
-        say("llama3 full seq", s, err)
-        assert err <= TOL
-        if y.dtype == torch.float32:
-            assert err <= TIGHT, ("llama3 full seq", s, "precision regression", err)
+    want = ref.attn(q.cpu().numpy(), oracle.row_meta([ctx - 1] * B, list(range(B))), B, 32, 1 / math.sqrt(128))
+    errs = np.max(np.abs(y.cpu().numpy() - want).reshape(B, -1), axis=1)
+    say("llama3 full shape: max |gpu - oracle| per sequence", float(errs.min()), "...", float(errs.max()))
+    assert float(errs.max()) <= TOL
+    if y.dtype == torch.float32:
+        assert float(errs.max()) <= TIGHT, ("llama3 full shape", "precision regression", float(errs.max()))
 
 
 def test_attn_errors(torch_cuda):
