@@ -41,7 +41,9 @@
 //    partitions writes (m, l, o) per partition and a second kernel merges
 //    them in partition order; there are no device-wide fences or atomics.
 #include <algorithm>
+#include <array>
 #include <cmath>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <queue>
@@ -78,6 +80,7 @@ constexpr uint32_t kBlockWords = 9;   // g0, ng, seq, lo, hi, n_parts, base, ple
 // Work-item records carry their group's (or block's) words and the
 // partition index, so a workgroup finds its work in one dependent load.
 constexpr uint32_t kItemWords = kGroupWords + 1;
+constexpr uint32_t kNoItem = 0xFFFFFFFFu;  // the empty second half of a prefill pair
 constexpr uint32_t kBItemWords = kBlockWords + 1;
 
 // Waves per workgroup and tiles in flight per wave of each head_dim
@@ -122,7 +125,10 @@ struct AttnArgs {
     const uint32_t* items;   // decode work items: group words + partition (kItemWords each)
     const uint32_t* ranges;  // [m][2]: lo, hi
     const uint32_t* bitems;  // prefill work items: block words + partition (kBItemWords each)
-    const uint32_t* order;   // attn_mixed: launch order of decode items and prefill blocks (bit 31)
+    // attn_prefill_wide: pairs of prefill work items one workgroup runs in
+    // turn (first, second or kNoItem), 2 words each
+    const uint32_t* bpairs;
+    const uint32_t* order;   // attn_mixed: launch order of decode items and prefill pairs (bit 31)
     const uint32_t* merge_groups;  // attn_merge: the groups that span several partitions
     const uint32_t* table;
     uint16_t* k;
@@ -1361,6 +1367,16 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
 #ifndef THB_PREFILL_NCG
 #define THB_PREFILL_NCG 2
 #endif
+// Wave priority by phase in attn_prefill_wide (0: none; 1: the products'
+// phases high, the probabilities' low; 2: the reverse).
+#ifndef THB_PREFILL_PRIO
+#define THB_PREFILL_PRIO 0
+#endif
+template <bool MATRIX>
+__device__ __forceinline__ void phase_prio() {
+    if constexpr (THB_PREFILL_PRIO == 1) __builtin_amdgcn_s_setprio(MATRIX ? 1 : 0);
+    if constexpr (THB_PREFILL_PRIO == 2) __builtin_amdgcn_s_setprio(MATRIX ? 0 : 1);
+}
 // LDS of one prefill workgroup: the double-buffered K and V tiles and the
 // partition's page list.
 template <int HD>
@@ -1395,18 +1411,34 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t a4 = lane >> 4, c = lane & 15u;
-    const uint32_t bitem = bid / a.n_kvh, kvh = bid - bitem * a.n_kvh;
+    const uint32_t pr = bid / a.n_kvh, kvh = bid - pr * a.n_kvh;
 
-    const uint32_t* Bk = a.bitems + static_cast<uint64_t>(bitem) * kBItemWords;
-    const uint32_t g0 = Bk[0], ng = Bk[1], seq = Bk[2], blo = Bk[3], bhi = Bk[4];
-    const uint32_t n_parts = Bk[5], bbase = Bk[6], P = Bk[7];
-    const uint32_t part = Bk[kBlockWords];
-    const uint32_t pbeg = bbase + part * P;
-    const uint32_t tb = max(blo, pbeg), te = min(bhi, pbeg + P);
+    // A pair of prefill work items of one sequence and partition (the host
+    // pairs a chunk's longest block with its shortest): the workgroup runs
+    // the first, then the second, over one stream of tiles (the second's
+    // first tile is loaded while the first's last is computed) and one page
+    // list (the union of their keys), so the launch's fixed costs are paid
+    // once per pair.  Each item's arithmetic is exactly that of a workgroup
+    // of its own.
+    const uint32_t it0 = a.bpairs[2 * pr], it1 = a.bpairs[2 * pr + 1];
+    const bool two = it1 != kNoItem;
+    const uint32_t* B0 = a.bitems + static_cast<uint64_t>(it0) * kBItemWords;
+    const uint32_t* B1 = a.bitems + static_cast<uint64_t>(two ? it1 : it0) * kBItemWords;
+    // Both items start their partition at the same key (the host pairs
+    // only such items); the page list spans the longer of the two.
+    const uint32_t seq = B0[2];
+    const uint32_t pbeg = B0[6] + B0[kBlockWords] * B0[7];
+    const uint32_t P = max(B0[7], B1[7]);
     const uint32_t hd = a.head_dim;
     const uint32_t pshift = a.page_shift;
     const uint32_t pmask = (1u << pshift) - 1u;
-    const uint32_t last = te > 0 ? te - 1 : 0;
+    // Per item: its keys [tb, te) in this partition, its first tile and tile
+    // count (scalars, selected by the item index: no indexed arrays).
+    const uint32_t tb0 = max(B0[3], pbeg), te0 = min(B0[4], pbeg + B0[7]);
+    const uint32_t tb1 = max(B1[3], pbeg), te1 = two ? min(B1[4], pbeg + B1[7]) : tb1;
+    const uint32_t tf0 = tb0 & ~31u, tf1 = tb1 & ~31u;
+    const uint32_t nt0 = te0 > tf0 ? (te0 - tf0 + TT - 1) / TT : 0u;
+    const uint32_t nt1 = te1 > tf1 ? (te1 - tf1 + TT - 1) / TT : 0u;
 
     {
         const uint32_t npg = P >> pshift;
@@ -1414,45 +1446,51 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
         const uint32_t* trow = a.table + static_cast<uint64_t>(seq) * a.max_pages;
         for (uint32_t i = tid; i < npg; i += NT) {
             const uint32_t lp = lp0 + i;
-            const bool used = tb < te && (lp << pshift) < te && ((lp + 1) << pshift) > tb;
+            const bool used = (tb0 < te0 && (lp << pshift) < te0 && ((lp + 1) << pshift) > tb0) ||
+                              (tb1 < te1 && (lp << pshift) < te1 && ((lp + 1) << pshift) > tb1);
             const uint32_t pg = used ? trow[lp] : 0u;
             s_page[i] = pg < a.pages ? pg : 0u;  // block_pages: a page outside the pool reads page 0
         }
     }
 
-    // This wave's two column groups; [wlo, whi) spans both groups' keys.
-    // Each column's key range is requested here and used after the first
-    // tile's loads and the queries' loads are out, so the three round trips
-    // overlap.
+    // This wave's two column groups of the current item; [wlo, whi) spans
+    // both groups' keys.  Each column's key range is requested here and used
+    // after the first tile's loads and the queries' loads are out, so the
+    // round trips overlap.
     bool con[NCG];
     uint32_t row[NCG], head[NCG], clo[NCG], chi[NCG], cspan[NCG], item0[NCG];
     uint32_t wlo = 0xFFFFFFFFu, whi = 0;
+    auto setup = [&](const uint32_t* Bk, uint32_t tb, uint32_t te) {
+        const uint32_t g0 = Bk[0], ng = Bk[1];
+        wlo = 0xFFFFFFFFu;
+        whi = 0;
 #pragma unroll
-    for (int g = 0; g < NCG; g++) {
-        const uint32_t gi = NCG * wave + g;
-        const bool gon = gi < ng;
-        const uint32_t* G = a.groups + (g0 + (gon ? gi : 0u)) * kGroupWords;
-        const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3];
-        item0[g] = G[10];
-        const uint32_t ncols = gon ? R * H : 0u;
-        con[g] = c < ncols;
-        const uint32_t rr = con[g] ? c / H : 0u;
-        row[g] = r0 + rr;
-        head[g] = kvh * a.nq_per_kv + h0 + (con[g] ? c - rr * H : 0u);
-        clo[g] = a.ranges[2 * row[g]];  // row r0 of an unused column: a valid index
-        chi[g] = a.ranges[2 * row[g] + 1];
-        if (gon) {
-            const uint32_t glo = max(G[5], tb), ghi = min(G[6], te);
-            if (glo < ghi) {
-                wlo = min(wlo, glo);
-                whi = max(whi, ghi);
+        for (int g = 0; g < NCG; g++) {
+            const uint32_t gi = NCG * wave + g;
+            const bool gon = gi < ng;
+            const uint32_t* G = a.groups + (g0 + (gon ? gi : 0u)) * kGroupWords;
+            const uint32_t r0 = G[0], R = G[1], h0 = G[2], H = G[3];
+            item0[g] = G[10];
+            const uint32_t ncols = gon ? R * H : 0u;
+            con[g] = c < ncols;
+            const uint32_t rr = con[g] ? c / H : 0u;
+            row[g] = r0 + rr;
+            head[g] = kvh * a.nq_per_kv + h0 + (con[g] ? c - rr * H : 0u);
+            clo[g] = a.ranges[2 * row[g]];  // row r0 of an unused column: a valid index
+            chi[g] = a.ranges[2 * row[g] + 1];
+            if (gon) {
+                const uint32_t glo = max(G[5], tb), ghi = min(G[6], te);
+                if (glo < ghi) {
+                    wlo = min(wlo, glo);
+                    whi = max(whi, ghi);
+                }
             }
         }
-    }
+    };
     // Per group, the keys every column reads: a 32-key step inside
     // [lomax, himin) needs no mask.
     uint32_t lomax[NCG], himin[NCG];
-    auto column_ranges = [&]() {
+    auto column_ranges = [&](uint32_t tb, uint32_t te) {
 #pragma unroll
         for (int g = 0; g < NCG; g++) {
             clo[g] = con[g] ? max(clo[g], tb) : 0u;
@@ -1473,11 +1511,12 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
     const uint16_t* kplane = a.k + static_cast<uint64_t>(kvh) * a.plane;
     const uint16_t* vplane = a.v + static_cast<uint64_t>(kvh) * a.plane;
 
-    // Global -> registers for one tile; tokens outside [tb, te) are clamped
-    // into it (their scores are masked).  At the template's own head_dim
-    // every unit is in range: the page numbers of all units are read from
-    // LDS first (one round trip), then every load is issued, with no guards.
-    auto load = [&](uint32_t t0, u32x4 (&kr)[KPT], u32x4 (&vr)[VPT][2]) {
+    // Global -> registers for one tile of an item whose keys are [tb, last];
+    // tokens outside are clamped into it (their scores are masked).  At the
+    // template's own head_dim every unit is in range: the page numbers of all
+    // units are read from LDS first (one round trip), then every load is
+    // issued, with no guards.
+    auto load = [&](uint32_t t0, uint32_t tb, uint32_t last, u32x4 (&kr)[KPT], u32x4 (&vr)[VPT][2]) {
         if constexpr (KU % NT == 0 && VP % NT == 0) {
             if (hd == static_cast<uint32_t>(HD)) {
                 uint32_t kpg[KPT], kin[KPT], vpg[VPT][2], vin[VPT][2];
@@ -1565,13 +1604,6 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
     // of probabilities (all 32 keys of a step, all four lane groups).
     float m[NCG];
     f32x4 o[NCG][MT], lsum[NCG];
-#pragma unroll
-    for (int g = 0; g < NCG; g++) {
-        m[g] = kFloor;
-        lsum[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int i = 0; i < MT; i++) o[g][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
     const float tanh_c = 2.8853900817779268f * a.qpost;  // 2 log2(e) |qscale|
     u32x4 ones;  // eight 1.0 in the KV type
     {
@@ -1583,8 +1615,16 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
     // qpost without a cap).
     const float inv_qpost = 1.0f / a.qpost;
     float thr[NCG];
+    auto init_state = [&]() {
 #pragma unroll
-    for (int g = 0; g < NCG; g++) thr[g] = CAP ? m[g] + kTau : (m[g] + kTau) * inv_qpost;
+        for (int g = 0; g < NCG; g++) {
+            m[g] = kFloor;
+            lsum[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < MT; i++) o[g][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            thr[g] = CAP ? m[g] + kTau : (m[g] + kTau) * inv_qpost;
+        }
+    };
 
     // 32-key steps, software-pipelined: the QK^T products of step s + 1 are
     // issued before the softmax of step s, so the matrix cores work on them
@@ -1594,6 +1634,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
     // mask is one unsigned range compare per score, and steps inside every
     // column's keys skip it.
     auto qk_step = [&](int buf, int st, f32x4 (&sc)[NCG][2]) {
+        phase_prio<true>();
 #pragma unroll
         for (int g = 0; g < NCG; g++) sc[g][0] = sc[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1616,6 +1657,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
         }
     };
     auto softmax_pv = [&](int buf, int st, uint32_t ts, const f32x4 (&sc)[NCG][2]) {
+        phase_prio<false>();
         in8 ph[NCG], pl[NCG];
         // Without the query's low half (the lean f16 kernel, whose registers
         // allow it) the step's V operands are requested before the softmax,
@@ -1682,6 +1724,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
             // exact softmax on N(0,1) .. N(0,4) data, both halves 3e-7.
             O::split8_fast(p, ph[g], pl[g]);
         }
+        phase_prio<true>();
 #pragma unroll
         for (int i = 0; i < MT; i += 2) {
             u32x4 vv[2];
@@ -1722,53 +1765,82 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
         }
     };
 
-    const uint32_t t_first = tb & ~31u;
-    const uint32_t n_tiles = te > t_first ? (te - t_first + TT - 1) / TT : 0u;
+    // Outputs of the current item: the normalised rows, or this partition's
+    // (m, l, o) when the item's block spans several partitions.
+    auto finish = [&](const uint32_t* Bk) {
+        const uint32_t n_parts = Bk[5], part = Bk[kBlockWords];
+#pragma unroll
+        for (int g = 0; g < NCG; g++) {
+            const float lg = lsum[g][0];
+            if (!con[g]) continue;
+            if (n_parts == 1) {
+                const float inv = 1.0f / lg;
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const uint32_t d = 16u * i + 4u * a4;
+                    if (d >= hd) continue;
+                    const f32x4 yv = o[g][i] * inv;
+                    const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
+                    store_y<4, FULL>(a, row[g], head[g], d, v4);
+                }
+                continue;
+            }
+            const uint64_t pb = (static_cast<uint64_t>(item0[g] + part) * a.n_kvh + kvh) * kCols + c;
+#pragma unroll
+            for (int i = 0; i < MT; i++)
+                *reinterpret_cast<f32x4*>(a.part_o + pb * HD + 16u * i + 4u * a4) = o[g][i];
+            if (a4 == 0) {
+                a.part_ml[2 * pb] = m[g];
+                a.part_ml[2 * pb + 1] = lg;
+            }
+        }
+    };
+
     __syncthreads();  // s_page complete
-    {
-        u32x4 kr[KPT], vr[VPT][2];
-        if (n_tiles) load(t_first, kr, vr);
+    u32x4 kr[KPT], vr[VPT][2];
+    uint32_t k_tile = 0;  // tiles of the pair computed so far (LDS buffer parity)
+    const uint32_t last1 = te1 > 0 ? te1 - 1 : 0;
+    // One item of the pair: straight-line code per item (a loop over the two
+    // items kept both items' state live and spilled).
+    auto run_item = [&](auto second_c) {
+        constexpr bool second = decltype(second_c)::value;
+        const uint32_t* Bk = second ? B1 : B0;
+        const uint32_t tb = second ? tb1 : tb0, te = second ? te1 : te0;
+        const uint32_t tf = second ? tf1 : tf0, nt = second ? nt1 : nt0;
+        const uint32_t last = te > 0 ? te - 1 : 0;
+        setup(Bk, tb, te);
+        if constexpr (!second) {
+            // The pair's first tile: the first item's, or the second's if
+            // the first has none.
+            if (nt0)
+                load(tf0, tb0, last, kr, vr);
+            else if (nt1)
+                load(tf1, tb1, last1, kr, vr);
+        }
         // The queries are loaded and split while the first tile's loads are
         // in flight (their round trips overlap).
 #pragma unroll
         for (int g = 0; g < NCG; g++) load_q<KS, O, FULL>(a, con[g], row[g], head[g], a4, qh[g], ql[g], a.qpre);
-        column_ranges();
-        if (n_tiles) store(0, kr, vr);
+        column_ranges(tb, te);
+        init_state();
+        if constexpr (!second)
+            if (nt0 || nt1) store(0, kr, vr);
         __syncthreads();
-        for (uint32_t i = 0; i < n_tiles; i++) {
-            const uint32_t t0 = t_first + i * TT;
-            const bool more = i + 1 < n_tiles;
-            if (more) load(t0 + TT, kr, vr);
-            compute(static_cast<int>(i & 1u), t0);
-            if (more) store(static_cast<int>((i + 1) & 1u), kr, vr);
+        // The second item's first tile follows the first item's last.
+        const uint32_t nt_next = second ? 0u : nt1;
+        for (uint32_t i = 0; i < nt; i++, k_tile++) {
+            const uint32_t t0 = tf + i * TT;
+            const bool own = i + 1 < nt;
+            const bool more = own || nt_next > 0;
+            if (more) load(own ? t0 + TT : tf1, own ? tb : tb1, own ? last : last1, kr, vr);
+            compute(static_cast<int>(k_tile & 1u), t0);
+            if (more) store(static_cast<int>((k_tile + 1) & 1u), kr, vr);
             __syncthreads();
         }
-    }
-#pragma unroll
-    for (int g = 0; g < NCG; g++) {
-        const float lg = lsum[g][0];
-        if (!con[g]) continue;
-        if (n_parts == 1) {
-            const float inv = 1.0f / lg;
-#pragma unroll
-            for (int i = 0; i < MT; i++) {
-                const uint32_t d = 16u * i + 4u * a4;
-                if (d >= hd) continue;
-                const f32x4 yv = o[g][i] * inv;
-                const float v4[4] = {yv[0], yv[1], yv[2], yv[3]};
-                store_y<4, FULL>(a, row[g], head[g], d, v4);
-            }
-            continue;
-        }
-        const uint64_t pb = (static_cast<uint64_t>(item0[g] + part) * a.n_kvh + kvh) * kCols + c;
-#pragma unroll
-        for (int i = 0; i < MT; i++)
-            *reinterpret_cast<f32x4*>(a.part_o + pb * HD + 16u * i + 4u * a4) = o[g][i];
-        if (a4 == 0) {
-            a.part_ml[2 * pb] = m[g];
-            a.part_ml[2 * pb + 1] = lg;
-        }
-    }
+        finish(Bk);
+    };
+    run_item(std::integral_constant<bool, false>{});
+    if (two) run_item(std::integral_constant<bool, true>{});
 }
 
 template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
@@ -2305,6 +2377,39 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     }
     const uint32_t n_bitems = static_cast<uint32_t>(bitems.size());
     if (n_items > 0x7FFFFFFFu || n_groups > 0x7FFFFFFFu) return fail(THB_ERR_CONFIG, "attention call too large");
+    // attn_prefill_wide runs pairs of work items: among the items of one
+    // sequence whose partitions start at the same key (one page list serves
+    // both), the k-th longest with the k-th shortest, so that each pair holds
+    // about the same number of tiles; pairs are launched longest first.  Work
+    // per item: its tiles.
+    std::vector<uint32_t> bpairs;
+    auto bitem_tiles = [&](uint32_t i) {
+        const uint32_t* bk = &blocks[static_cast<size_t>(bitems[i]) * kBlockWords];
+        const uint64_t p0 = uint64_t(bk[6]) + uint64_t(i - bk[8]) * bk[7];
+        const uint64_t tb = std::max<uint64_t>(bk[3], p0), te = std::min<uint64_t>(bk[4], p0 + bk[7]);
+        return te > (tb & ~uint64_t(31)) ? (te - (tb & ~uint64_t(31)) + 63) / 64 : uint64_t(0);
+    };
+    if (wide) {
+        // (seq, first key of the item's partition) -> items
+        std::map<std::array<uint32_t, 2>, std::vector<uint32_t>> same;
+        for (uint32_t i = 0; i < n_bitems; i++) {
+            const uint32_t* bk = &blocks[static_cast<size_t>(bitems[i]) * kBlockWords];
+            same[{bk[2], bk[6] + (i - bk[8]) * bk[7]}].push_back(i);
+        }
+        std::vector<std::pair<uint64_t, std::array<uint32_t, 2>>> prs;
+        for (auto& kv : same) {
+            auto& v = kv.second;
+            std::stable_sort(v.begin(), v.end(), [&](uint32_t x, uint32_t y) { return bitem_tiles(x) > bitem_tiles(y); });
+            for (size_t k = 0, n = v.size(); k < (n + 1) / 2; k++) {
+                const bool solo = 2 * k + 1 == n;
+                const uint32_t x = v[k], y = solo ? kNoItem : v[n - 1 - k];
+                prs.push_back({bitem_tiles(x) + (solo ? 0 : bitem_tiles(y)), {x, y}});
+            }
+        }
+        std::stable_sort(prs.begin(), prs.end(), [](const auto& x, const auto& y) { return x.first > y.first; });
+        for (auto& pp : prs) bpairs.insert(bpairs.end(), {pp.second[0], pp.second[1]});
+    }
+    const uint32_t n_bpairs = static_cast<uint32_t>(bpairs.size() / 2);
 
     std::vector<uint32_t> blob;
     blob.reserve(groups.size() + n_items * kItemWords + 2 * m + n_bitems * kBItemWords);
@@ -2323,6 +2428,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         blob.insert(blob.end(), bk, bk + kBlockWords);
         blob.push_back(i - bk[8]);
     }
+    blob.insert(blob.end(), bpairs.begin(), bpairs.end());
     // A call with both kinds of work runs them in one launch (attn_mixed).
     // Its order comes from a list schedule over record slots (CUs / KV
     // heads; a record is a decode item or a prefill block over all its KV
@@ -2342,18 +2448,17 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
         const uint32_t n_kvh = pool->kv_heads;
         std::vector<std::pair<double, uint32_t>> dec, pre;  // (bytes per workgroup | us, record)
         dec.reserve(n_items);
-        pre.reserve(n_bitems);
+        pre.reserve(n_bpairs);
         for (uint32_t i = 0; i < n_items; i++) {
             const uint32_t* gr = &groups[static_cast<size_t>(items[i]) * kGroupWords];
             const uint64_t p0 = uint64_t(gr[8]) + uint64_t(i - gr[10]) * gr[9];
             const uint64_t keys = gr[6] > p0 ? std::min<uint64_t>(gr[9], gr[6] - p0) : 0;
             dec.push_back({static_cast<double>(keys) * 4.0 * hd, i});
         }
-        for (uint32_t i = 0; i < n_bitems; i++) {
-            const uint32_t* bk = &blocks[static_cast<size_t>(bitems[i]) * kBlockWords];
-            const uint64_t p0 = uint64_t(bk[6]) + uint64_t(i - bk[8]) * bk[7];
-            const uint64_t keys = bk[4] > p0 ? std::min<uint64_t>(bk[7], bk[4] - p0) : 0;
-            pre.push_back({10.0 + static_cast<double>((keys + 63) / 64) * 4.5 * hd_t / 128.0, 0x80000000u | i});
+        for (uint32_t i = 0; i < n_bpairs; i++) {  // one fixed cost per pair
+            uint64_t tiles = bitem_tiles(bpairs[2 * i]);
+            if (bpairs[2 * i + 1] != kNoItem) tiles += bitem_tiles(bpairs[2 * i + 1]);
+            pre.push_back({10.0 + static_cast<double>(tiles) * 4.5 * hd_t / 128.0, 0x80000000u | i});
         }
         auto longest_first = [](const std::pair<double, uint32_t>& x, const std::pair<double, uint32_t>& y) {
             return x.first > y.first;
@@ -2422,6 +2527,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     plan.n_items = n_items;
     plan.n_blocks = n_blocks;
     plan.n_bitems = n_bitems;
+    plan.n_bpairs = n_bpairs;
     plan.n_slots = n_slots;
     plan.split = any_split;
     plan.n_merge = n_merge;
@@ -2567,7 +2673,8 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.items = blob + static_cast<size_t>(plan.n_groups) * kGroupWords;
     a.ranges = a.items + static_cast<size_t>(plan.n_items) * kItemWords;
     a.bitems = a.ranges + 2 * static_cast<size_t>(sp.m);
-    a.order = a.bitems + static_cast<size_t>(plan.n_bitems) * kBItemWords;
+    a.bpairs = a.bitems + static_cast<size_t>(plan.n_bitems) * kBItemWords;
+    a.order = a.bpairs + 2 * static_cast<size_t>(plan.n_bpairs);
     a.merge_groups = blob + plan.merge_off;
     a.table = pool->table_dev;
     a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
@@ -2604,7 +2711,8 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.krope = rope ? rope_dev(*rope, false) : RopeDev{};
     const bool f16 = pool->kv_dtype == THB_KV_F16_RNE;
     const uint64_t n_wg = static_cast<uint64_t>(plan.n_items) * pool->kv_heads;
-    const uint64_t n_pwg = static_cast<uint64_t>(plan.n_bitems) * pool->kv_heads;
+    // attn_prefill_wide runs pairs of prefill items, attn_prefill single items
+    const uint64_t n_pwg = static_cast<uint64_t>(plan.wide ? plan.n_bpairs : plan.n_bitems) * pool->kv_heads;
     if (n_wg > 0x7FFFFFFFull || n_pwg > 0x7FFFFFFFull)
         throw HipError{hipErrorInvalidConfiguration, "attention grid too large"};
     // A call with decode items and attn_prefill_wide blocks runs them in one

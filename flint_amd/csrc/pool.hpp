@@ -34,6 +34,7 @@ struct AttnPlan {
     // value
     uint32_t n_groups = 0, n_items = 0;     // decode work items
     uint32_t n_blocks = 0, n_bitems = 0;    // prefill blocks and their work items
+    uint32_t n_bpairs = 0;                  // pairs of work items (attn_prefill_wide)
     uint32_t n_slots = 0;                   // partial-result slots (all groups' partitions)
     uint32_t hd_t = 0;   // head_dim template of the kernel
     bool wide = false;   // prefill blocks run attn_prefill_wide (head_dim <= 128)
@@ -42,7 +43,7 @@ struct AttnPlan {
     uint32_t n_merge = 0, merge_off = 0;  // groups of several partitions: count, blob offset (words)
     uint32_t n_merge_dec = 0;             // of those, decode groups (listed first)
     bool fusable = false;  // an append of the call's rows can run inside the launch
-    std::vector<uint32_t> blob;  // [groups | items | row ranges | prefill items | order | merge list]
+    std::vector<uint32_t> blob;  // [groups | items | row ranges | prefill items | pairs | order | merge list]
     DevBuf dev;                  // blob on the device, when uploaded
     bool uploaded = false;
     uint64_t last_use = 0;
