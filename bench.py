@@ -697,6 +697,27 @@ def measure_secondary(name, args):
             lb = B * keys * nkv * hd * 2 * 2 + m * nkv * hd * 2 * 2
             out[f"{kind}_layer"] = {"us": round(lus, 1), "pct_of_peak": round(100 * lb / (lus * 1e3) / PEAK_HBM_GBPS, 1)}
         byts = B * (4096 + ctx + 8) // 2 * nkv * hd * 2 * 2 + m * nkv * hd * 2 * 2
+        # Gemma-2-shaped chunked prefill: 8 fresh 512-token causal chunks, window 4096, soft-cap 50
+        # (the head_dim-256 path of attn_prefill_wide), two layers of their own pool
+        npre, pre = 8, 512
+        pp = make([pre] * npre, npre * pre // 16, nkv, hd, 2)
+        for s_ in range(npre):
+            pp.alloc(s_, 0, pre)
+        randomize(pp, range(2), 1014)
+        rp = RowMeta(npre * pre)
+        rp.write([p for _ in range(npre) for p in range(pre)], [s_ for s_ in range(npre) for _ in range(pre)],
+                 npre * pre)
+        qp = torch.randn(npre * pre, nq, hd, device=dev, generator=g).half()
+        yp = torch.empty_like(qp)
+        spp = spec(rp, nq, hd, npre * pre, window=4096, softcap=50.0)
+        pus = _time_steps(torch, lambda: [ops.attn(qp, pp, layer, yp, spp) for layer in range(2)],
+                          args.steps, args.warmup) / 2
+        pflops = npre * (pre * (pre + 1) // 2) * nq * hd * 4
+        out["gemma_prefill"] = {"us_per_layer": round(pus, 1), "TFLOPs": round(pflops / (pus * 1e-6) / 1e12, 1),
+                                "mfma_frac_of_2.5PF": round(pflops / (pus * 1e-6) / 2.5e15, 4), "flops": pflops,
+                                "note": "8 x 512 causal rows, 16q/8kv/hd256, window 4096, soft-cap 50, f16 queries "
+                                        "and outputs; unmasked (q,k) pairs x 4 x nq x hd"}
+        pp.close()
         out["config"] = {"workload": "gemma2-9b C4: B=16 at ctx 8192, 16q/8kv/hd256, soft-cap 50, layers alternate "
                                      "window 4096 / global; step = append 4 drafts + 4-row causal verify (fused), "
                                      f"{L} layers"}

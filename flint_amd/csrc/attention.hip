@@ -1372,6 +1372,11 @@ __global__ __launch_bounds__(64 * W, HD <= 128 ? 4 : 1) void attn_prefill(AttnAr
 #ifndef THB_PREFILL_PRIO
 #define THB_PREFILL_PRIO 0
 #endif
+// Query groups per wave of attn_prefill_wide: two up to head_dim 128 (every
+// K or V operand read from LDS feeds both), one at 256 (its accumulators
+// alone take 64 registers).
+constexpr int prefill_ncg(int hd) { return hd > 128 ? 1 : THB_PREFILL_NCG; }
+
 template <bool MATRIX>
 __device__ __forceinline__ void phase_prio() {
     if constexpr (THB_PREFILL_PRIO == 1) __builtin_amdgcn_s_setprio(MATRIX ? 1 : 0);
@@ -1392,7 +1397,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
     typedef typename O::in8 in8;
     constexpr int KS = HD / 32;
     constexpr int MT = HD / 16;
-    constexpr int NCG = THB_PREFILL_NCG;   // column groups per wave
+    constexpr int NCG = prefill_ncg(HD);   // column groups per wave
     constexpr int TT = THB_PREFILL_TILE;   // tokens per tile
     constexpr int NS = TT / 32;            // 32-token steps per tile
     constexpr int CPH = HD / 8;            // 8-dim chunks of a key
@@ -1663,7 +1668,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
         // allow it) the step's V operands are requested before the softmax,
         // whose vector work covers their LDS latency; the other kernels read
         // them pair by pair beside the products.
-        constexpr bool VPRE = !FULL && !QLO;
+        constexpr bool VPRE = !FULL && !QLO && HD <= 128;  // 64 more registers at 256
         auto vread = [&](int i) {
             const uint32_t d = 16u * i + c;
             return s_v[buf][(st * HD + d) * 4 + (a4 ^ ((d >> 2) & 3u))];
@@ -2097,14 +2102,15 @@ void launch(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s
     }
 }
 
-// Waves of attn_prefill_wide (head_dim <= 128; two query groups per wave).
+// Waves of attn_prefill_wide (head_dim <= 256).
 #ifndef THB_PREFILL_WAVES
 #define THB_PREFILL_WAVES 8
 #endif
-// Query groups per prefill block: 2 per wave of attn_prefill_wide, 1 per wave
-// of attn_prefill (wider heads).
+// Query groups per prefill block: prefill_ncg per wave of attn_prefill_wide,
+// 1 per wave of attn_prefill (head_dim 512).
 constexpr uint32_t block_groups(bool wide, uint32_t hd_t) {
-    return wide ? THB_PREFILL_NCG * THB_PREFILL_WAVES : static_cast<uint32_t>(waves_for(static_cast<int>(hd_t)));
+    return wide ? static_cast<uint32_t>(prefill_ncg(static_cast<int>(hd_t))) * THB_PREFILL_WAVES
+                : static_cast<uint32_t>(waves_for(static_cast<int>(hd_t)));
 }
 
 // Score scale applied to the query (log2 units, or 1 / softcap).
@@ -2112,8 +2118,8 @@ float q_scale(const thb_attn_spec& sp) {
     return sp.softcap > 0.0f ? sp.scale / sp.softcap : sp.scale * 1.4426950408889634f;
 }
 
-// attn_prefill_wide serves head_dim <= 128; attn_prefill the wider heads.
-bool prefill_wide(uint32_t hd_t) { return hd_t <= 128; }
+// attn_prefill_wide serves head_dim <= 256; attn_prefill head_dim 512.
+bool prefill_wide(uint32_t hd_t) { return hd_t <= 256; }
 
 // An f16 query read as it is (the lean kernels: no rotation, no norm)
 // against f16 keys: its low half after the split is exactly zero, and the
@@ -2122,7 +2128,7 @@ bool query_exact(const AttnArgs& a, bool f16_kv) { return f16_kv && !a.full && a
 
 template <int HD, bool F16>
 void launch_prefill_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
-    if constexpr (HD <= 128) {
+    if constexpr (HD <= 256) {
         constexpr int W = THB_PREFILL_WAVES;
         const bool cap = a.cap2 != 0.0f;
         if (a.full && cap)
@@ -2442,7 +2448,7 @@ int build_plan(thb_pool* pool, const thb_rows* rows, const thb_attn_spec& sp, ui
     // starts); a prefill block costs ~10 us plus ~4.5 us per 64-key tile
     // (head_dim 128, beside streaming decode).  The order changes no row's
     // arithmetic.
-    const bool mixed = n_items > 0 && n_bitems > 0 && wide && THB_ATTN_WAVES == THB_PREFILL_WAVES;
+    const bool mixed = n_items > 0 && n_bitems > 0 && wide && hd_t <= 128 && THB_ATTN_WAVES == THB_PREFILL_WAVES;
     if (mixed) {
         constexpr double kHbmBytesPerUs = 6.2e6, kCuBytesPerUs = 3.7e4 * THB_PREFILL_WAVES / 8;
         const uint32_t n_kvh = pool->kv_heads;

@@ -431,7 +431,7 @@ def test_fused_append_matches_separate_calls(torch_cuda, case):
         assert err <= TIGHT, (name, "precision regression", err)
 
 
-@pytest.mark.parametrize("hd,nq,nkv", [(128, 32, 8), (64, 14, 2)])
+@pytest.mark.parametrize("hd,nq,nkv", [(128, 32, 8), (64, 14, 2), (256, 16, 8)])
 def test_prefill_f16_query_bit_identical_to_f32(torch_cuda, hd, nq, nkv):
     """An f16 query against f16 keys takes the prefill kernels that skip the
     products of the query's low half (exactly zero after the split).  The
@@ -536,3 +536,51 @@ def test_chunked_prefill_parity(torch_cuda, case):
                                                               causal=True, seq=None, args=rows, softcap=cap))
     torch.cuda.synchronize()
     assert torch.equal(ys, y[:chunk]), "batch == solo"
+
+
+def test_gemma2_prefill_chunks(torch_cuda):
+    """Gemma-2-9B geometry (16q/8kv/hd256, window 4096, soft-cap 50): eight
+    fresh 512-token causal chunks in one call, the head_dim-256 path of
+    attn_prefill_wide (pairs of 64-row blocks, 16x16x32 products).  Three
+    chunks in full against the oracle; one chunk called alone is
+    bit-identical to the batch."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    nq, nkv, hd, n, pre = 16, 8, 256, 8, 512
+    lens = [pre] * n
+    pool = make_pool(lens, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype="f16")
+    scattered_alloc(pool, lens, random.Random(2024), 16)
+    rows = RowMeta(n * pre)
+    fill(torch, pool, RowMeta(256), lens, seed=2024, scale=2.0)
+    positions = [p for _ in range(n) for p in range(pre)]
+    seqs = [s for s in range(n) for _ in range(pre)]
+    m = len(seqs)
+    rows.write(positions, seqs, m)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2024)
+    q = (torch.randn(m, nq, hd, device="cuda", generator=g) * 2.0).half()
+    y = torch.empty(m, nq, hd, device="cuda")
+    spec = ops.AttnSpec(q_heads=nq, window=4096, scale=1.0 / math.sqrt(hd), m=m, causal=True, seq=None, args=rows,
+                        softcap=50.0)
+    ops.attn(q, pool, 0, y, spec)
+    torch.cuda.synchronize()
+    ref = oracle_layer(torch, pool)
+    qn, got_all = q.float().cpu().numpy(), y.cpu().numpy()
+    assert np.all(np.isfinite(got_all))
+    for c in (0, 5, 7):  # whole chunks: the oracle derives each row's keys from its chunk's rows
+        r = slice(c * pre, (c + 1) * pre)
+        want = ref.attn(qn[r], oracle.row_meta(positions[r], seqs[r]), pre, nq, 1.0 / math.sqrt(hd), window=4096,
+                        softcap=50.0)
+        err = float(np.max(np.abs(got_all[r] - want)))
+        say("gemma2 prefill chunk", c, "max abs err", err)
+        assert err <= TIGHT, (c, err)
+    rows1 = RowMeta(pre)
+    rows1.write(positions[3 * pre:4 * pre], seqs[3 * pre:4 * pre], pre)
+    y1 = torch.empty(pre, nq, hd, device="cuda")
+    ops.attn(q[3 * pre:4 * pre].contiguous(), pool, 0, y1,
+             ops.AttnSpec(q_heads=nq, window=4096, scale=1.0 / math.sqrt(hd), m=pre, causal=True, seq=None,
+                          args=rows1, softcap=50.0))
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y[3 * pre:4 * pre]), "batch == solo"
