@@ -632,6 +632,33 @@ def measure_secondary(name, args):
         us = _time_steps(torch, step, args.steps, args.warmup) / L
         byts = sum(c + 1 for c in ctx) * nkv * hd * 2 * 2 + 8 * pre * nkv * hd * 2 * 2
         flops = 8 * (pre * (pre + 1) // 2) * nq * hd * 4
+        # the same mixed step planned on the device (work-list plan) and captured in a HIP graph:
+        # one thb_dplan_build per step, then per layer kv_store + thb_attn_dplan; 5 steps per graph
+        plan = ops.DevicePlan(pool, max_m=m, q_heads=nq, prefill=True)
+        yg = torch.empty_like(q)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(5):
+                    plan.build(sp, q, yg)
+                    for layer in range(L):
+                        ops.kv_store(k, v, pool, layer, m, rows)
+                        plan.attn(layer, q, yg)
+        torch.cuda.current_stream().wait_stream(side)
+        gus = _time_steps(torch, graph.replay, max(1, args.steps // 5), 2) / (5 * L)
+        ops.kv_store_attn(k, v, q, pool, L - 1, y, sp)
+        torch.cuda.synchronize()
+        same = bool(torch.equal(y, yg))
+        del graph
+        plan.close()
+        out["list_plan_graph"] = {"us_per_layer": round(gus, 1), "eager_us_per_layer": round(us, 1),
+                                  "ratio_to_eager": round(gus / us, 3), "bit_identical_to_eager": same,
+                                  "note": "thb_dplan_create_ex(THB_DPLAN_PREFILL): decode rows and the 8 prefill "
+                                          "chunks planned on the device, captured (build once per step, kv_store "
+                                          "+ thb_attn_dplan per layer, 5 steps per graph) and replayed; eager = "
+                                          "one fused thb_attn_step per layer planned on the host"}
         # the prefill rows alone (their K/V already appended), for the matrix-core roofline
         rp = RowMeta(8 * pre)
         rp.write(positions[64:], seqs[64:], 8 * pre)
@@ -959,7 +986,8 @@ def main():
             rec = measure_secondary(name, sec)
             out[key] = {k: rec[k] for k in ("value", "unit", "us_per_layer_step", "pct_of_peak", "bytes_per_layer_step",
                                             "prefill", "norm_rope_step", "window_layer", "global_layer",
-                                            "gemma_prefill", "graph_step", "arena_bytes", "cpu_baseline")
+                                            "gemma_prefill", "graph_step", "list_plan_graph", "arena_bytes",
+                                            "cpu_baseline")
                         if k in rec and rec[k] is not None}
             out[key]["pct_of_read_ceiling"] = round(100 * rec["value"] / rd, 1)
             out[key]["workload"] = rec["config"]["workload"]

@@ -171,6 +171,7 @@ SIGNATURES = [
     ("thb_gemm_acc", _int, [_vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _vp]),
     ("thb_attn_noalloc", _int, [_vp, _u32, _vp, _vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_dplan_create", _int, [_vp, _u32, _u32, ctypes.POINTER(_vp)]),
+    ("thb_dplan_create_ex", _int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_vp)]),
     ("thb_dplan_destroy", None, [_vp]),
     ("thb_dplan_build", _int, [_vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_attn_dplan", _int, [_vp, _u32, _vp, _vp, _vp, _vp]),

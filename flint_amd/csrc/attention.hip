@@ -129,6 +129,8 @@ struct AttnArgs {
     // turn (first, second or kNoItem), 2 words each
     const uint32_t* bpairs;
     const uint32_t* order;   // attn_mixed: launch order of decode items and prefill pairs (bit 31)
+    // attn_list: the device plan's header (entries, claim counter, done counter)
+    uint32_t* list;
     const uint32_t* merge_groups;  // attn_merge: the groups that span several partitions
     const uint32_t* table;
     uint16_t* k;
@@ -650,7 +652,8 @@ struct DecodeLds : DecodeQLds<typename Ops<F16>::in8, HD / 32, q_in_lds(HD)> {
 // loads are kept in flight per wave: tile i + NB is requested as soon as
 // tile i has been consumed.
 template <int HD, bool F16, int W, int NB, bool FULL>
-__device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, DecodeLds<HD, F16, W>& L) {
+__device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, DecodeLds<HD, F16, W>& L,
+                                          uint32_t tid_arg) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
     typedef typename O::in4 in4;
@@ -663,7 +666,7 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
     auto& s_l = L.l;
     auto& s_arrived = L.arrived;
 
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = tid_arg;  // threadIdx.x (opaque in attn_list)
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t a4 = lane >> 4, c = lane & 15u;
     // 1-D grid, KV head fastest: consecutive workgroups share a work item,
@@ -1092,7 +1095,7 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, uint32_t bid, Decod
 template <int HD, bool F16, int W, int NB, bool FULL>
 __global__ __launch_bounds__(64 * W) void attn_mfma(AttnArgs a) {
     __shared__ DecodeLds<HD, F16, W> lds;
-    decode_wg<HD, F16, W, NB, FULL>(a, blockIdx.x, lds);
+    decode_wg<HD, F16, W, NB, FULL>(a, blockIdx.x, lds, threadIdx.x);
 }
 
 // Merges the partitions of every group that has more than one, in
@@ -1392,7 +1395,8 @@ struct PrefillLds {
 };
 
 template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
-__device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid, PrefillLds<HD>& L) {
+__device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid, PrefillLds<HD>& L,
+                                                uint32_t tid_arg) {
     using O = Ops<F16>;
     typedef typename O::in8 in8;
     constexpr int KS = HD / 32;
@@ -1413,7 +1417,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
     auto& s_v = L.v;
     auto& s_page = L.page;
 
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = tid_arg;  // threadIdx.x (opaque in attn_list)
     const uint32_t lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t a4 = lane >> 4, c = lane & 15u;
     const uint32_t pr = bid / a.n_kvh, kvh = bid - pr * a.n_kvh;
@@ -1851,7 +1855,7 @@ __device__ __forceinline__ void prefill_wide_wg(const AttnArgs& a, uint32_t bid,
 template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
 __global__ __launch_bounds__(64 * W, W >= 8 ? W / 4 : 1) void attn_prefill_wide(AttnArgs a) {
     __shared__ PrefillLds<HD> lds;
-    prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, blockIdx.x, lds);
+    prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, blockIdx.x, lds, threadIdx.x);
 }
 
 // A call with decode items and prefill blocks (a continuous batch) as one
@@ -1875,9 +1879,53 @@ __global__ __launch_bounds__(64 * W, 2) void attn_mixed(AttnArgs a) {
     const uint32_t w = a.order[rec];
     const uint32_t bid = (w & 0x7FFFFFFFu) * a.n_kvh + kvh;
     if (w >> 31)
-        prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, bid, lds.p);
+        prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(a, bid, lds.p, threadIdx.x);
     else
-        decode_wg<HD, F16, W, ring_for(HD), FULL>(a, bid, lds.d);
+        decode_wg<HD, F16, W, ring_for(HD), FULL>(a, bid, lds.d, threadIdx.x);
+}
+
+// A device-planned call in list mode (thb_dplan_create_ex with
+// THB_DPLAN_PREFILL): workgroups claim entries of the plan's launch order
+// from a counter in its header (entry e covers its record's KV heads as
+// workgroups e * n_kvh .. + n_kvh - 1) and run each with its own kernel's
+// code, as attn_mixed does; the last workgroup to find no entry left resets
+// the counters for the next launch.  Head_dim <= 256 (both bodies 8 waves).
+template <int HD, bool F16, int W, bool FULL, bool CAP, bool QLO = true>
+__global__ __launch_bounds__(64 * W, 2) void attn_list(AttnArgs a) {
+    __shared__ MixedLds<HD, F16, W> lds;
+    __shared__ uint32_t s_w;
+    // Each entry reads the arguments through a pointer the compiler must
+    // take as new on every pass (an empty asm), so their scalar loads stay
+    // inside the loop: hoisted, both bodies' loop-invariant values stayed
+    // live across the loop and spilled.
+    typedef const __attribute__((address_space(4))) AttnArgs* KArgs;
+    const KArgs kargs = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t* hdr = a.list;
+    const uint32_t n_kvh = a.n_kvh;
+    const uint32_t n = hdr[0] * n_kvh;
+    for (;;) {
+        if (threadIdx.x == 0) s_w = __hip_atomic_fetch_add(&hdr[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const uint32_t w = s_w;
+        if (w >= n) break;
+        KArgs kp = kargs;
+        asm volatile("" : "+s"(kp));
+        const AttnArgs& ar = *(const AttnArgs*)kp;
+        uint32_t tid = threadIdx.x;  // opaque too: values derived from it stay inside the loop
+        asm volatile("" : "+v"(tid));
+        const uint32_t rec = w / n_kvh, kvh = w - rec * n_kvh;
+        const uint32_t e = ar.order[rec];
+        if (e >> 31)
+            prefill_wide_wg<HD, F16, W, FULL, CAP, QLO>(ar, (e & 0x7FFFFFFFu) * n_kvh + kvh, lds.p, tid);
+        else
+            decode_wg<HD, F16, W, ring_for(HD), FULL>(ar, e * n_kvh + kvh, lds.d, tid);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(&hdr[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u == gridDim.x) {
+        __hip_atomic_store(&hdr[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&hdr[2], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ---------------------------------------------------- device-side planning
@@ -1953,17 +2001,23 @@ __device__ void dplan_fail(uint32_t* hdr, uint32_t code, uint32_t x, uint32_t y,
     }
 }
 
-__global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
-    __shared__ uint32_t s_ck[kDPlanMaxRows];      // chunk of each row
-    __shared__ uint32_t s_cs[kDPlanMaxRows + 1];  // first row of each chunk, then m
-    __shared__ uint32_t s_lo[kDPlanMaxRows], s_hi[kDPlanMaxRows];
-    __shared__ uint32_t s_red[kDPlanThreads / 64];
-    __shared__ uint32_t s_carry;
+// The row phases of both planners: chunks (maximal runs of rows of one
+// sequence; one chunk with a fixed seq) into s_ck (chunk of each row) and
+// s_cs (first row of each chunk, then m; *n_chunks), then each row's key
+// range (plan_rows) into s_lo / s_hi and ranges_out; a row its pages do
+// not cover reads nothing and is reported in the allocator's status word.
+struct DPlanRows {
+    const uint32_t* meta;
+    uint32_t* ranges_out;
+    uint32_t* state;
+    uint32_t npages_off, m, seq_fixed, causal, window, page_shift, seqs;
+};
+
+__device__ void dplan_rows(const DPlanRows& a, uint32_t* s_ck, uint32_t* s_cs, uint32_t* s_lo, uint32_t* s_hi,
+                           uint32_t* s_red, uint32_t& s_carry) {
     const uint32_t tid = threadIdx.x, m = a.m;
     const bool per_row = a.seq_fixed == THB_SEQ_PER_ROW;
     auto seq_of = [&](uint32_t r) { return per_row ? a.meta[8u * r + 1] : a.seq_fixed; };
-
-    // Chunks: maximal runs of rows of one sequence (one chunk with a fixed seq).
     if (tid == 0) s_carry = 0;
     __syncthreads();
     for (uint32_t t0 = 0; t0 < m; t0 += kDPlanThreads) {
@@ -1982,8 +2036,6 @@ __global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
     }
     if (tid == 0) s_cs[s_carry] = m;
     __syncthreads();
-
-    // Key ranges (plan_rows); a row its pages do not cover reads nothing.
     const uint32_t* npages = a.state + a.npages_off;
     for (uint32_t r = tid; r < m; r += kDPlanThreads) {
         const uint32_t ck = s_ck[r], c0 = s_cs[ck], c1 = s_cs[ck + 1];
@@ -2008,10 +2060,35 @@ __global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
         }
         s_lo[r] = lo;
         s_hi[r] = hi;
-        a.blob[a.ranges_off + 2u * r] = lo;
-        a.blob[a.ranges_off + 2u * r + 1] = hi;
+        a.ranges_out[2u * r] = lo;
+        a.ranges_out[2u * r + 1] = hi;
     }
     __syncthreads();
+}
+
+__global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
+    __shared__ uint32_t s_ck[kDPlanMaxRows];      // chunk of each row
+    __shared__ uint32_t s_cs[kDPlanMaxRows + 1];  // first row of each chunk, then m
+    __shared__ uint32_t s_lo[kDPlanMaxRows], s_hi[kDPlanMaxRows];
+    __shared__ uint32_t s_red[kDPlanThreads / 64];
+    __shared__ uint32_t s_carry;
+    const uint32_t tid = threadIdx.x, m = a.m;
+    const bool per_row = a.seq_fixed == THB_SEQ_PER_ROW;
+    auto seq_of = [&](uint32_t r) { return per_row ? a.meta[8u * r + 1] : a.seq_fixed; };
+    {
+        DPlanRows ra;
+        ra.meta = a.meta;
+        ra.ranges_out = a.blob + a.ranges_off;
+        ra.state = a.state;
+        ra.npages_off = a.npages_off;
+        ra.m = m;
+        ra.seq_fixed = a.seq_fixed;
+        ra.causal = a.causal;
+        ra.window = a.window;
+        ra.page_shift = a.page_shift;
+        ra.seqs = a.seqs;
+        dplan_rows(ra, s_ck, s_cs, s_lo, s_hi, s_red, s_carry);
+    }
 
     // Groups: rows r0 .. r0 + R - 1 of a chunk (R <= 16 / G), or at G > 16 one
     // row and 16 of its query heads per group; group words as build_plan's.
@@ -2077,6 +2154,187 @@ __global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
     for (uint32_t g = s_carry + tid; g < a.gmax; g += kDPlanThreads) {
         const uint32_t w[kGroupWords] = {0u, 1u, 0u, 1u, 0u, 0u, 0u, 0u, 0u, a.align, g * a.pmax};
         write_group(g, w);
+    }
+}
+
+// ---------------------------- device-planned calls with prefill (list mode)
+// A plan made by thb_dplan_create_ex(THB_DPLAN_PREFILL) is a compact work
+// list instead of the slots of a fixed grid:
+//  * decode items: (group, partition), a group's partitions consecutive
+//    (their partial-result slots), for every group not in a prefill block;
+//  * prefill blocks: a chunk of four or more groups (build_plan's rule) is
+//    cut into blocks of WB consecutive groups, and a block whose keys fit
+//    one partition runs on attn_prefill_wide (build_plan's block record, so
+//    each row's arithmetic is thb_attn's); a block spanning several
+//    partitions leaves its groups to the decode items;
+//  * the launch order: every entry, longest first by the host planner's
+//    cost model (a decode workgroup streams at one CU's rate; a prefill
+//    block costs 10 us + 4.5 us per 64-key tile at head_dim 128), by a
+//    counting sort over 1-us buckets.
+// attn_list then claims entries from a counter in the plan header (the last
+// workgroup out resets it), so its grid does not depend on the rows.
+constexpr uint32_t kDPlanListMaxRows = 8192;
+constexpr uint32_t kListHdrWords = 8;  // entries, claim counter, done counter, decode items, blocks
+constexpr uint32_t kListBuckets = 256;
+
+struct DListArgs {
+    DPlanRows rows;
+    uint32_t* blob;
+    uint32_t G, PL, align, WB, hd_t, pmax;
+    uint32_t groups_off, items_off, bitems_off, pairs_off, order_off;
+    float dec_us_per_key;  // decode cost model: microseconds per key of a partition
+};
+
+__global__ __launch_bounds__(kDPlanThreads) void dplan_list_kernel(DListArgs a) {
+    __shared__ uint32_t s_ck[kDPlanListMaxRows];
+    __shared__ uint32_t s_cs[kDPlanListMaxRows + 1];
+    __shared__ uint32_t s_lo[kDPlanListMaxRows], s_hi[kDPlanListMaxRows];
+    __shared__ uint32_t s_red[kDPlanThreads / 64];
+    __shared__ uint32_t s_hist[kListBuckets];
+    __shared__ uint32_t s_carry, s_gc, s_ic, s_bc;
+    const uint32_t tid = threadIdx.x, m = a.rows.m;
+    const bool per_row = a.rows.seq_fixed == THB_SEQ_PER_ROW;
+    auto seq_of = [&](uint32_t r) { return per_row ? a.rows.meta[8u * r + 1] : a.rows.seq_fixed; };
+    dplan_rows(a.rows, s_ck, s_cs, s_lo, s_hi, s_red, s_carry);
+
+    uint32_t* groups = a.blob + a.groups_off;
+    uint32_t* items = a.blob + a.items_off;
+    uint32_t* bitems = a.blob + a.bitems_off;
+    uint32_t* pairs = a.blob + a.pairs_off;
+    const uint32_t rg = a.G <= kCols ? kCols / a.G : 1u;
+    const uint32_t hs = a.G <= kCols ? 1u : (a.G + kCols - 1) / kCols;
+    if (tid == 0) s_gc = s_ic = s_bc = 0;
+    __syncthreads();
+    for (uint32_t t0 = 0; t0 < m; t0 += kDPlanThreads) {
+        const uint32_t r = t0 + tid;
+        bool head = false, blocked = false, bhead = false;
+        uint32_t c0 = 0, c1 = 0, R = 0, lo = 0xFFFFFFFFu, hi = 0, base = 0, np = 1, plen = a.align;
+        uint32_t blo = 0xFFFFFFFFu, bhi = 0, bbase = 0, bnp = 1, bplen = a.align, bng = 0;
+        if (r < m) {
+            const uint32_t ck = s_ck[r];
+            c0 = s_cs[ck];
+            c1 = s_cs[ck + 1];
+            head = (r - c0) % rg == 0;
+        }
+        if (head) {
+            R = min(rg, c1 - r);
+            for (uint32_t j = r; j < r + R; j++)
+                if (s_hi[j] > s_lo[j]) {
+                    lo = min(lo, s_lo[j]);
+                    hi = max(hi, s_hi[j]);
+                }
+            dplan_partition(lo, hi, a.PL, a.align, base, np, plen);
+            np = min(np, a.pmax);  // pmax covers every span the pool's sequences allow
+            // A prefill chunk's block of WB groups that fits one partition.
+            const uint32_t ncg = (c1 - c0 + rg - 1) / rg;
+            if (a.WB && hs == 1 && ncg >= 4) {
+                const uint32_t idx = (r - c0) / rg, br0 = c0 + (idx / a.WB) * a.WB * rg;
+                const uint32_t br1 = min(c1, br0 + a.WB * rg);
+                for (uint32_t j = br0; j < br1; j++)
+                    if (s_hi[j] > s_lo[j]) {
+                        blo = min(blo, s_lo[j]);
+                        bhi = max(bhi, s_hi[j]);
+                    }
+                dplan_partition(blo, bhi, a.PL, a.align, bbase, bnp, bplen);
+                blocked = bnp == 1;
+                bhead = blocked && idx % a.WB == 0;
+                bng = (br1 - br0 + rg - 1) / rg;
+            }
+        }
+        const uint32_t dn = head && !blocked ? np : 0u;  // decode items of each of the row's groups
+        uint32_t tg = 0, ti = 0, tb = 0;
+        const uint32_t ig = dplan_scan(head ? hs : 0u, s_red, &tg);
+        const uint32_t ii = dplan_scan(dn * hs, s_red, &ti);
+        const uint32_t ib = dplan_scan(bhead ? 1u : 0u, s_red, &tb);
+        const uint32_t gc = s_gc, ic = s_ic, bc = s_bc;
+        if (head) {
+            for (uint32_t k = 0; k < hs; k++) {
+                const uint32_t g = gc + ig - hs + k;
+                const uint32_t item0 = ic + ii - dn * hs + k * dn;
+                const uint32_t h0 = k * kCols;
+                const uint32_t H = a.G <= kCols ? a.G : min(kCols, a.G - h0);
+                const uint32_t w[kGroupWords] = {r, a.G <= kCols ? R : 1u, h0, H, seq_of(r), lo, hi, dn, base, plen,
+                                                 item0};
+#pragma unroll
+                for (uint32_t q = 0; q < kGroupWords; q++) groups[g * kGroupWords + q] = w[q];
+                for (uint32_t p = 0; p < dn; p++) {
+                    uint32_t* it = items + static_cast<size_t>(item0 + p) * kItemWords;
+#pragma unroll
+                    for (uint32_t q = 0; q < kGroupWords; q++) it[q] = w[q];
+                    it[kGroupWords] = p;
+                }
+                if (bhead) {
+                    const uint32_t b = bc + ib - 1;
+                    const uint32_t bw[kBItemWords] = {g, bng, seq_of(r), blo, bhi, 1u, bbase, bplen, b, 0u};
+#pragma unroll
+                    for (uint32_t q = 0; q < kBItemWords; q++) bitems[b * kBItemWords + q] = bw[q];
+                    pairs[2 * b] = b;
+                    pairs[2 * b + 1] = kNoItem;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            s_gc = gc + tg;
+            s_ic = ic + ti;
+            s_bc = bc + tb;
+        }
+        __syncthreads();
+    }
+    const uint32_t n_items = s_ic, n_blocks = s_bc, n_entries = n_items + n_blocks;
+    // Launch order: counting sort of every entry by its estimated time,
+    // longest first (bucket kListBuckets - 1 - estimate).
+    auto bucket_of = [&](uint32_t e) -> uint32_t {
+        float us;
+        if (e < n_items) {
+            const uint32_t* it = items + static_cast<size_t>(e) * kItemWords;
+            const uint64_t p0 = uint64_t(it[8]) + uint64_t(it[kGroupWords]) * it[9];
+            const uint64_t keys = it[6] > p0 ? min(uint64_t(it[9]), uint64_t(it[6]) - p0) : 0;
+            us = static_cast<float>(keys) * a.dec_us_per_key;
+        } else {
+            const uint32_t* bk = bitems + static_cast<size_t>(e - n_items) * kBItemWords;
+            const uint32_t tb0 = bk[3] & ~31u, tiles = bk[4] > tb0 ? (bk[4] - tb0 + 63u) / 64u : 0u;
+            us = 10.0f + 4.5f * static_cast<float>(tiles) * static_cast<float>(a.hd_t) / 128.0f;
+        }
+        const uint32_t b = static_cast<uint32_t>(min(us, static_cast<float>(kListBuckets - 1)));
+        return kListBuckets - 1 - b;
+    };
+    for (uint32_t i = tid; i < kListBuckets; i += kDPlanThreads) s_hist[i] = 0;
+    __syncthreads();
+    for (uint32_t e = tid; e < n_entries; e += kDPlanThreads) atomicAdd(&s_hist[bucket_of(e)], 1u);
+    __syncthreads();
+    if (tid < 64) {  // exclusive scan of the histogram, four buckets per lane
+        uint32_t v[4], sum = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            v[k] = s_hist[4 * tid + k];
+            sum += v[k];
+        }
+        uint32_t incl = sum;
+#pragma unroll
+        for (uint32_t d = 1; d < 64; d <<= 1) {
+            const uint32_t t = __shfl_up(incl, d);
+            if (tid >= d) incl += t;
+        }
+        uint32_t run = incl - sum;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            s_hist[4 * tid + k] = run;
+            run += v[k];
+        }
+    }
+    __syncthreads();
+    uint32_t* order = a.blob + a.order_off;
+    for (uint32_t e = tid; e < n_entries; e += kDPlanThreads) {
+        const uint32_t pos = atomicAdd(&s_hist[bucket_of(e)], 1u);
+        order[pos] = e < n_items ? e : (0x80000000u | (e - n_items));
+    }
+    if (tid == 0) {
+        a.blob[0] = n_entries;
+        a.blob[1] = 0u;  // claim counter
+        a.blob[2] = 0u;  // workgroups done
+        a.blob[3] = n_items;
+        a.blob[4] = n_blocks;
     }
 }
 
@@ -2182,6 +2440,33 @@ void launch_mixed(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStre
         f16 ? launch_mixed_hd<64, true>(grid, a, s) : launch_mixed_hd<64, false>(grid, a, s);
     else
         f16 ? launch_mixed_hd<128, true>(grid, a, s) : launch_mixed_hd<128, false>(grid, a, s);
+}
+
+template <int HD, bool F16>
+void launch_list_hd(dim3 grid, const AttnArgs& a, hipStream_t s) {
+    constexpr int W = THB_PREFILL_WAVES;
+    static_assert(decode_waves(HD) == W, "list launch waves");
+    const bool cap = a.cap2 != 0.0f;
+    if (a.full && cap)
+        hipLaunchKernelGGL((attn_list<HD, F16, W, true, true>), grid, dim3(64 * W), 0, s, a);
+    else if (a.full)
+        hipLaunchKernelGGL((attn_list<HD, F16, W, true, false>), grid, dim3(64 * W), 0, s, a);
+    else if (cap)
+        hipLaunchKernelGGL((attn_list<HD, F16, W, false, true>), grid, dim3(64 * W), 0, s, a);
+    else if (query_exact(a, F16))
+        hipLaunchKernelGGL((attn_list<HD, true, W, false, false, false>), grid, dim3(64 * W), 0, s, a);
+    else
+        hipLaunchKernelGGL((attn_list<HD, F16, W, false, false>), grid, dim3(64 * W), 0, s, a);
+}
+
+// List-mode device plans exist at head_dim <= 256 (attn_prefill_wide).
+void launch_list(uint32_t hd_t, bool f16, dim3 grid, const AttnArgs& a, hipStream_t s) {
+    if (hd_t == 64)
+        f16 ? launch_list_hd<64, true>(grid, a, s) : launch_list_hd<64, false>(grid, a, s);
+    else if (hd_t == 128)
+        f16 ? launch_list_hd<128, true>(grid, a, s) : launch_list_hd<128, false>(grid, a, s);
+    else
+        f16 ? launch_list_hd<256, true>(grid, a, s) : launch_list_hd<256, false>(grid, a, s);
 }
 
 template <int HD>
@@ -2649,48 +2934,20 @@ uint64_t partial_bytes(const thb_pool* pool, const AttnPlan& plan, uint64_t* o_b
     return *o_bytes + n_part * 8;
 }
 
-// Launches attention (and, when app is set, the fused append) for a plan
-// whose blob is at `blob` on the device, with the split-K partial results
-// (when the plan splits) at `part`.  With merge_cnt (zeroed counters, one
-// per decode item and KV head, left zero again), each split decode group is
-// combined by the workgroup of its last partition; without, by the merge
-// kernel after the launch.  With rope set, the query is rotated as it is
-// loaded (and the fused append rotates the key); meta is the row meta of
-// the call's first row.
-void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const thb_attn_spec& sp, const AttnPlan& plan,
-                 bool fused_append, const uint32_t* meta, const uint32_t* blob, uint8_t* part, uint32_t* merge_cnt,
-                 hipStream_t s) {
+// The arguments of every attention launch that do not depend on the plan's
+// blob: tensors, geometry, score scale, dtypes and the thb_attn_io
+// extensions.
+void fill_args(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const thb_attn_spec& sp, const uint32_t* meta,
+               AttnArgs& a) {
     const thb_rope* rope = io.rope;
-    const uint32_t hd = pool->geom[layer].head_dim;
-    const uint32_t hd_t = plan.hd_t;
-    float* part_o = nullptr;
-    float* part_ml = nullptr;
-    if (plan.split) {
-        uint64_t o_bytes = 0;
-        partial_bytes(pool, plan, &o_bytes);
-        part_o = reinterpret_cast<float*>(part);
-        part_ml = reinterpret_cast<float*>(part + o_bytes);
-    }
     const LayerGeom& g = pool->geom[layer];
-    AttnArgs a;
+    const uint32_t hd = g.head_dim;
+    a = AttnArgs{};
     a.q = io.q_dev;
     a.y = io.y_dev;
-    a.groups = blob;
-    a.items = blob + static_cast<size_t>(plan.n_groups) * kGroupWords;
-    a.ranges = a.items + static_cast<size_t>(plan.n_items) * kItemWords;
-    a.bitems = a.ranges + 2 * static_cast<size_t>(sp.m);
-    a.bpairs = a.bitems + static_cast<size_t>(plan.n_bitems) * kBItemWords;
-    a.order = a.bpairs + 2 * static_cast<size_t>(plan.n_bpairs);
-    a.merge_groups = blob + plan.merge_off;
     a.table = pool->table_dev;
     a.k = reinterpret_cast<uint16_t*>(pool->mem + g.k_off);
     a.v = reinterpret_cast<uint16_t*>(pool->mem + g.v_off);
-    a.k_src = fused_append ? io.k_src_dev : nullptr;
-    a.v_src = fused_append ? io.v_src_dev : nullptr;
-    a.src_dtype = fused_append ? io.src_dtype : 0u;
-    a.part_o = part_o;
-    a.part_ml = part_ml;
-    a.merge_cnt = plan.split ? merge_cnt : nullptr;
     a.plane = static_cast<uint64_t>(pool->arena.a.pages()) * pool->page_len * hd;
     a.max_pages = pool->arena.a.max_pages();
     a.pages = pool->arena.a.pages();
@@ -2715,6 +2972,43 @@ void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const th
     a.meta = meta;
     a.qrope = rope ? rope_dev(*rope, true) : RopeDev{};
     a.krope = rope ? rope_dev(*rope, false) : RopeDev{};
+}
+
+// Launches attention (and, when app is set, the fused append) for a plan
+// whose blob is at `blob` on the device, with the split-K partial results
+// (when the plan splits) at `part`.  With merge_cnt (zeroed counters, one
+// per decode item and KV head, left zero again), each split decode group is
+// combined by the workgroup of its last partition; without, by the merge
+// kernel after the launch.  With rope set, the query is rotated as it is
+// loaded (and the fused append rotates the key); meta is the row meta of
+// the call's first row.
+void launch_plan(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const thb_attn_spec& sp, const AttnPlan& plan,
+                 bool fused_append, const uint32_t* meta, const uint32_t* blob, uint8_t* part, uint32_t* merge_cnt,
+                 hipStream_t s) {
+    const uint32_t hd_t = plan.hd_t;
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    if (plan.split) {
+        uint64_t o_bytes = 0;
+        partial_bytes(pool, plan, &o_bytes);
+        part_o = reinterpret_cast<float*>(part);
+        part_ml = reinterpret_cast<float*>(part + o_bytes);
+    }
+    AttnArgs a;
+    fill_args(pool, layer, io, sp, meta, a);
+    a.groups = blob;
+    a.items = blob + static_cast<size_t>(plan.n_groups) * kGroupWords;
+    a.ranges = a.items + static_cast<size_t>(plan.n_items) * kItemWords;
+    a.bitems = a.ranges + 2 * static_cast<size_t>(sp.m);
+    a.bpairs = a.bitems + static_cast<size_t>(plan.n_bitems) * kBItemWords;
+    a.order = a.bpairs + 2 * static_cast<size_t>(plan.n_bpairs);
+    a.merge_groups = blob + plan.merge_off;
+    a.k_src = fused_append ? io.k_src_dev : nullptr;
+    a.v_src = fused_append ? io.v_src_dev : nullptr;
+    a.src_dtype = fused_append ? io.src_dtype : 0u;
+    a.part_o = part_o;
+    a.part_ml = part_ml;
+    a.merge_cnt = plan.split ? merge_cnt : nullptr;
     const bool f16 = pool->kv_dtype == THB_KV_F16_RNE;
     const uint64_t n_wg = static_cast<uint64_t>(plan.n_items) * pool->kv_heads;
     // attn_prefill_wide runs pairs of prefill items, attn_prefill single items
@@ -2971,6 +3265,12 @@ struct thb_dplan {
     uint32_t max_m = 0, q_heads = 0, gmax = 0, pmax = 0;
     uint32_t items_off = 0, ranges_off = 0, merge_off = 0;
     uint32_t hd_max = 0;  // widest head_dim template of the pool's layers
+    // List mode (THB_DPLAN_PREFILL): a work list with prefill blocks, launched
+    // as attn_list; the blob is [header | groups | items | ranges | blocks |
+    // pairs | order].
+    bool list = false;
+    uint32_t imax = 0, bmax = 0, wb = 0;
+    uint32_t groups_off = 0, bitems_off = 0, pairs_off = 0, order_off = 0;
     bool built = false;
     thb_attn_spec spec{};
     const thb_rows* rows = nullptr;
@@ -2988,7 +3288,21 @@ void dplan_layout(thb_dplan* p) {
     p->merge_off = p->ranges_off + 2 * p->max_m;
 }
 
-// The launch-side plan of a device plan: every slot of the fixed grid.
+// Blob layout of a list-mode plan.
+void dplan_list_layout(thb_dplan* p) {
+    p->imax = p->gmax * p->pmax;
+    p->bmax = p->gmax / 2 + 1;  // blocks of >= 4 groups, plus each prefill chunk's last partial block
+    p->groups_off = kListHdrWords;
+    p->items_off = p->groups_off + p->gmax * kGroupWords;
+    p->ranges_off = p->items_off + p->imax * kItemWords;
+    p->bitems_off = p->ranges_off + 2 * p->max_m;
+    p->pairs_off = p->bitems_off + p->bmax * kBItemWords;
+    p->order_off = p->pairs_off + 2 * p->bmax;
+    p->merge_off = p->order_off + p->imax + p->bmax;
+}
+
+// The launch-side plan of a device plan: every slot of the fixed grid (or
+// of the list's capacity).
 void dplan_shape(const thb_dplan* p, uint32_t hd, AttnPlan& a) {
     a.n_groups = p->gmax;
     a.n_items = p->gmax * p->pmax;
@@ -3005,10 +3319,17 @@ void dplan_shape(const thb_dplan* p, uint32_t hd, AttnPlan& a) {
 extern "C" {
 
 int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan** out) {
+    return thb_dplan_create_ex(pool, max_m, q_heads, 0u, out);
+}
+
+int thb_dplan_create_ex(thb_pool* pool, uint32_t max_m, uint32_t q_heads, uint32_t flags, thb_dplan** out) {
     if (!pool || !out) return fail(THB_ERR_INVALID, "null pool or out");
     *out = nullptr;
-    if (max_m == 0 || max_m > kDPlanMaxRows)
-        return fail(THB_ERR_INVALID, "device-planned calls take 1 to " + std::to_string(kDPlanMaxRows) + " rows, not " +
+    if (flags & ~THB_DPLAN_PREFILL) return fail(THB_ERR_INVALID, "unknown dplan flags " + std::to_string(flags));
+    const bool list = (flags & THB_DPLAN_PREFILL) != 0;
+    const uint32_t max_rows = list ? kDPlanListMaxRows : kDPlanMaxRows;
+    if (max_m == 0 || max_m > max_rows)
+        return fail(THB_ERR_INVALID, "device-planned calls take 1 to " + std::to_string(max_rows) + " rows, not " +
                                          std::to_string(max_m));
     if (q_heads == 0 || q_heads % pool->kv_heads != 0)
         return fail(THB_ERR_CONFIG, "q_heads " + std::to_string(q_heads) + " must be a positive multiple of kv_heads " +
@@ -3033,7 +3354,15 @@ int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan
                                             std::to_string(pool->part_len) + " tokens");
         p->pmax = n;
         for (const auto& g : pool->geom) p->hd_max = std::max(p->hd_max, template_hd(g.head_dim));
-        dplan_layout(p.get());
+        if (list) {
+            if (p->hd_max > 256)
+                return fail(THB_ERR_CONFIG, "device plans with prefill blocks take head_dim <= 256");
+            p->list = true;
+            p->wb = block_groups(true, p->hd_max);
+            dplan_list_layout(p.get());
+        } else {
+            dplan_layout(p.get());
+        }
         const size_t words = static_cast<size_t>(p->merge_off) + static_cast<size_t>(p->gmax) * kMergeWords;
         p->blob.reserve(words * 4, true, nullptr);
         AttnPlan shape;
@@ -3071,6 +3400,39 @@ int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* 
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);  // queued page-API calls first: the plan reads the page counts
+        if (plan->list) {
+            DListArgs la;
+            la.rows.meta = rows->dev + 8 * static_cast<size_t>(spec->row_off);
+            la.rows.ranges_out = static_cast<uint32_t*>(plan->blob.get()) + plan->ranges_off;
+            la.rows.state = pool->state_dev;
+            la.rows.npages_off = pool->state.npages_off;
+            la.rows.m = spec->m;
+            la.rows.seq_fixed = spec->seq;
+            la.rows.causal = spec->causal;
+            la.rows.window = spec->window;
+            la.rows.page_shift = pool->page_shift;
+            la.rows.seqs = pool->arena.a.seqs();
+            la.blob = static_cast<uint32_t*>(plan->blob.get());
+            la.G = spec->q_heads / pool->kv_heads;
+            la.PL = pool->part_len;
+            la.align = std::max<uint32_t>(pool->page_len, 16);
+            la.WB = plan->wb;
+            la.pmax = plan->pmax;
+            la.hd_t = plan->hd_max;
+            la.groups_off = plan->groups_off;
+            la.items_off = plan->items_off;
+            la.bitems_off = plan->bitems_off;
+            la.pairs_off = plan->pairs_off;
+            la.order_off = plan->order_off;
+            // a decode workgroup streams K and V at ~37 GB/s (one CU's share)
+            la.dec_us_per_key = static_cast<float>(4.0 * plan->hd_max / 3.7e4);
+            hipLaunchKernelGGL(dplan_list_kernel, dim3(1), dim3(kDPlanThreads), 0, s, la);
+            THB_HIP(hipGetLastError());
+            plan->spec = *spec;
+            plan->rows = rows;
+            plan->built = true;
+            return THB_OK;
+        }
         DPlanArgs a;
         a.meta = rows->dev + 8 * static_cast<size_t>(spec->row_off);
         a.blob = static_cast<uint32_t*>(plan->blob.get());
@@ -3113,6 +3475,34 @@ int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q, void* y, const
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
         const uint32_t hd = pool->geom[layer].head_dim;
+        if (plan->list) {
+            // The work list over one workgroup per CU: attn_list claims its
+            // entries (decode items with in-launch merges, prefill blocks).
+            const uint32_t* blob = static_cast<const uint32_t*>(plan->blob.get());
+            const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
+            AttnArgs a;
+            fill_args(pool, layer, io, plan->spec, plan->rows->dev + 8 * static_cast<size_t>(plan->spec.row_off), a);
+            a.groups = blob + plan->groups_off;
+            a.items = blob + plan->items_off;
+            a.ranges = blob + plan->ranges_off;
+            a.bitems = blob + plan->bitems_off;
+            a.bpairs = blob + plan->pairs_off;
+            a.order = blob + plan->order_off;
+            a.merge_groups = blob + plan->merge_off;
+            a.list = const_cast<uint32_t*>(blob);
+            AttnPlan shape;
+            dplan_shape(plan, plan->hd_max, shape);
+            if (shape.split) {
+                uint64_t o_bytes = 0;
+                partial_bytes(pool, shape, &o_bytes);
+                a.part_o = reinterpret_cast<float*>(plan->part.get());
+                a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(plan->part.get()) + o_bytes);
+                a.merge_cnt = static_cast<uint32_t*>(plan->cnt.get());
+            }
+            launch_list(template_hd(hd), pool->kv_dtype == THB_KV_F16_RNE, dim3(pool->cus), a, s);
+            THB_HIP(hipGetLastError());
+            return THB_OK;
+        }
         AttnPlan shape;
         dplan_shape(plan, hd, shape);
         const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);

@@ -167,9 +167,12 @@ class DevicePlan:
     one layer over the plan.  Each (group, partition) computes what ``attn``
     computes, bit for bit."""
 
-    def __init__(self, kv: KvPool, max_m: int, q_heads: int):
+    def __init__(self, kv: KvPool, max_m: int, q_heads: int, prefill: bool = False):
+        """prefill=True: a work-list plan (thb_dplan_create_ex with
+        THB_DPLAN_PREFILL) that also runs prefill chunks on the prefill
+        kernel."""
         h = ctypes.c_void_p()
-        check(lib().thb_dplan_create(kv.handle, max_m, q_heads, ctypes.byref(h)))
+        check(lib().thb_dplan_create_ex(kv.handle, max_m, q_heads, 1 if prefill else 0, ctypes.byref(h)))
         self._h = h.value
         self.kv, self.max_m, self.q_heads = kv, max_m, q_heads
         self.spec = None

@@ -452,6 +452,20 @@ int thb_attn_noalloc(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_
  * buffers: calls that use it must not overlap. */
 typedef struct thb_dplan thb_dplan;
 int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan** out);
+/* No reference counterpart: thb_dplan_create with flags.  THB_DPLAN_PREFILL
+ * makes the plan a work list (calls of up to 8192 rows, head_dim <= 256):
+ * thb_dplan_build also cuts chunks of four or more groups into blocks of
+ * consecutive groups (thb_attn's prefill blocks) and runs each block whose
+ * keys fit one partition on the prefill kernel, the other groups as decode
+ * items, and orders every entry longest first; thb_attn_dplan launches one
+ * workgroup per compute unit that claims entries from a counter in the plan
+ * (reset by the launch's last workgroup).  Decode rows, and chunks whose
+ * blocks each fit one partition, give thb_attn's outputs bit for bit; a
+ * block spanning several partitions runs as decode items where thb_attn
+ * runs the prefill kernel and a merge, so its rows differ from thb_attn's
+ * in the order of the sums only (within 1e-5 on the tested cases). */
+#define THB_DPLAN_PREFILL 1u
+int thb_dplan_create_ex(thb_pool* pool, uint32_t max_m, uint32_t q_heads, uint32_t flags, thb_dplan** out);
 void thb_dplan_destroy(thb_dplan* plan);
 int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* rows, void* stream);
 int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_dplan* plan,

@@ -12,7 +12,8 @@ import zlib
 import numpy as np
 import pytest
 
-from gpu_util import fill, make_pool, say, scattered_alloc
+import oracle
+from gpu_util import fill, make_pool, oracle_layer, say, scattered_alloc
 
 pytestmark = pytest.mark.gpu
 
@@ -204,3 +205,130 @@ def test_device_plan_errors(torch_cuda):
     assert "rows" in str(e.value)
     plan.close()
     np.testing.assert_equal(True, True)
+
+
+# name, nq, nkv, hd, kv, decode lens, prefill chunks (seq len, chunk rows), part_len, window, softcap, exact.
+# exact: every prefill block's keys fit one partition, so the list plan runs
+# each block on the prefill kernel as thb_attn does (bit-identical); a block
+# spanning partitions runs as decode groups (thb_attn: the prefill kernel plus
+# the merge), a different summation order: within the oracle's bound.
+LIST_CASES = [
+    ("c3-like", 32, 8, 128, "f16", [3000, 40, 1500, 777, 2049, 9000], [(512, 512), (700, 300)], 4096, 0, 0.0, True),
+    ("gemma-window-softcap", 16, 8, 256, "f16", [1300, 5000], [(600, 200), (4700, 130)], 4096, 4096, 50.0, False),
+    ("long-prefix-split-blocks", 32, 8, 128, "f16", [900], [(6000, 256)], 2048, 0, 0.0, False),
+    ("qwen2-bf16", 14, 2, 64, "bf16", [128, 512, 300], [(400, 100)], 512, 0, 0.0, True),
+    ("gemma-one-partition", 16, 8, 256, "f16", [1300, 2000], [(600, 200), (512, 512)], 4096, 4096, 50.0, True),
+]
+
+
+@pytest.mark.parametrize("case", LIST_CASES, ids=[c[0] for c in LIST_CASES])
+def test_list_plan_with_prefill_matches_attn(torch_cuda, case):
+    """A work-list device plan (prefill=True): decode rows and prefill
+    chunks in one call, the chunks' blocks on the prefill kernel (or, when a
+    block spans several partitions, as decode groups).  Where every block
+    fits one partition the outputs equal thb_attn's bit for bit; otherwise
+    they are within 1e-4 of the oracle and 1e-5 of thb_attn."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    name, nq, nkv, hd, kv, dlens, chunks, part_len, window, softcap, exact = case
+    say("list plan", name)
+    lens = dlens + [n for n, _ in chunks]
+    pool = make_pool(lens, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype=kv, extra_pages=5, part_len=part_len)
+    scattered_alloc(pool, lens, random.Random(zlib.crc32(name.encode())), 16)
+    fill(torch, pool, RowMeta(256), lens, seed=11)
+    positions = [n - 1 for n in dlens]
+    seqs = list(range(len(dlens)))
+    for i, (n, c) in enumerate(chunks):
+        positions += list(range(n - c, n))
+        seqs += [len(dlens) + i] * c
+    m = len(seqs)
+    rows = RowMeta(m)
+    rows.write(positions, seqs, m)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(12)
+    q = torch.randn(m, nq, hd, device="cuda", generator=g).half()
+    spec = ops.AttnSpec(q_heads=nq, window=window, scale=1.0 / math.sqrt(hd), m=m, causal=True, seq=None, args=rows,
+                        softcap=softcap)
+    want = torch.empty(m, nq, hd, device="cuda")
+    got = torch.full_like(want, 7.0)
+    ops.attn(q, pool, 0, want, spec)
+    plan = ops.DevicePlan(pool, max_m=m + 5, q_heads=nq, prefill=True)
+    plan.build(spec, q, got)
+    plan.attn(0, q, got)
+    plan.attn(0, q, got)  # a second launch: the claim counter was reset by the first
+    torch.cuda.synchronize()
+    assert torch.isfinite(want).all(), name
+    if exact:
+        assert torch.equal(got, want), (name, float((got - want).abs().max()))
+    else:
+        assert float((got - want).abs().max()) <= 1e-5, name
+        ref = oracle_layer(torch, pool)
+        oracle_y = ref.attn(q.float().cpu().numpy(), oracle.row_meta(positions, seqs), m, nq, 1.0 / math.sqrt(hd),
+                            window=window, softcap=softcap)
+        err = float(np.max(np.abs(got.cpu().numpy() - oracle_y)))
+        say("list plan", name, "max abs err vs oracle", err)
+        assert err <= 1e-4, (name, err)
+    pool.status()
+    plan.close()
+
+
+def test_list_plan_graph_replay_chunked_prefill(torch_cuda):
+    """A captured step of the list plan (build + attention over two layers)
+    replayed while a 256-row prefill chunk advances through a 1024-token
+    prompt beside four decode rows: every replay equals thb_attn at that
+    step's positions, bit for bit."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    nq, nkv, hd, L = 32, 8, 128, 2
+    dlens = [2100, 700, 4500, 1300]
+    budget = [n + 8 for n in dlens] + [1024]
+    pool = make_pool(budget, kv_heads=nkv, head_dim=hd, page_len=16, kv_dtype="f16", layers=L, part_len=1024)
+    scattered_alloc(pool, budget, random.Random(33), 16)
+    for layer in range(L):
+        fill(torch, pool, RowMeta(256), budget, layer=layer, seed=33 + layer)
+    c = 256
+    m = len(dlens) + c
+    rows = RowMeta(m)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(34)
+    q = [torch.randn(m, nq, hd, device="cuda", generator=g).half() for _ in range(L)]
+    y = [torch.empty(m, nq, hd, device="cuda") for _ in range(L)]
+    spec = ops.AttnSpec(q_heads=nq, window=0, scale=1.0 / math.sqrt(hd), m=m, causal=True, seq=None, args=rows)
+    plan = ops.DevicePlan(pool, max_m=m, q_heads=nq, prefill=True)
+    seqs = list(range(len(dlens))) + [len(dlens)] * c
+
+    def positions(step):
+        return [n - 1 + step for n in dlens] + list(range(step * c, step * c + c))
+
+    rows.write(positions(0), seqs, m)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            plan.build(spec, q[0], y[0])
+            for layer in range(L):
+                plan.attn(layer, q[layer], y[layer])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    want = torch.empty(m, nq, hd, device="cuda")
+    for step in range(4):
+        rows.write(positions(step), seqs, m)
+        for t in y:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for layer in range(L):
+            ops.attn(q[layer], pool, layer, want, spec)
+            torch.cuda.synchronize()
+            say("list plan replay step", step, "layer", layer)
+            assert torch.isfinite(want).all()
+            assert torch.equal(y[layer], want), (step, layer, float((y[layer] - want).abs().max()))
+    pool.status()
+    del graph
+    plan.close()
