@@ -2181,129 +2181,355 @@ struct DListArgs {
     DPlanRows rows;
     uint32_t* blob;
     uint32_t G, PL, align, WB, hd_t, pmax;
+    uint32_t rg_magic, wb_magic;  // div16 multipliers of the rows per group and WB
     uint32_t groups_off, items_off, bitems_off, pairs_off, order_off;
     float dec_us_per_key;  // decode cost model: microseconds per key of a partition
 };
 
-__global__ __launch_bounds__(kDPlanThreads) void dplan_list_kernel(DListArgs a) {
-    __shared__ uint32_t s_ck[kDPlanListMaxRows];
-    __shared__ uint32_t s_cs[kDPlanListMaxRows + 1];
-    __shared__ uint32_t s_lo[kDPlanListMaxRows], s_hi[kDPlanListMaxRows];
-    __shared__ uint32_t s_red[kDPlanThreads / 64];
-    __shared__ uint32_t s_hist[kListBuckets];
-    __shared__ uint32_t s_carry, s_gc, s_ic, s_bc;
-    const uint32_t tid = threadIdx.x, m = a.rows.m;
-    const bool per_row = a.rows.seq_fixed == THB_SEQ_PER_ROW;
-    auto seq_of = [&](uint32_t r) { return per_row ? a.rows.meta[8u * r + 1] : a.rows.seq_fixed; };
-    dplan_rows(a.rows, s_ck, s_cs, s_lo, s_hi, s_red, s_carry);
+// Exclusive sums over the workgroup of C per-thread values (v in, v out),
+// totals in tot.  Every thread calls it; red holds (blockDim.x / 64) * C
+// words.
+template <int C>
+__device__ void dplan_scan_c(uint32_t (&v)[C], uint32_t* red, uint32_t (&tot)[C]) {
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    uint32_t x[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) x[c] = v[c];
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            const uint32_t t = __shfl_up(x[c], d);
+            if (lane >= d) x[c] += t;
+        }
+    }
+    if (lane == 63) {
+#pragma unroll
+        for (int c = 0; c < C; c++) red[w * C + c] = x[c];
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            uint32_t y = lane < nw ? red[lane * C + c] : 0u;
+#pragma unroll
+            for (uint32_t d = 1; d < 16; d <<= 1) {
+                const uint32_t t = __shfl_up(y, d);
+                if (lane >= d) y += t;
+            }
+            if (lane < nw) red[lane * C + c] = y;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        v[c] = x[c] - v[c] + (w > 0 ? red[(w - 1) * C + c] : 0u);
+        tot[c] = red[(nw - 1) * C + c];
+    }
+    __syncthreads();
+}
 
+// The list planner.  Each thread owns kListRowsPerThread consecutive rows
+// and every phase is one pass over all rows (a sum over the workgroup where
+// a phase numbers what it makes), so the plan costs a few memory round
+// trips and barriers whatever the row count:
+//  1. positions and sequences of the rows (one batch of loads);
+//  2. chunks: chunk of each row, first row of each chunk;
+//  3. each row's key range (plan_rows), the page-coverage check;
+//  4. each group's key range (at its first row) and partition;
+//  5. prefill blocks: a block's first group takes the block's range from
+//     its groups' ranges and marks them blocked when it fits one partition;
+//  6. groups, decode items and blocks numbered in row order, written, and
+//     counted into the launch-order histogram;
+//  7. the launch order (counting sort, longest first).
+constexpr uint32_t kListRowsPerThread = kDPlanListMaxRows / kDPlanThreads;
+constexpr uint32_t kListMaxWB = 16;  // groups per prefill block the list planner takes
+// s_np word of a row: kRowHead at a group's first row, with the group's
+// partition count; for a group of a prefill block kRowBlocked instead of
+// the count, and at the block's first group also kRowBlockHead and the
+// block's group count.
+constexpr uint16_t kRowBlocked = 0x8000u;
+constexpr uint16_t kRowBlockHead = 0x4000u;
+constexpr uint16_t kRowHead = 0x2000u;
+constexpr uint16_t kRowCount = 0x1FFFu;
+static_assert(kMaxParts <= kRowCount && kListMaxWB <= kRowCount, "row word fields");
+
+// x / d for x < 2^16 and 1 <= d < 2^16, with mg = floor(2^32 / d) + 1 (0 for
+// d = 1): mg = (2^32 + e) / d with 0 < e <= d, so x mg / 2^32 exceeds x / d
+// by less than x / 2^32 < 1 / d, which never crosses the next integer.
+__device__ inline uint32_t div16(uint32_t x, uint32_t d, uint32_t mg) { return d == 1 ? x : __umulhi(x, mg); }
+inline uint32_t div16_magic(uint32_t d) { return d <= 1 ? 0u : static_cast<uint32_t>((1ull << 32) / d + 1); }
+
+// part_split of the list planner: 32-bit arithmetic below 2^31 keys, the
+// 64-bit form (one out-of-line copy) from there.
+__device__ __noinline__ uint64_t dplan_split_wide(uint32_t span, uint32_t PL, uint32_t align) {
+    uint32_t n_parts, plen;
+    part_split(span, PL, align, n_parts, plen);
+    return (uint64_t(n_parts) << 32) | plen;
+}
+__device__ inline void dplan_split(uint32_t span, uint32_t PL, uint32_t align, uint32_t& n_parts, uint32_t& plen) {
+    if (span < 0x80000000u) {
+        part_split32(span, PL, align, n_parts, plen);
+    } else {
+        const uint64_t np = dplan_split_wide(span, PL, align);
+        n_parts = static_cast<uint32_t>(np >> 32);
+        plen = static_cast<uint32_t>(np);
+    }
+}
+
+__global__ __launch_bounds__(kDPlanThreads) void dplan_list_kernel(DListArgs a) {
+    constexpr uint32_t K = kListRowsPerThread, T = kDPlanThreads;
+    __shared__ uint32_t s_lo[kDPlanListMaxRows], s_hi[kDPlanListMaxRows];
+    __shared__ uint32_t s_seq[kDPlanListMaxRows];
+    __shared__ uint16_t s_ck[kDPlanListMaxRows];      // chunk of each row
+    __shared__ uint16_t s_cs[kDPlanListMaxRows + 1];  // first row of each chunk, then m
+    __shared__ uint16_t s_np[kDPlanListMaxRows];      // row word
+    __shared__ uint32_t s_red[(kDPlanThreads / 64) * 3];
+    __shared__ uint32_t s_hist[kListBuckets];
+    const uint32_t tid = threadIdx.x, m = a.rows.m, r0 = tid * K;  // rows r0 .. r0 + K - 1: numbering phases
+    const bool per_row = a.rows.seq_fixed == THB_SEQ_PER_ROW;
+    const uint32_t rg = a.G <= kCols ? kCols / a.G : 1u;
+    const uint32_t hs = a.G <= kCols ? 1u : (a.G + kCols - 1) / kCols;
+    const uint32_t amask = ~(a.align - 1);
+
+    // 1. positions and sequences (rows tid + k T: coalesced)
+#pragma unroll
+    for (uint32_t k = 0; k < K; k++) {
+        const uint32_t r = tid + k * T;
+        if (r < m) {
+            uint32_t pos, sq = a.rows.seq_fixed;
+            if (per_row) {
+                const uint2 ps = *reinterpret_cast<const uint2*>(a.rows.meta + 8u * r);
+                pos = ps.x;
+                sq = ps.y;
+            } else {
+                pos = a.rows.meta[8u * r];
+            }
+            s_lo[r] = pos;
+            s_seq[r] = sq;
+            s_np[r] = 0;
+        }
+    }
+    for (uint32_t i = tid; i < kListBuckets; i += T) s_hist[i] = 0;
+    __syncthreads();
+
+    // 2. chunks: maximal runs of rows of one sequence
+    auto is_start = [&](uint32_t r) { return r < m && (r == 0 || (per_row && s_seq[r] != s_seq[r - 1])); };
+    uint32_t nst[1] = {0}, nck[1];
+#pragma unroll
+    for (uint32_t k = 0; k < K; k++) nst[0] += is_start(r0 + k) ? 1u : 0u;
+    dplan_scan_c<1>(nst, s_red, nck);
+    {
+        uint32_t ck = nst[0];
+#pragma unroll
+        for (uint32_t k = 0; k < K; k++) {
+            const uint32_t r = r0 + k;
+            if (r < m) {
+                if (is_start(r)) s_cs[ck++] = static_cast<uint16_t>(r);
+                s_ck[r] = static_cast<uint16_t>(ck - 1);
+            }
+        }
+    }
+    if (tid == 0) s_cs[nck[0]] = static_cast<uint16_t>(m);
+    __syncthreads();
+
+    // 3. key range of each row (plan_rows), pages covering it (rows tid + k T)
+    {
+        uint32_t lo[K], hi[K], np_seq[K];
+        const uint32_t* npages = a.rows.state + a.rows.npages_off;
+#pragma unroll
+        for (uint32_t k = 0; k < K; k++) {
+            const uint32_t r = tid + k * T;
+            lo[k] = hi[k] = np_seq[k] = 0;
+            if (r >= m) continue;
+            const uint32_t ck = s_ck[r], c0 = s_cs[ck], c1 = s_cs[ck + 1];
+            const uint32_t n = c1 - c0, i = r - c0, pos = s_lo[r];
+            const uint32_t blk_last = min((i / 8u) * 8u + 8u, n);
+            const uint64_t kv_len = a.rows.causal ? uint64_t(s_lo[c0 + blk_last - 1]) + 1 : uint64_t(s_lo[c1 - 1]) + 1;
+            uint64_t ws = 0;
+            if (a.rows.causal && a.rows.window != 0 && uint64_t(pos) + 1 > a.rows.window)
+                ws = uint64_t(pos) + 1 - a.rows.window;
+            uint64_t h = kv_len;
+            if (a.rows.causal && uint64_t(pos) + 1 < h) h = uint64_t(pos) + 1;
+            lo[k] = static_cast<uint32_t>(ws);
+            hi[k] = static_cast<uint32_t>(min(h, uint64_t(0xFFFFFFFFu)));
+            const uint32_t sq = s_seq[r];
+            if (hi[k] > lo[k] && sq < a.rows.seqs) np_seq[k] = npages[sq];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < K; k++) {
+            const uint32_t r = tid + k * T;
+            if (r >= m || hi[k] <= lo[k]) continue;
+            const uint32_t sq = s_seq[r];
+            if (sq >= a.rows.seqs) {
+                dplan_fail(a.rows.state, kPageStBadSeq, sq, a.rows.seqs, 0u);
+                lo[k] = hi[k] = 0;
+            } else if ((uint64_t(np_seq[k]) << a.rows.page_shift) < hi[k]) {
+                dplan_fail(a.rows.state, kPageStCover, sq, np_seq[k] << a.rows.page_shift, hi[k]);
+                lo[k] = hi[k] = 0;
+            }
+        }
+        __syncthreads();  // every position read
+#pragma unroll
+        for (uint32_t k = 0; k < K; k++) {
+            const uint32_t r = tid + k * T;
+            if (r < m) {
+                s_lo[r] = lo[k];
+                s_hi[r] = hi[k];
+                a.rows.ranges_out[2u * r] = lo[k];  // the ranges may start at an odd word
+                a.rows.ranges_out[2u * r + 1] = hi[k];
+            }
+        }
+    }
+    __syncthreads();
+
+    // 4. groups (rows r .. r + R - 1 of a chunk, R <= rg): key range at the
+    // group's first row (0xFFFFFFFF / 0 when empty) and partition count.
+    // Phases 4 to 7 take each thread's consecutive rows, so that the lanes
+    // of a wave meet group and block starts together.
+#pragma unroll 1
+    for (uint32_t r = r0; r < min(m, r0 + K); r++) {
+        const uint32_t ck = s_ck[r], c0 = s_cs[ck], c1 = s_cs[ck + 1];
+        const uint32_t i = r - c0;
+        if (i != div16(i, rg, a.rg_magic) * rg) continue;
+        const uint32_t R = min(rg, c1 - r);
+        uint32_t glo = 0xFFFFFFFFu, ghi = 0;
+#pragma unroll 4
+        for (uint32_t j = r; j < r + R; j++) {
+            const uint32_t l = s_lo[j], h = s_hi[j];
+            if (h > l) {
+                glo = min(glo, l);
+                ghi = max(ghi, h);
+            }
+        }
+        uint32_t np = 1, plen;
+        if (ghi > glo && glo != 0xFFFFFFFFu) dplan_split(ghi - (glo & amask), a.PL, a.align, np, plen);
+        s_lo[r] = glo;  // the group's rows r + 1 .. are no other group's
+        s_hi[r] = ghi;
+        s_np[r] = kRowHead | static_cast<uint16_t>(min(np, a.pmax));  // pmax covers every span of the pool
+    }
+    __syncthreads();
+
+    // 5. prefill blocks: WB consecutive groups of a chunk of >= 4 groups
+    // (build_plan's rule), run on the prefill kernel when their keys fit
+    // one partition.  The block's range over its groups' ranges.
+    auto block_range = [&](uint32_t r, uint32_t bng, uint32_t& blo, uint32_t& bhi) {
+        blo = 0xFFFFFFFFu;
+        bhi = 0;
+#pragma unroll 4
+        for (uint32_t j = 0; j < bng; j++) {
+            blo = min(blo, s_lo[r + j * rg]);
+            bhi = max(bhi, s_hi[r + j * rg]);
+        }
+    };
+    const bool blocks = a.WB != 0 && hs == 1;
+    if (blocks) {
+#pragma unroll 1
+        for (uint32_t r = r0; r < min(m, r0 + K); r++) {
+            if (!(s_np[r] & kRowHead)) continue;
+            const uint32_t ck = s_ck[r], c0 = s_cs[ck], c1 = s_cs[ck + 1];
+            const uint32_t idx = div16(r - c0, rg, a.rg_magic);
+            if (div16(c1 - c0 + rg - 1, rg, a.rg_magic) < 4 || idx != div16(idx, a.WB, a.wb_magic) * a.WB) continue;
+            const uint32_t bng = div16(min(c1, r + a.WB * rg) - r + rg - 1, rg, a.rg_magic);
+            uint32_t blo, bhi, bnp = 1, bplen;
+            block_range(r, bng, blo, bhi);
+            if (bhi > blo && blo != 0xFFFFFFFFu) dplan_split(bhi - (blo & amask), a.PL, a.align, bnp, bplen);
+            if (bnp == 1) {
+                for (uint32_t j = 1; j < bng; j++) s_np[r + j * rg] = kRowHead | kRowBlocked;
+                s_np[r] = kRowHead | kRowBlocked | kRowBlockHead | static_cast<uint16_t>(bng);
+            }
+        }
+    }
+    __syncthreads();
+
+    // 6. number the groups, items and blocks in row order; write them
+    uint32_t cnt[3] = {0, 0, 0}, tot[3];  // groups, decode items, blocks
+#pragma unroll
+    for (uint32_t k = 0; k < K; k++) {
+        const uint32_t w = r0 + k < m ? s_np[r0 + k] : 0u;
+        if (!(w & kRowHead)) continue;
+        cnt[0] += hs;
+        cnt[1] += (w & kRowBlocked) ? 0u : (w & kRowCount) * hs;
+        cnt[2] += (w & kRowBlockHead) ? 1u : 0u;
+    }
+    dplan_scan_c<3>(cnt, s_red, tot);
+    const uint32_t n_items = tot[1], n_blocks = tot[2], n_entries = n_items + n_blocks;
     uint32_t* groups = a.blob + a.groups_off;
     uint32_t* items = a.blob + a.items_off;
     uint32_t* bitems = a.blob + a.bitems_off;
     uint32_t* pairs = a.blob + a.pairs_off;
-    const uint32_t rg = a.G <= kCols ? kCols / a.G : 1u;
-    const uint32_t hs = a.G <= kCols ? 1u : (a.G + kCols - 1) / kCols;
-    if (tid == 0) s_gc = s_ic = s_bc = 0;
-    __syncthreads();
-    for (uint32_t t0 = 0; t0 < m; t0 += kDPlanThreads) {
-        const uint32_t r = t0 + tid;
-        bool head = false, blocked = false, bhead = false;
-        uint32_t c0 = 0, c1 = 0, R = 0, lo = 0xFFFFFFFFu, hi = 0, base = 0, np = 1, plen = a.align;
-        uint32_t blo = 0xFFFFFFFFu, bhi = 0, bbase = 0, bnp = 1, bplen = a.align, bng = 0;
-        if (r < m) {
-            const uint32_t ck = s_ck[r];
-            c0 = s_cs[ck];
-            c1 = s_cs[ck + 1];
-            head = (r - c0) % rg == 0;
+    // launch-order bucket of an entry: kListBuckets - 1 - estimated us
+    auto bucket = [&](float us) -> uint32_t {
+        return kListBuckets - 1 - static_cast<uint32_t>(min(us, static_cast<float>(kListBuckets - 1)));
+    };
+    auto item_bucket = [&](uint32_t base, uint32_t plen, uint32_t ghi, uint32_t p) -> uint32_t {
+        const uint64_t p0 = uint64_t(base) + uint64_t(p) * plen;
+        const uint64_t keys = ghi > p0 ? min(uint64_t(plen), uint64_t(ghi) - p0) : 0;
+        return bucket(static_cast<float>(keys) * a.dec_us_per_key);
+    };
+    auto block_bucket = [&](uint32_t blo, uint32_t bhi) -> uint32_t {
+        const uint32_t tb0 = blo & ~31u, tiles = bhi > tb0 ? (bhi - tb0 + 63u) / 64u : 0u;
+        return bucket(10.0f + 4.5f * static_cast<float>(tiles) * static_cast<float>(a.hd_t) / 128.0f);
+    };
+    // a group (or block): lo, hi (0, 0 when empty), base, plen
+    auto span_of = [&](uint32_t& lo, uint32_t& hi, uint32_t& base, uint32_t& plen) {
+        base = 0;
+        plen = a.align;
+        if (hi <= lo || lo == 0xFFFFFFFFu) {
+            lo = hi = 0;
+        } else {
+            uint32_t np;
+            base = lo & amask;
+            dplan_split(hi - base, a.PL, a.align, np, plen);
         }
-        if (head) {
-            R = min(rg, c1 - r);
-            for (uint32_t j = r; j < r + R; j++)
-                if (s_hi[j] > s_lo[j]) {
-                    lo = min(lo, s_lo[j]);
-                    hi = max(hi, s_hi[j]);
-                }
-            dplan_partition(lo, hi, a.PL, a.align, base, np, plen);
-            np = min(np, a.pmax);  // pmax covers every span the pool's sequences allow
-            // A prefill chunk's block of WB groups that fits one partition.
-            const uint32_t ncg = (c1 - c0 + rg - 1) / rg;
-            if (a.WB && hs == 1 && ncg >= 4) {
-                const uint32_t idx = (r - c0) / rg, br0 = c0 + (idx / a.WB) * a.WB * rg;
-                const uint32_t br1 = min(c1, br0 + a.WB * rg);
-                for (uint32_t j = br0; j < br1; j++)
-                    if (s_hi[j] > s_lo[j]) {
-                        blo = min(blo, s_lo[j]);
-                        bhi = max(bhi, s_hi[j]);
-                    }
-                dplan_partition(blo, bhi, a.PL, a.align, bbase, bnp, bplen);
-                blocked = bnp == 1;
-                bhead = blocked && idx % a.WB == 0;
-                bng = (br1 - br0 + rg - 1) / rg;
-            }
-        }
-        const uint32_t dn = head && !blocked ? np : 0u;  // decode items of each of the row's groups
-        uint32_t tg = 0, ti = 0, tb = 0;
-        const uint32_t ig = dplan_scan(head ? hs : 0u, s_red, &tg);
-        const uint32_t ii = dplan_scan(dn * hs, s_red, &ti);
-        const uint32_t ib = dplan_scan(bhead ? 1u : 0u, s_red, &tb);
-        const uint32_t gc = s_gc, ic = s_ic, bc = s_bc;
-        if (head) {
-            for (uint32_t k = 0; k < hs; k++) {
-                const uint32_t g = gc + ig - hs + k;
-                const uint32_t item0 = ic + ii - dn * hs + k * dn;
-                const uint32_t h0 = k * kCols;
+    };
+    {
+        uint32_t gi = cnt[0], ii = cnt[1], bi = cnt[2];
+#pragma unroll 1
+        for (uint32_t k = 0; k < K; k++) {
+            const uint32_t r = r0 + k;
+            const uint32_t rw = r < m ? s_np[r] : 0u;
+            if (!(rw & kRowHead)) continue;
+            const uint32_t dn = (rw & kRowBlocked) ? 0u : (rw & kRowCount);
+            const uint32_t R = min(rg, static_cast<uint32_t>(s_cs[s_ck[r] + 1]) - r);
+            const uint32_t sq = s_seq[r];
+            uint32_t glo = s_lo[r], ghi = s_hi[r], base, plen;
+            span_of(glo, ghi, base, plen);
+            for (uint32_t sub = 0; sub < hs; sub++) {
+                const uint32_t g = gi++;
+                const uint32_t h0 = sub * kCols;
                 const uint32_t H = a.G <= kCols ? a.G : min(kCols, a.G - h0);
-                const uint32_t w[kGroupWords] = {r, a.G <= kCols ? R : 1u, h0, H, seq_of(r), lo, hi, dn, base, plen,
-                                                 item0};
+                const uint32_t w[kGroupWords] = {r, a.G <= kCols ? R : 1u, h0, H, sq, glo, ghi, dn, base, plen, ii};
 #pragma unroll
                 for (uint32_t q = 0; q < kGroupWords; q++) groups[g * kGroupWords + q] = w[q];
                 for (uint32_t p = 0; p < dn; p++) {
-                    uint32_t* it = items + static_cast<size_t>(item0 + p) * kItemWords;
+                    uint32_t* it = items + static_cast<size_t>(ii + p) * kItemWords;
 #pragma unroll
                     for (uint32_t q = 0; q < kGroupWords; q++) it[q] = w[q];
                     it[kGroupWords] = p;
+                    atomicAdd(&s_hist[item_bucket(base, plen, ghi, p)], 1u);
                 }
-                if (bhead) {
-                    const uint32_t b = bc + ib - 1;
-                    const uint32_t bw[kBItemWords] = {g, bng, seq_of(r), blo, bhi, 1u, bbase, bplen, b, 0u};
+                ii += dn;
+            }
+            if (rw & kRowBlockHead) {
+                const uint32_t bng = rw & kRowCount;
+                uint32_t blo, bhi, bbase, bplen;
+                block_range(r, bng, blo, bhi);
+                span_of(blo, bhi, bbase, bplen);
+                const uint32_t b = bi++;
+                const uint32_t bw[kBItemWords] = {gi - 1, bng, sq, blo, bhi, 1u, bbase, bplen, b, 0u};
 #pragma unroll
-                    for (uint32_t q = 0; q < kBItemWords; q++) bitems[b * kBItemWords + q] = bw[q];
-                    pairs[2 * b] = b;
-                    pairs[2 * b + 1] = kNoItem;
-                }
+                for (uint32_t q = 0; q < kBItemWords; q++) bitems[b * kBItemWords + q] = bw[q];
+                pairs[2 * b] = b;
+                pairs[2 * b + 1] = kNoItem;
+                atomicAdd(&s_hist[block_bucket(blo, bhi)], 1u);
             }
         }
-        __syncthreads();
-        if (tid == 0) {
-            s_gc = gc + tg;
-            s_ic = ic + ti;
-            s_bc = bc + tb;
-        }
-        __syncthreads();
     }
-    const uint32_t n_items = s_ic, n_blocks = s_bc, n_entries = n_items + n_blocks;
-    // Launch order: counting sort of every entry by its estimated time,
-    // longest first (bucket kListBuckets - 1 - estimate).
-    auto bucket_of = [&](uint32_t e) -> uint32_t {
-        float us;
-        if (e < n_items) {
-            const uint32_t* it = items + static_cast<size_t>(e) * kItemWords;
-            const uint64_t p0 = uint64_t(it[8]) + uint64_t(it[kGroupWords]) * it[9];
-            const uint64_t keys = it[6] > p0 ? min(uint64_t(it[9]), uint64_t(it[6]) - p0) : 0;
-            us = static_cast<float>(keys) * a.dec_us_per_key;
-        } else {
-            const uint32_t* bk = bitems + static_cast<size_t>(e - n_items) * kBItemWords;
-            const uint32_t tb0 = bk[3] & ~31u, tiles = bk[4] > tb0 ? (bk[4] - tb0 + 63u) / 64u : 0u;
-            us = 10.0f + 4.5f * static_cast<float>(tiles) * static_cast<float>(a.hd_t) / 128.0f;
-        }
-        const uint32_t b = static_cast<uint32_t>(min(us, static_cast<float>(kListBuckets - 1)));
-        return kListBuckets - 1 - b;
-    };
-    for (uint32_t i = tid; i < kListBuckets; i += kDPlanThreads) s_hist[i] = 0;
     __syncthreads();
-    for (uint32_t e = tid; e < n_entries; e += kDPlanThreads) atomicAdd(&s_hist[bucket_of(e)], 1u);
-    __syncthreads();
-    if (tid < 64) {  // exclusive scan of the histogram, four buckets per lane
+
+    // 7. launch order: every entry, longest first (counting sort)
+    if (tid < 64) {  // exclusive sums of the histogram, four buckets per lane
         uint32_t v[4], sum = 0;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -2325,9 +2551,26 @@ __global__ __launch_bounds__(kDPlanThreads) void dplan_list_kernel(DListArgs a) 
     }
     __syncthreads();
     uint32_t* order = a.blob + a.order_off;
-    for (uint32_t e = tid; e < n_entries; e += kDPlanThreads) {
-        const uint32_t pos = atomicAdd(&s_hist[bucket_of(e)], 1u);
-        order[pos] = e < n_items ? e : (0x80000000u | (e - n_items));
+    {
+        uint32_t ii = cnt[1], bi = cnt[2];
+#pragma unroll 1
+        for (uint32_t k = 0; k < K; k++) {
+            const uint32_t r = r0 + k;
+            const uint32_t rw = r < m ? s_np[r] : 0u;
+            if (!(rw & kRowHead)) continue;
+            if (rw & kRowBlockHead) {
+                uint32_t blo, bhi, bbase, bplen;
+                block_range(r, rw & kRowCount, blo, bhi);
+                span_of(blo, bhi, bbase, bplen);
+                order[atomicAdd(&s_hist[block_bucket(blo, bhi)], 1u)] = 0x80000000u | bi++;
+            }
+            if (rw & kRowBlocked) continue;
+            uint32_t glo = s_lo[r], ghi = s_hi[r], base, plen;
+            span_of(glo, ghi, base, plen);
+            for (uint32_t sub = 0; sub < hs; sub++)
+                for (uint32_t p = 0; p < (rw & kRowCount); p++)
+                    order[atomicAdd(&s_hist[item_bucket(base, plen, ghi, p)], 1u)] = ii++;
+        }
     }
     if (tid == 0) {
         a.blob[0] = n_entries;
@@ -3359,6 +3602,9 @@ int thb_dplan_create_ex(thb_pool* pool, uint32_t max_m, uint32_t q_heads, uint32
                 return fail(THB_ERR_CONFIG, "device plans with prefill blocks take head_dim <= 256");
             p->list = true;
             p->wb = block_groups(true, p->hd_max);
+            if (p->wb > kListMaxWB)
+                return fail(THB_ERR_CONFIG, "prefill blocks of " + std::to_string(p->wb) + " groups exceed " +
+                                                std::to_string(kListMaxWB));
             dplan_list_layout(p.get());
         } else {
             dplan_layout(p.get());
@@ -3417,6 +3663,8 @@ int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* 
             la.PL = pool->part_len;
             la.align = std::max<uint32_t>(pool->page_len, 16);
             la.WB = plan->wb;
+            la.rg_magic = div16_magic(la.G <= kCols ? kCols / la.G : 1u);
+            la.wb_magic = div16_magic(la.WB);
             la.pmax = plan->pmax;
             la.hd_t = plan->hd_max;
             la.groups_off = plan->groups_off;

@@ -27,4 +27,22 @@ __host__ __device__ inline void part_split(uint64_t span, uint32_t PL, uint32_t 
     n_parts = static_cast<uint32_t>((span + plen - 1) / plen);
 }
 
+// part_split for 0 < span < 2^31 and a power-of-two align, in 32-bit
+// arithmetic with shifts for the power-of-two divisors (n and align): the
+// device planner's form (a 64-bit division is a long instruction sequence
+// on the GPU).  Same results as part_split.
+__host__ __device__ inline void part_split32(uint32_t span, uint32_t PL, uint32_t align, uint32_t& n_parts,
+                                             uint32_t& plen) {
+    const uint32_t k = span / PL;
+    uint32_t n = k + (span - k * PL != 0 ? 1u : 0u);
+    if (n > 2 && span - k * PL <= k * (PL / 64)) n = k;
+    uint32_t sh = 0;
+    if (n > 1) {
+        sh = 32 - __builtin_clz(n - 1);
+        n = 1u << sh;
+    }
+    plen = (((span + n - 1) >> sh) + align - 1) & ~(align - 1);
+    n_parts = (span + plen - 1) / plen;
+}
+
 }  // namespace thb

@@ -160,12 +160,14 @@ def attn(q, kv: KvPool, layer: int, y, spec: AttnSpec, stream=None) -> None:
 
 
 class DevicePlan:
-    """thb_dplan_*: a decode call planned on the device from the row meta in
-    device memory (no reference counterpart), so that a step can be captured
-    in a graph once and replayed while positions move.  ``build`` plans the
-    spec's rows (q and y give the spec's dtypes); ``attn`` runs attention of
-    one layer over the plan.  Each (group, partition) computes what ``attn``
-    computes, bit for bit."""
+    """thb_dplan_*: an attention call planned on the device from the row meta
+    in device memory (no reference counterpart), so that a step can be
+    captured in a graph once and replayed while positions move.  ``build``
+    plans the spec's rows (q and y give the spec's dtypes); ``attn`` runs
+    attention of one layer over the plan.  Each (group, partition) computes
+    what ``attn`` computes, bit for bit; in a work-list plan (prefill=True) a
+    prefill block whose keys span several partitions runs as decode groups,
+    whose sums are ordered differently from ``attn``'s."""
 
     def __init__(self, kv: KvPool, max_m: int, q_heads: int, prefill: bool = False):
         """prefill=True: a work-list plan (thb_dplan_create_ex with

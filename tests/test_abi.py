@@ -3,6 +3,7 @@ CPU only: no compute entry point is called."""
 
 import ctypes
 import os
+import random
 import re
 
 import pytest
@@ -129,7 +130,8 @@ def test_partition_rule(tmp_path):
     at most part_len + part_len / 64 (rounded up to the alignment) long, never
     outnumber ceil(span / part_len) rounded up to a power of two, and at the
     longest part_len the pool accepts (1008 pages) fit the kernels' 1024 staged
-    page numbers."""
+    page numbers.  thb::part_split32 (the device planner's 32-bit form, for
+    spans below 2^31) gives the same result on every such case."""
     import subprocess
 
     known = {  # span -> (n_parts, plen) at part_len 4096, align 16
@@ -142,16 +144,24 @@ def test_partition_rule(tmp_path):
         for s in list(range(1, 3 * pl, max(1, pl // 61))) + [k * pl + d for k in range(2, 40) for d in (0, 1, pl // 64 * k,
                                                                                                       pl // 64 * k + 1)]:
             cases.append((s, pl, align))
+    rng = random.Random(7)
+    for _ in range(4000):
+        cases.append((rng.randrange(1, 1 << 31), rng.randrange(1, 1009) * 16, 1 << rng.randrange(4, 9)))
+    cases += [((1 << 31) - 1, 4096, 16), ((1 << 31) - 1, 16128, 256), ((1 << 31) - 5000, 16, 16)]
     src = tmp_path / "parts.cpp"
     src.write_text('#include <cstdio>\n#include "partition.hpp"\nint main() {\n'
                    f"static const unsigned long long c[][3] = {{{','.join(f'{{{s},{p},{a}}}' for s, p, a in cases)}}};\n"
-                   "for (const auto& x : c) { uint32_t n, plen; thb::part_split(x[0], (uint32_t)x[1], (uint32_t)x[2], n, plen);"
-                   ' std::printf("%u %u\\n", n, plen); }\nreturn 0; }\n')
+                   "for (const auto& x : c) { uint32_t n, plen, n32, plen32;"
+                   " thb::part_split(x[0], (uint32_t)x[1], (uint32_t)x[2], n, plen);"
+                   " thb::part_split32((uint32_t)x[0], (uint32_t)x[1], (uint32_t)x[2], n32, plen32);"
+                   ' std::printf("%u %u %u %u\\n", n, plen, n32, plen32); }\nreturn 0; }\n')
     exe = tmp_path / "parts"
     subprocess.run(["g++", "-std=c++17", "-O1", "-D__host__=", "-D__device__=", "-I",
                     os.path.join(ROOT, "flint_amd", "csrc"), str(src), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
-    got = [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(len(cases))]
+    got = [(int(out[4 * i]), int(out[4 * i + 1])) for i in range(len(cases))]
+    got32 = [(int(out[4 * i + 2]), int(out[4 * i + 3])) for i in range(len(cases))]
+    assert got32 == got
     for s, np_ in zip(known, got):
         assert np_ == known[s], (s, np_)
     for (s, pl, align), (n, plen) in zip(cases, got):

@@ -218,6 +218,9 @@ LIST_CASES = [
     ("long-prefix-split-blocks", 32, 8, 128, "f16", [900], [(6000, 256)], 2048, 0, 0.0, False),
     ("qwen2-bf16", 14, 2, 64, "bf16", [128, 512, 300], [(400, 100)], 512, 0, 0.0, True),
     ("gemma-one-partition", 16, 8, 256, "f16", [1300, 2000], [(600, 200), (512, 512)], 4096, 4096, 50.0, True),
+    ("6k-rows", 32, 8, 128, "f16", [5000] * 5 + [90, 17000, 1], [(2048, 2048), (4096, 2048), (3000, 1999)], 4096, 0,
+     0.0, True),
+    ("g32-two-groups-per-row", 32, 1, 128, "f16", [700, 3000], [(600, 300), (5000, 77)], 2048, 0, 0.0, False),
 ]
 
 
