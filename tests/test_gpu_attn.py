@@ -308,7 +308,7 @@ def test_split_groups_combined_in_launch(torch_cuda, case):
         assert torch.equal(y, y2), (name, i, float((y - y2).abs().max()))
 
 
-def test_llama3_full_shape_sampled(torch_cuda):
+def test_llama3_full_shape(torch_cuda):
     """BASELINE config 2 at full size (B=32, ctx 4096, 32q/8kv/hd128, f16 KV,
     scattered block tables): the oracle checks all 32 sequences in full, and
     every output is a convex combination of V (|y| <= max |V|)."""
