@@ -67,9 +67,11 @@ def test_device_plan_matches_attn(torch_cuda, case):
     plan.close()
 
 
-def test_device_plan_fixed_sequence(torch_cuda):
+@pytest.mark.parametrize("prefill", [False, True], ids=["grid", "list"])
+def test_device_plan_fixed_sequence(torch_cuda, prefill):
     """Reference mode: spec.seq fixed, a 3-row chunk (one group of 4 heads x 3
-    rows at G = 4), rows of the chunk reading different key counts."""
+    rows at G = 4), rows of the chunk reading different key counts; in both
+    plan forms."""
     torch = torch_cuda
     from flint_amd import ops
     from flint_amd.pool import RowMeta
@@ -84,11 +86,40 @@ def test_device_plan_fixed_sequence(torch_cuda):
     spec = ops.AttnSpec(q_heads=8, window=0, scale=0.125, m=3, causal=True, seq=1, args=rows)
     want, got = torch.empty_like(q), torch.empty_like(q)
     ops.attn(q, pool, 0, want, spec)
-    plan = ops.DevicePlan(pool, max_m=3, q_heads=8)
+    plan = ops.DevicePlan(pool, max_m=3, q_heads=8, prefill=prefill)
     plan.build(spec, q, got)
     plan.attn(0, q, got)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_list_plan_fixed_sequence_prefill_chunk(torch_cuda):
+    """Reference mode in a work-list plan: a 40-row prefill chunk of one
+    sequence with spec.seq fixed (the reference's one dispatch per chunk),
+    causal and not, cut into prefill blocks; equal to thb_attn bit for bit."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    lens = [700, 300]
+    pool = make_pool(lens, kv_heads=2, head_dim=64, page_len=16, kv_dtype="f16", part_len=1024)
+    scattered_alloc(pool, lens, random.Random(40), 16)
+    rows = RowMeta(64)
+    fill(torch, pool, rows, lens, seed=40)
+    rows.write(list(range(600, 640)), [0] * 40, 40)
+    q = torch.randn(40, 16, 64, device="cuda")
+    plan = ops.DevicePlan(pool, max_m=40, q_heads=16, prefill=True)
+    for causal in (True, False):
+        spec = ops.AttnSpec(q_heads=16, window=0, scale=0.125, m=40, causal=causal, seq=0, args=rows)
+        want, got = torch.empty_like(q), torch.full_like(q, 7.0)
+        ops.attn(q, pool, 0, want, spec)
+        plan.build(spec, q, got)
+        plan.attn(0, q, got)
+        torch.cuda.synchronize()
+        say("list plan fixed-seq chunk, causal", causal)
+        assert torch.isfinite(want).all()
+        assert torch.equal(got, want), (causal, float((got - want).abs().max()))
+    plan.close()
 
 
 def test_graph_replay_with_moving_positions(torch_cuda):
@@ -144,10 +175,12 @@ def test_graph_replay_with_moving_positions(torch_cuda):
     plan.close()
 
 
-def test_uncovered_row_reads_nothing_and_is_reported(torch_cuda):
+@pytest.mark.parametrize("prefill", [False, True], ids=["grid", "list"])
+def test_uncovered_row_reads_nothing_and_is_reported(torch_cuda, prefill):
     """A row past its sequence's pages: thb_attn refuses the call; the device
-    plan gives that row NaN, the other rows their thb_attn values, and
-    thb_pool_status reports the first uncovered row (then clears)."""
+    plan (either form) gives that row NaN, the other rows their thb_attn
+    values, and thb_pool_status reports the first uncovered row (then
+    clears)."""
     torch = torch_cuda
     from flint_amd import ThubanError, ops
     from flint_amd.pool import RowMeta
@@ -164,7 +197,7 @@ def test_uncovered_row_reads_nothing_and_is_reported(torch_cuda):
         ops.attn(q, pool, 0, torch.empty_like(q), spec)
     assert "pages must cover the chunk" in str(e.value)
     got = torch.empty_like(q)
-    plan = ops.DevicePlan(pool, max_m=2, q_heads=4)
+    plan = ops.DevicePlan(pool, max_m=2, q_heads=4, prefill=prefill)
     plan.build(spec, q, got)
     plan.attn(0, q, got)
     torch.cuda.synchronize()
@@ -221,6 +254,7 @@ LIST_CASES = [
     ("6k-rows", 32, 8, 128, "f16", [5000] * 5 + [90, 17000, 1], [(2048, 2048), (4096, 2048), (3000, 1999)], 4096, 0,
      0.0, True),
     ("g32-two-groups-per-row", 32, 1, 128, "f16", [700, 3000], [(600, 300), (5000, 77)], 2048, 0, 0.0, False),
+    ("8192-rows", 32, 8, 128, "f16", [3000, 90], [(4096, 4094), (4096, 4096)], 4096, 0, 0.0, True),
 ]
 
 
@@ -257,7 +291,7 @@ def test_list_plan_with_prefill_matches_attn(torch_cuda, case):
     want = torch.empty(m, nq, hd, device="cuda")
     got = torch.full_like(want, 7.0)
     ops.attn(q, pool, 0, want, spec)
-    plan = ops.DevicePlan(pool, max_m=m + 5, q_heads=nq, prefill=True)
+    plan = ops.DevicePlan(pool, max_m=min(m + 5, 8192), q_heads=nq, prefill=True)
     plan.build(spec, q, got)
     plan.attn(0, q, got)
     plan.attn(0, q, got)  # a second launch: the claim counter was reset by the first
