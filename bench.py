@@ -449,7 +449,7 @@ def cpu_baseline_record(value_gbps, median_s, runs, sample):
 
 def cpu_baseline(torch, pool, q0, y0, cfg, scale, seconds):
     """Times the oracle on layer 0 of the workload: median of >= 20 runs
-    after 3 warm-ups (BASELINE.md section 3)."""
+    after 3 warm-ups."""
     import numpy as np
 
     import oracle
