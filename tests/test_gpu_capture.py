@@ -6,7 +6,9 @@ crates/thuban_model/src/pool.rs:47-65), kv_store and attention
 thb_kv_store, thb_dplan_build and thb_attn_dplan, then replayed while the
 rows move, sequences fork and speculative rollbacks truncate into shared
 pages (so replays must copy on write).  Every replay equals the eager path
-bit for bit, and the device allocator's state equals oracle/arena.py.  Calls
+bit for bit, and the device allocator's state equals oracle/arena.py; the
+same holds for a continuous batch (decode rows and a walking prefill chunk)
+captured with the work-list plan.  Calls
 that cannot replay correctly refuse a capturing stream, and once the page
 allocation is captured the host reloads its mirror from the device before
 every host-side call."""
@@ -279,3 +281,112 @@ def test_replayed_alloc_rows_rejects_bad_and_repeated_sequences(torch_cuda):
     pool.pull()
     assert len(pool.arena.table_of(0)) == 2 and len(pool.arena.table_of(2)) == 2
     del graph
+
+
+def test_captured_continuous_batch_with_list_plan_matches_eager(torch_cuda):
+    """Continuous batching in a captured step (the engine's mixed plans,
+    thuban_generate/src/engine.rs:237-300, one forward over decode rows and
+    prefill chunks, transformer/forward.rs:314-336): four sequences decode
+    one token per step while a 256-row prefill chunk walks through three
+    arriving 512-token prompts, two chunks each.  E runs each step eagerly
+    (alloc_rows, kv_store and thb_attn per layer); G replays one captured
+    graph of (alloc_rows, kv_store per layer, one build of a work-list device
+    plan, thb_attn_dplan per layer).  Every step's outputs are identical bit
+    for bit, and at the end both pools' bytes and allocator states are equal
+    and equal the oracle's."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    nq, nkv, hd, P, L, C, plen = 32, 8, 128, 16, 2, 256, 512
+    prompts = [300, 1200, 77, 640]
+    arriving = [4, 5, 6]
+    budgets = [n + 16 for n in prompts] + [plen] * len(arriving)
+    pools = []
+    for _ in range(2):
+        pool = make_pool(budgets, kv_heads=nkv, head_dim=hd, page_len=P, kv_dtype="f16", layers=L)
+        scattered_alloc(pool, prompts, random.Random(23), P)
+        fr = RowMeta(256)
+        for layer in range(L):
+            fill(torch, pool, fr, prompts, layer=layer, seed=60 + layer)
+        pool.sync()
+        pools.append(pool)
+    E, G = pools
+    orc = KvArena(budgets, pages=E.arena.pages(), page_len=P)
+    rng = random.Random(23)
+    need = [-(-n // P) for n in prompts]
+    have = [0] * len(prompts)
+    order = [s for s in range(len(prompts)) for _ in range(need[s])]
+    rng.shuffle(order)
+    for s in order:  # scattered_alloc's calls, in its order
+        orc.alloc(s, have[s] * P, P if (have[s] + 1) * P <= prompts[s] else prompts[s] - have[s] * P)
+        have[s] += 1
+    orc.copies.clear()
+    assert _state(E) == _state(G) == (orc.free, orc.refs, orc.table())
+
+    m = len(prompts) + C
+    rows = {"E": RowMeta(m), "G": RowMeta(m)}
+    k_in = [torch.empty(m, nkv, hd, device="cuda", dtype=torch.float16) for _ in range(L)]
+    v_in = [torch.empty_like(k_in[0]) for _ in range(L)]
+    q_in = [torch.empty(m, nq, hd, device="cuda", dtype=torch.float16) for _ in range(L)]
+    y = {"E": [torch.empty(m, nq, hd, device="cuda") for _ in range(L)],
+         "G": [torch.empty(m, nq, hd, device="cuda") for _ in range(L)]}
+    specs = {w: ops.AttnSpec(q_heads=nq, window=0, scale=1 / math.sqrt(hd), m=m, causal=True, seq=None,
+                             args=rows[w]) for w in rows}
+
+    def eager_step():
+        E.alloc_rows(rows["E"], m)
+        for layer in range(L):
+            ops.kv_store(k_in[layer], v_in[layer], E, layer, m, rows["E"])
+            ops.attn(q_in[layer], E, layer, y["E"][layer], specs["E"])
+
+    plan = ops.DevicePlan(G, max_m=m, q_heads=nq, prefill=True)
+
+    def graph_step():
+        G.alloc_rows(rows["G"], m)
+        for layer in range(L):
+            ops.kv_store(k_in[layer], v_in[layer], G, layer, m, rows["G"])
+        plan.build(specs["G"], q_in[0], y["G"][0])
+        for layer in range(L):
+            plan.attn(layer, q_in[layer], y["G"][layer])
+
+    graph = _capture(torch, graph_step)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(61)
+    dpos = list(prompts)
+    for step in range(2 * len(arriving)):
+        seq, c0 = arriving[step // 2], (step % 2) * C
+        positions = dpos + list(range(c0, c0 + C))
+        seqs = list(range(len(prompts))) + [seq] * C
+        for w in rows:
+            rows[w].write(positions, seqs, m)
+        for layer in range(L):
+            k_in[layer].copy_(torch.randn(m, nkv, hd, device="cuda", generator=gen))
+            v_in[layer].copy_(torch.randn(m, nkv, hd, device="cuda", generator=gen))
+            q_in[layer].copy_(torch.randn(m, nq, hd, device="cuda", generator=gen))
+        for w in ("E", "G"):
+            for layer in range(L):
+                y[w][layer].fill_(float("nan"))
+        torch.cuda.synchronize()
+        eager_step()
+        graph.replay()
+        orc.alloc_rows(positions, seqs)
+        orc.copies.clear()
+        torch.cuda.synchronize()
+        say("captured continuous batch step", step, "prefill seq", seq, "rows", c0, "..", c0 + C - 1)
+        for layer in range(L):
+            assert torch.isfinite(y["E"][layer]).all(), (step, layer)
+            assert torch.equal(y["G"][layer], y["E"][layer]), (step, layer,
+                                                               float((y["G"][layer] - y["E"][layer]).abs().max()))
+        dpos = [p + 1 for p in dpos]
+    G.status()
+    G.pull()
+    want = (orc.free, orc.refs, orc.table())
+    assert _state(G) == want
+    assert _state(E) == want
+    for layer in range(L):
+        ka, va = E.read_layer(layer)
+        kb, vb = G.read_layer(layer)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb), layer
+    del graph
+    plan.close()
