@@ -5,10 +5,12 @@ partitions), random contexts, 1-4 rows per sequence, a random window and
 soft-cap.  Checked against the CPU oracle (exact softmax in double, the
 reference's kv_len / window / causal rules of attn.wgsl:78-88,169), and
 bit for bit between the paths that must agree: the fused append
-(thb_attn_append) against kv_store followed by attn, the device-planned call
-(thb_dplan_*) and the no-allocation call (thb_attn_noalloc, whose split
-groups are combined by the merge kernel after the launch) against thb_attn
-(combined inside the launch)."""
+(thb_attn_append) against kv_store followed by attn, the device-planned calls
+(thb_dplan_*: the fixed grid and the work list) and the no-allocation call
+(thb_attn_noalloc, whose split groups are combined by the merge kernel after
+the launch) against thb_attn (combined inside the launch).  A second set of
+seeded calls mixes decode rows with prefill chunks (random sizes and
+prefixes) and checks the work-list plan against the oracle and thb_attn."""
 
 import ctypes
 import math
@@ -105,13 +107,14 @@ def test_random_calls_agree(torch_cuda, seed):
     say("random call", seed, "max abs err", err)
     assert err <= TIGHT, (seed, err)
 
-    yc = torch.full_like(q, 7.0)
-    plan = ops.DevicePlan(pools[0], max_m=m, q_heads=nq)
-    plan.build(spec, q, yc)
-    plan.attn(0, q, yc)
-    torch.cuda.synchronize()
-    plan.close()
-    assert torch.equal(yc, ya), (seed, "device plan", float((yc - ya).abs().max()))
+    for prefill in (False, True):  # the fixed grid and the work list
+        yc = torch.full_like(q, 7.0)
+        plan = ops.DevicePlan(pools[0], max_m=m, q_heads=nq, prefill=prefill)
+        plan.build(spec, q, yc)
+        plan.attn(0, q, yc)
+        torch.cuda.synchronize()
+        plan.close()
+        assert torch.equal(yc, ya), (seed, "device plan", prefill, float((yc - ya).abs().max()))
 
     yd = torch.full_like(q, 7.0)
     rc = _noalloc(pools[0], q, yd, spec)
@@ -121,3 +124,82 @@ def test_random_calls_agree(torch_cuda, seed):
         return
     torch.cuda.synchronize()
     assert torch.equal(yd, ya), (seed, "no-allocation call", float((yd - ya).abs().max()))
+
+
+N_MIXED = 10
+
+
+def _mixed_case(seed):
+    rng = random.Random(seed)
+    hd = rng.choice([64, 128, 128, 256])
+    nkv = rng.choice([1, 2, 4, 8])
+    g = rng.choice([1, 2, 4, 7, 8])
+    pl = rng.choice([16, 32])
+    part_len = rng.choice([128, 512, 1024, 2048])
+    dlens = [rng.randint(2, 1500) for _ in range(rng.randint(0, 4))]
+    chunks = [(rng.randint(0, 1200), rng.randint(4, 200)) for _ in range(rng.randint(1, 2))]  # (prefix, rows)
+    window = rng.choice([0, 0, rng.randint(64, 900)])
+    cap = rng.choice([0.0, 0.0, 30.0])
+    return dict(hd=hd, nkv=nkv, nq=g * nkv, pl=pl, part_len=part_len, dlens=dlens, chunks=chunks, window=window,
+                cap=cap, kv=rng.choice(["f16", "bf16"]), q16=rng.choice([True, False]))
+
+
+@pytest.mark.parametrize("seed", range(N_MIXED))
+def test_random_mixed_calls_list_plan(torch_cuda, seed):
+    """Seeded random calls of decode rows and prefill chunks (random head_dim,
+    grouping, page and partition lengths, window, soft-cap, KV type, f16 or
+    f32 queries, chunk sizes and prefixes): the work-list device plan against
+    the oracle (1e-4) and against thb_attn, bit for bit when every chunk's
+    keys fit one partition (its blocks then run on the prefill kernel in
+    both), else within 1e-5 (a block spanning partitions runs as decode
+    groups in the list)."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+
+    c = _mixed_case(2000 + seed)
+    say("random mixed call", seed, c)
+    hd, nkv, nq, pl, PL, window = c["hd"], c["nkv"], c["nq"], c["pl"], c["part_len"], c["window"]
+    lens = c["dlens"] + [p + n for p, n in c["chunks"]]
+    pool = make_pool(lens, kv_heads=nkv, head_dim=hd, page_len=pl, kv_dtype=c["kv"], extra_pages=3, part_len=PL)
+    scattered_alloc(pool, lens, random.Random(seed), pl)
+    fill(torch, pool, RowMeta(256), lens, seed=seed)
+    positions = [n - 1 for n in c["dlens"]]
+    seqs = list(range(len(c["dlens"])))
+    exact = True
+    align = max(pl, 16)
+    for i, (p, n) in enumerate(c["chunks"]):
+        positions += list(range(p, p + n))
+        seqs += [len(c["dlens"]) + i] * n
+        lo = max(0, p + 1 - window) if window else 0
+        exact = exact and (p + n) - (lo - lo % align) <= PL
+    m = len(seqs)
+    rows = RowMeta(m)
+    rows.write(positions, seqs, m)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    q = torch.randn(m, nq, hd, device="cuda", generator=gen)
+    if c["q16"]:
+        q = q.half()
+    spec = ops.AttnSpec(q_heads=nq, window=window, scale=1 / math.sqrt(hd), m=m, causal=True, seq=None, args=rows,
+                        softcap=c["cap"])
+    want = torch.empty(m, nq, hd, device="cuda")
+    got = torch.full_like(want, 7.0)
+    ops.attn(q, pool, 0, want, spec)
+    plan = ops.DevicePlan(pool, max_m=m, q_heads=nq, prefill=True)
+    plan.build(spec, q, got)
+    plan.attn(0, q, got)
+    torch.cuda.synchronize()
+    plan.close()
+    ref = oracle_layer(torch, pool).attn(q.float().cpu().numpy(), oracle.row_meta(positions, seqs), m, nq,
+                                         1 / math.sqrt(hd), window=window, softcap=c["cap"])
+    g_np = got.cpu().numpy()
+    finite = np.isfinite(ref)
+    assert np.array_equal(finite, np.isfinite(g_np)), (seed, "NaN rows differ from the oracle")
+    err = float(np.max(np.abs(g_np[finite] - ref[finite]))) if finite.any() else 0.0
+    say("random mixed call", seed, "exact" if exact else "split blocks", "max abs err vs oracle", err)
+    assert err <= TIGHT, (seed, err)
+    if exact:
+        assert torch.equal(got, want), (seed, float((got - want).abs().max()))
+    else:
+        assert float((got - want).abs().max()) <= 1e-5, seed
