@@ -104,6 +104,37 @@ def time_append_graph(torch, ops, pool, rows, k, v, layer, m, launches=50, repla
         return None
 
 
+def time_decode_graph(torch, ops, pool, spec, q, k_new, v_new, y_eager, L, B, nq, replays):
+    """The headline step as a serving loop replays it: one thb_dplan_build,
+    then for each layer thb_attn_append_dplan (append + decode in one launch
+    over the device plan), captured once in a HIP graph.  Returns (us per
+    layer over the replays, outputs bit-identical to the eager step's)."""
+    plan = ops.DevicePlan(pool, max_m=B, q_heads=nq, append=True)
+    yg = torch.empty_like(y_eager)
+
+    def body():
+        plan.build(spec, q[0], yg[0])
+        for layer in range(L):
+            plan.attn_append(layer, k_new[layer], v_new[layer], q[layer], yg[layer])
+
+    body()  # outside the capture first: nothing left to set up
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            body()
+    torch.cuda.current_stream().wait_stream(side)
+    yg.fill_(float("nan"))
+    us = _time_steps(torch, graph.replay, replays, 2) / L
+    same = bool(torch.equal(yg, y_eager))
+    pool.status()  # the plan's checks passed on every replay
+    del graph
+    plan.close()
+    return us, same
+
+
 def time_hbm_ceiling(torch, dev, mib=1024, reps=5):
     """The device's achievable linear HBM rate, measured next to the 8 TB/s
     specification: thb_hbm_stream over `mib` MiB with 16-byte non-temporal
@@ -558,31 +589,53 @@ def measure_secondary(name, args):
         sp = spec(rows, nq, hd, B)
         us = _time_steps(torch, lambda: ops.kv_store_attn(k, v, q, pool, 0, y, sp), args.steps, args.warmup)
         byts = sum(c + 1 for c in ctx) * nkv * hd * 2 * 2
-        # the same step as a serving loop replays it: kv_store + device-planned attention captured
-        # once in a HIP graph (thb_attn plans on the host and cannot be captured); 20 steps per graph
-        plan = ops.DevicePlan(pool, max_m=B, q_heads=nq)
-        yg = torch.empty_like(q)
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(graph, stream=side):
-                for _ in range(20):
+        # the same step as a serving loop replays it, captured once in a HIP graph (thb_attn plans
+        # on the host and cannot be captured), 20 steps per graph: thb_dplan_build +
+        # thb_attn_append_dplan (the append inside the attention launch), and for comparison
+        # kv_store + thb_dplan_build + thb_attn_dplan
+        def graph_us(fused):
+            plan = ops.DevicePlan(pool, max_m=B, q_heads=nq, append=fused)
+            yg = torch.empty_like(q)
+
+            def body():
+                if not fused:
                     ops.kv_store(k, v, pool, 0, B, rows)
-                    plan.build(sp, q, yg)
+                plan.build(sp, q, yg)
+                if fused:
+                    plan.attn_append(0, k, v, q, yg)
+                else:
                     plan.attn(0, q, yg)
-        torch.cuda.current_stream().wait_stream(side)
-        gus = _time_steps(torch, graph.replay, max(1, args.steps // 5), 2) / 20
-        ops.kv_store_attn(k, v, q, pool, 0, y, sp)
-        torch.cuda.synchronize()
-        same = bool(torch.equal(y, yg))
-        del graph
-        plan.close()
+
+            body()  # outside the capture first: nothing left to set up
+            torch.cuda.synchronize()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(graph, stream=side):
+                    for _ in range(20):
+                        body()
+            torch.cuda.current_stream().wait_stream(side)
+            yg.fill_(float("nan"))
+            t = _time_steps(torch, graph.replay, max(1, args.steps // 5), 2) / 20
+            ops.kv_store_attn(k, v, q, pool, 0, y, sp)
+            torch.cuda.synchronize()
+            same = bool(torch.equal(y, yg))
+            pool.status()
+            del graph
+            plan.close()
+            return t, same
+
+        gus, same = graph_us(True)
+        gus3, same3 = graph_us(False)
         out["graph_step"] = {"us_per_step": round(gus, 2), "GBps": round(byts / (gus * 1e-6) / 1e9, 1),
-                             "bit_identical_to_eager": same,
-                             "note": "kv_store + thb_dplan_build + thb_attn_dplan captured in a HIP graph (20 "
-                                     "steps per graph), replayed; the eager line above is one fused launch per "
-                                     "step issued from Python"}
+                             "bit_identical_to_eager": same and same3,
+                             "three_launch_us_per_step": round(gus3, 2),
+                             "note": "thb_dplan_build + thb_attn_append_dplan (append and decode in one launch) "
+                                     "captured in a HIP graph (20 steps per graph), replayed; "
+                                     "three_launch_us_per_step: kv_store + thb_dplan_build + thb_attn_dplan "
+                                     "the same way; the eager line above is one fused launch per step issued "
+                                     "from Python with the plan made on the host"}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = c1_cpu_baseline(torch, pool, rows, k, v, q, y, ctx, nq, hd, byts,
                                                   min(args.cpu_seconds, 3.0))
@@ -893,6 +946,9 @@ def main():
     torch.cuda.synchronize()
     log(f"rope step: reference-shaped 4 launches {rope_us['unfused']:.1f} us/layer, "
         f"fused {rope_us['fused']:.1f} us/layer")
+    graph_us, graph_same = time_decode_graph(torch, ops, pool, spec, q, k_new, v_new, y, L, B, nq,
+                                             max(2, min(args.steps, 10)))
+    log(f"captured step: {graph_us:.2f} us/layer (eager {attn_us:.2f}), bit-identical {graph_same}")
 
     kv_bytes = B * nkv * ctx * hd * 2 * 2
     qo_bytes = 2 * B * nq * hd * 2
@@ -939,6 +995,14 @@ def main():
                      "algorithmic_bytes": fused_bytes, "launches_timed": len(timed) * per_run},
         "cpu_baseline": None,
     }
+    out["graph_step"] = {"us_per_step": round(graph_us * L, 1), "eager_us_per_step": round(ms_step * 1e3, 1),
+                         "us_per_layer": round(graph_us, 2), "eager_us_per_layer": round(attn_us, 2),
+                         "ratio_to_eager": round(graph_us / attn_us, 4),
+                         "GBps": round(fused_bytes / (graph_us * 1e-6) / 1e9, 1),
+                         "bit_identical_to_eager": graph_same,
+                         "note": "the step captured once in a HIP graph and replayed: one thb_dplan_build per "
+                                 "step, then per layer thb_attn_append_dplan (append + decode planned on the "
+                                 "device, one launch); us_per_layer includes the plan build's share"}
     out["rope"] = {"fused_us_per_layer": round(rope_us["fused"], 2),
                    "unfused_us_per_layer": round(rope_us["unfused"], 2),
                    "fused_GBps": round(fused_bytes / (rope_us["fused"] * 1e-6) / 1e9, 1),

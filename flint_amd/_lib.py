@@ -175,6 +175,7 @@ SIGNATURES = [
     ("thb_dplan_destroy", None, [_vp]),
     ("thb_dplan_build", _int, [_vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_attn_dplan", _int, [_vp, _u32, _vp, _vp, _vp, _vp]),
+    ("thb_attn_append_dplan", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_gather_batch", _int, [_vp, ctypes.POINTER(KvRangeC), _u32, _vp, _vp, _vp]),

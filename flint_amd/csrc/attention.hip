@@ -1949,6 +1949,7 @@ struct DPlanArgs {
     uint32_t npages_off;
     uint32_t m, seq_fixed, causal, window, G, PL, align, pmax, gmax, page_shift, seqs;
     uint32_t items_off, ranges_off, merge_off;
+    uint32_t append;  // the plan serves thb_attn_append_dplan: check that the append can run in the launch
 };
 
 // build_plan's partition of a key range [lo, hi) (lo = hi = 0 when empty).
@@ -2066,6 +2067,78 @@ __device__ void dplan_rows(const DPlanRows& a, uint32_t* s_ck, uint32_t* s_cs, u
     __syncthreads();
 }
 
+// For a plan that serves thb_attn_append_dplan: build_plan's conditions for
+// running the append inside the attention launch, checked on the device at
+// every build.  Each chunk fits one group; every row's keys end at its new
+// token (hi == pos + 1, lo <= pos) and positions rise within the chunk; with
+// a fixed sequence every row's own sequence is that one (the append takes
+// the row meta's); no sequence heads two chunks (two groups would append to
+// and read one sequence's pages in one launch).  At the first failing row
+// (lowest row; code row << 3 | reason) the status is recorded and every
+// row's range emptied: the launch then appends nothing and writes NaN.
+constexpr uint32_t kFuseSetBits = 13;
+constexpr uint32_t kFuseSet = 1u << kFuseSetBits;  // open-addressing set of the chunk heads' sequences
+static_assert(kFuseSet >= 2 * kDPlanMaxRows, "the set keeps at least half its slots empty");
+
+__device__ void dplan_check_fused(const DPlanArgs& a, const uint32_t* s_ck, const uint32_t* s_cs, uint32_t* s_lo,
+                                  uint32_t* s_hi) {
+    constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+    __shared__ uint32_t s_key[kFuseSet], s_first[kFuseSet];  // a sequence, its lowest chunk-head row
+    __shared__ uint32_t s_bad;
+    const uint32_t tid = threadIdx.x, m = a.m;
+    const bool per_row = a.seq_fixed == THB_SEQ_PER_ROW;
+    const uint32_t rg = a.G <= kCols ? kCols / a.G : 1u;
+    for (uint32_t i = tid; i < kFuseSet; i += kDPlanThreads) {
+        s_key[i] = kEmpty;
+        s_first[i] = kEmpty;
+    }
+    if (tid == 0) s_bad = kEmpty;
+    __syncthreads();
+    auto slot = [](uint32_t seq) { return (seq * 0x9E3779B1u) >> (32 - kFuseSetBits); };
+    for (uint32_t r = tid; r < m; r += kDPlanThreads) {
+        const uint32_t ck = s_ck[r], c0 = s_cs[ck], n = s_cs[ck + 1] - c0;
+        const uint32_t pos = a.meta[8u * r], seq = a.meta[8u * r + 1];
+        uint32_t why = 0;
+        if (n > rg)
+            why = kNoFuseChunk;
+        else if (uint64_t(s_hi[r]) != uint64_t(pos) + 1 || s_lo[r] > pos || (r > c0 && pos <= a.meta[8u * (r - 1)]))
+            why = kNoFuseKeys;  // also a row its pages do not cover (its range is empty)
+        else if (!per_row && seq != a.seq_fixed)
+            why = kNoFuseSeq;
+        if (why) atomicMin(&s_bad, (r << 3) | why);
+        if (per_row && r == c0 && seq < a.seqs) {
+            uint32_t h = slot(seq);
+            for (;;) {
+                const uint32_t old = atomicCAS(&s_key[h], kEmpty, seq);
+                if (old == kEmpty || old == seq) break;
+                h = (h + 1) & (kFuseSet - 1);
+            }
+            atomicMin(&s_first[h], r);
+        }
+    }
+    __syncthreads();
+    for (uint32_t r = tid; r < m; r += kDPlanThreads) {
+        const uint32_t seq = a.meta[8u * r + 1];
+        if (!per_row || s_cs[s_ck[r]] != r || seq >= a.seqs) continue;
+        uint32_t h = slot(seq);
+        while (s_key[h] != seq) h = (h + 1) & (kFuseSet - 1);
+        if (s_first[h] != r) atomicMin(&s_bad, (r << 3) | kNoFuseTwice);
+    }
+    __syncthreads();
+    const uint32_t bad = s_bad;
+    if (bad == kEmpty) return;
+    if (tid == 0) {
+        const uint32_t r = bad >> 3, why = bad & 7u;
+        dplan_fail(a.state, kPageStNoFuse, r, per_row || why == kNoFuseSeq ? a.meta[8u * r + 1] : a.seq_fixed, why);
+    }
+    uint32_t* ranges = a.blob + a.ranges_off;
+    for (uint32_t r = tid; r < m; r += kDPlanThreads) {
+        s_lo[r] = s_hi[r] = 0;
+        ranges[2u * r] = ranges[2u * r + 1] = 0;
+    }
+    __syncthreads();
+}
+
 __global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
     __shared__ uint32_t s_ck[kDPlanMaxRows];      // chunk of each row
     __shared__ uint32_t s_cs[kDPlanMaxRows + 1];  // first row of each chunk, then m
@@ -2089,6 +2162,7 @@ __global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
         ra.seqs = a.seqs;
         dplan_rows(ra, s_ck, s_cs, s_lo, s_hi, s_red, s_carry);
     }
+    if (a.append) dplan_check_fused(a, s_ck, s_cs, s_lo, s_hi);
 
     // Groups: rows r0 .. r0 + R - 1 of a chunk (R <= 16 / G), or at G > 16 one
     // row and 16 of its query heads per group; group words as build_plan's.
@@ -3512,6 +3586,7 @@ struct thb_dplan {
     // as attn_list; the blob is [header | groups | items | ranges | blocks |
     // pairs | order].
     bool list = false;
+    bool append = false;  // THB_DPLAN_APPEND: each build checks that the append can run in the launch
     uint32_t imax = 0, bmax = 0, wb = 0;
     uint32_t groups_off = 0, bitems_off = 0, pairs_off = 0, order_off = 0;
     bool built = false;
@@ -3557,6 +3632,31 @@ void dplan_shape(const thb_dplan* p, uint32_t hd, AttnPlan& a) {
     a.merge_off = p->merge_off;
 }
 
+// The checks of a launch over a built device plan.
+int dplan_call_check(const thb_pool* pool, uint32_t layer, const void* q, const void* y, const thb_dplan* plan) {
+    if (!pool || !plan) return fail(THB_ERR_INVALID, "null pool or plan");
+    if (plan->pool != pool) return fail(THB_ERR_INVALID, "the plan belongs to another pool");
+    if (!plan->built) return fail(THB_ERR_INVALID, "the plan has not been built (thb_dplan_build)");
+    if (layer >= pool->layers)
+        return fail(THB_ERR_INVALID, "layer " + std::to_string(layer) + " out of range (" +
+                                         std::to_string(pool->layers) + " layers)");
+    if (!q || !y) return fail(THB_ERR_INVALID, "null q or y");
+    if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u))
+        return fail(THB_ERR_INVALID, "q and y must be 16-byte aligned");
+    return THB_OK;
+}
+
+// Attention over a fixed-grid device plan, with the append inside the
+// launch when io carries sources.
+void dplan_launch_grid(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const thb_dplan* plan, hipStream_t s) {
+    AttnPlan shape;
+    dplan_shape(plan, pool->geom[layer].head_dim, shape);
+    const uint32_t* meta = plan->rows->dev + 8 * static_cast<size_t>(plan->spec.row_off);
+    launch_plan(pool, layer, io, plan->spec, shape, io.k_src_dev != nullptr, meta,
+                static_cast<const uint32_t*>(plan->blob.get()), static_cast<uint8_t*>(plan->part.get()),
+                static_cast<uint32_t*>(plan->cnt.get()), s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -3568,8 +3668,11 @@ int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan
 int thb_dplan_create_ex(thb_pool* pool, uint32_t max_m, uint32_t q_heads, uint32_t flags, thb_dplan** out) {
     if (!pool || !out) return fail(THB_ERR_INVALID, "null pool or out");
     *out = nullptr;
-    if (flags & ~THB_DPLAN_PREFILL) return fail(THB_ERR_INVALID, "unknown dplan flags " + std::to_string(flags));
+    if (flags & ~(THB_DPLAN_PREFILL | THB_DPLAN_APPEND))
+        return fail(THB_ERR_INVALID, "unknown dplan flags " + std::to_string(flags));
     const bool list = (flags & THB_DPLAN_PREFILL) != 0;
+    if (list && (flags & THB_DPLAN_APPEND))
+        return fail(THB_ERR_INVALID, "THB_DPLAN_APPEND takes the fixed-grid plan (without THB_DPLAN_PREFILL)");
     const uint32_t max_rows = list ? kDPlanListMaxRows : kDPlanMaxRows;
     if (max_m == 0 || max_m > max_rows)
         return fail(THB_ERR_INVALID, "device-planned calls take 1 to " + std::to_string(max_rows) + " rows, not " +
@@ -3584,6 +3687,7 @@ int thb_dplan_create_ex(thb_pool* pool, uint32_t max_m, uint32_t q_heads, uint32
         p->pool = pool;
         p->max_m = max_m;
         p->q_heads = q_heads;
+        p->append = (flags & THB_DPLAN_APPEND) != 0;
         const uint32_t G = q_heads / pool->kv_heads;
         p->gmax = G <= kCols ? max_m : max_m * ((G + kCols - 1) / kCols);
         // Partitions of the longest key range any sequence of the pool allows
@@ -3643,6 +3747,9 @@ int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* 
     if (!(spec->softcap >= 0.0f)) return fail(THB_ERR_INVALID, "softcap must be >= 0");
     if (spec->q_dtype > THB_DT_BF16 || spec->y_dtype > THB_DT_BF16)
         return fail(THB_ERR_INVALID, "q_dtype and y_dtype must be THB_DT_F32, THB_DT_F16 or THB_DT_BF16");
+    if (plan->append && !spec->causal)
+        return fail(THB_ERR_INVALID, "a plan made with THB_DPLAN_APPEND takes causal calls only (the append runs "
+                                     "inside the attention launch)");
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);  // queued page-API calls first: the plan reads the page counts
@@ -3700,6 +3807,7 @@ int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* 
         a.items_off = plan->items_off;
         a.ranges_off = plan->ranges_off;
         a.merge_off = plan->merge_off;
+        a.append = plan->append ? 1u : 0u;
         hipLaunchKernelGGL(dplan_kernel, dim3(1), dim3(kDPlanThreads), 0, s, a);
         THB_HIP(hipGetLastError());
         plan->spec = *spec;
@@ -3710,15 +3818,7 @@ int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* 
 }
 
 int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q, void* y, const thb_dplan* plan, void* stream) {
-    if (!pool || !plan) return fail(THB_ERR_INVALID, "null pool or plan");
-    if (plan->pool != pool) return fail(THB_ERR_INVALID, "the plan belongs to another pool");
-    if (!plan->built) return fail(THB_ERR_INVALID, "the plan has not been built (thb_dplan_build)");
-    if (layer >= pool->layers)
-        return fail(THB_ERR_INVALID, "layer " + std::to_string(layer) + " out of range (" +
-                                         std::to_string(pool->layers) + " layers)");
-    if (!q || !y) return fail(THB_ERR_INVALID, "null q or y");
-    if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u))
-        return fail(THB_ERR_INVALID, "q and y must be 16-byte aligned");
+    if (int rc = dplan_call_check(pool, layer, q, y, plan)) return rc;
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
@@ -3751,12 +3851,23 @@ int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q, void* y, const
             THB_HIP(hipGetLastError());
             return THB_OK;
         }
-        AttnPlan shape;
-        dplan_shape(plan, hd, shape);
-        const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
-        const uint32_t* meta = plan->rows->dev + 8 * static_cast<size_t>(plan->spec.row_off);
-        launch_plan(pool, layer, io, plan->spec, shape, false, meta, static_cast<const uint32_t*>(plan->blob.get()),
-                    static_cast<uint8_t*>(plan->part.get()), static_cast<uint32_t*>(plan->cnt.get()), s);
+        dplan_launch_grid(pool, layer, make_io(q, y, nullptr, nullptr, 0, nullptr), plan, s);
+        return THB_OK;
+    });
+}
+
+int thb_attn_append_dplan(thb_pool* pool, uint32_t layer, const void* k_src, const void* v_src, uint32_t src_dtype,
+                          const void* q, void* y, const thb_dplan* plan, void* stream) {
+    if (int rc = dplan_call_check(pool, layer, q, y, plan)) return rc;
+    if (!plan->append) return fail(THB_ERR_INVALID, "the plan was not made with THB_DPLAN_APPEND");
+    if (!k_src || !v_src) return fail(THB_ERR_INVALID, "null source buffer");
+    if (src_dtype > THB_DT_BF16) return fail(THB_ERR_INVALID, "unknown src_dtype " + std::to_string(src_dtype));
+    if ((reinterpret_cast<uintptr_t>(k_src) & 15u) || (reinterpret_cast<uintptr_t>(v_src) & 15u))
+        return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        dplan_launch_grid(pool, layer, make_io(q, y, k_src, v_src, src_dtype, nullptr), plan, s);
         return THB_OK;
     });
 }

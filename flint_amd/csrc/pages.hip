@@ -43,7 +43,8 @@ enum : uint32_t {
     kStForkCover = 4,
     kStBadSeq = kPageStBadSeq,
     kStCover = kPageStCover,
-    kStDupSeq = 7
+    kStDupSeq = 7,
+    kStNoFuse = kPageStNoFuse
 };
 enum : uint32_t {
     kHdrTop = 0,
@@ -565,6 +566,17 @@ std::string status_message(const uint32_t* hdr) {
         case kStCover:
             return "pages must cover the chunk: sequence " + std::to_string(a) + " holds " + std::to_string(b) +
                    " slots, a row reads " + std::to_string(hdr[kHdrC]);
+        case kStNoFuse: {
+            const uint32_t why = hdr[kHdrC];
+            const char* reason = why == kNoFuseChunk   ? "its chunk holds more rows than one group"
+                                 : why == kNoFuseKeys  ? "its keys do not end at its new token (position + 1), or "
+                                                         "positions do not rise within its chunk"
+                                 : why == kNoFuseSeq   ? "its sequence is not the call's fixed sequence"
+                                 : why == kNoFuseTwice ? "its sequence heads an earlier chunk of the call too"
+                                                       : "unknown reason";
+            return "the append cannot run inside the attention launch: row " + std::to_string(a) + " (sequence " +
+                   std::to_string(b) + "): " + reason + "; nothing was appended";
+        }
         default: return "device page allocator status " + std::to_string(hdr[kHdrStatus]);
     }
 }
@@ -783,7 +795,9 @@ int thb_pool_status(thb_pool* pool, void* stream) {
         const std::string msg = status_message(h.data());
         const uint32_t zero[4] = {0, 0, 0, 0};
         THB_HIP(hipMemcpy(pool->state_dev + kHdrStatus, zero, sizeof(zero), hipMemcpyHostToDevice));
-        return fail(h[kHdrStatus] == kStBadSeq || h[kHdrStatus] == kStDupSeq ? THB_ERR_INVALID : THB_ERR_MODEL, msg);
+        const uint32_t code = h[kHdrStatus];
+        return fail(code == kStBadSeq || code == kStDupSeq || code == kStNoFuse ? THB_ERR_INVALID : THB_ERR_MODEL,
+                    msg);
     });
 }
 

@@ -54,11 +54,15 @@ enum : uint32_t { kPageOpAlloc = 1, kPageOpFree = 2, kPageOpTruncate = 3, kPageO
 // Device allocator header: the status word (first failure since the last
 // thb_pool_status, then 3 arguments), and the status a device-planned
 // attention call records for a row its sequence's pages do not cover
-// (arguments: sequence, slots held, keys the row reads).
+// (arguments: sequence, slots held, keys the row reads) or for a call whose
+// append cannot run inside its attention launch (arguments: row, sequence,
+// reason kNoFuse*).
 constexpr uint32_t kPageHdrStatus = 1;
 constexpr uint32_t kPageHdrCopies = 5;  // copy-on-write copies in the device list
 constexpr uint32_t kPageStBadSeq = 5;
 constexpr uint32_t kPageStCover = 6;
+constexpr uint32_t kPageStNoFuse = 8;
+enum : uint32_t { kNoFuseChunk = 1, kNoFuseKeys = 2, kNoFuseSeq = 3, kNoFuseTwice = 4 };
 
 // A page-API call queued for the device allocator (pages.hip): it has run on
 // the host mirror and runs on the device before the pool's next kernel.

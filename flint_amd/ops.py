@@ -167,14 +167,18 @@ class DevicePlan:
     attention of one layer over the plan.  Each (group, partition) computes
     what ``attn`` computes, bit for bit; in a work-list plan (prefill=True) a
     prefill block whose keys span several partitions runs as decode groups,
-    whose sums are ordered differently from ``attn``'s."""
+    whose sums are ordered differently from ``attn``'s.  ``attn_append``
+    (append=True) is ``kv_store_attn`` over the plan, in one launch."""
 
-    def __init__(self, kv: KvPool, max_m: int, q_heads: int, prefill: bool = False):
+    def __init__(self, kv: KvPool, max_m: int, q_heads: int, prefill: bool = False, append: bool = False):
         """prefill=True: a work-list plan (thb_dplan_create_ex with
         THB_DPLAN_PREFILL) that also runs prefill chunks on the prefill
-        kernel."""
+        kernel.  append=True (THB_DPLAN_APPEND, fixed-grid plans): each build
+        also checks on the device that the call's append can run inside the
+        attention launch, for ``attn_append``."""
         h = ctypes.c_void_p()
-        check(lib().thb_dplan_create_ex(kv.handle, max_m, q_heads, 1 if prefill else 0, ctypes.byref(h)))
+        flags = (1 if prefill else 0) | (2 if append else 0)
+        check(lib().thb_dplan_create_ex(kv.handle, max_m, q_heads, flags, ctypes.byref(h)))
         self._h = h.value
         self.kv, self.max_m, self.q_heads = kv, max_m, q_heads
         self.spec = None
@@ -194,6 +198,19 @@ class DevicePlan:
         _buf("y", y, n, (self._dt[1],))
         check(lib().thb_attn_dplan(self.kv.handle, layer, _addr("q", q), _addr("y", y), self._h,
                                    _stream_ptr(stream)))
+
+    def attn_append(self, layer: int, k_src, v_src, q, y, stream=None) -> None:
+        """thb_attn_append_dplan: the plan's rows of k_src / v_src appended
+        and attention run in one launch, bit-identical to ``kv_store_attn``."""
+        if self.spec is None:
+            raise ThubanError(_lib.THB_ERR_INVALID, "the plan has not been built")
+        _src_bufs(self.kv, layer, self.spec.m, k_src, v_src)
+        n = self.spec.m * self.spec.q_heads * _head_dim(self.kv, layer)
+        _buf("q", q, n, (self._dt[0],))
+        _buf("y", y, n, (self._dt[1],))
+        check(lib().thb_attn_append_dplan(self.kv.handle, layer, _addr("k_src", k_src), _addr("v_src", v_src),
+                                          _dtype_code(getattr(k_src, "dtype", None)), _addr("q", q), _addr("y", y),
+                                          self._h, _stream_ptr(stream)))
 
     def close(self) -> None:
         if self._h:

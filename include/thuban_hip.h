@@ -465,11 +465,30 @@ int thb_dplan_create(thb_pool* pool, uint32_t max_m, uint32_t q_heads, thb_dplan
  * runs the prefill kernel and a merge, so its rows differ from thb_attn's
  * in the order of the sums only (within 1e-5 on the tested cases). */
 #define THB_DPLAN_PREFILL 1u
+/* THB_DPLAN_APPEND (fixed-grid plans only; causal calls) makes the plan
+ * serve thb_attn_append_dplan as well: each thb_dplan_build also checks, on
+ * the device, the conditions under which thb_attn_append appends inside its
+ * attention launch (each chunk fits one group, every row's keys end at its
+ * new token with positions rising in the chunk, every row in the fixed
+ * sequence when spec.seq is fixed, no sequence heading two chunks).  A call
+ * that fails them is not planned at all: thb_pool_status reports the first
+ * failing row ("the append cannot run inside the attention launch: ..."),
+ * the launch appends nothing and every output is NaN. */
+#define THB_DPLAN_APPEND 2u
 int thb_dplan_create_ex(thb_pool* pool, uint32_t max_m, uint32_t q_heads, uint32_t flags, thb_dplan** out);
 void thb_dplan_destroy(thb_dplan* plan);
 int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* rows, void* stream);
 int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_dev, const thb_dplan* plan,
                    void* stream);
+/* No reference counterpart: kv_store then attention of a decode step
+ * (transformer/forward.rs:300-336, as thb_attn_append) over a plan made with
+ * THB_DPLAN_APPEND, in one launch: the workgroup whose keys hold a row's new
+ * token stores the row's K and V (rows [0, m) of k_src_dev / v_src_dev,
+ * [m, kv_heads, head_dim] in src_dtype, as thb_kv_store) before reading
+ * them.  Outputs and pool bytes equal thb_attn_append's bit for bit; it can
+ * be captured with thb_dplan_build, so a replayed step is two launches. */
+int thb_attn_append_dplan(thb_pool* pool, uint32_t layer, const void* k_src_dev, const void* v_src_dev,
+                          uint32_t src_dtype, const void* q_dev, void* y_dev, const thb_dplan* plan, void* stream);
 
 /* No reference counterpart.  Copies tokens [t0, t0 + n) of seq, layer
  * `layer`, into contiguous k_dst/v_dst [kv_heads, n, head_dim] in the KV type
