@@ -176,6 +176,8 @@ SIGNATURES = [
     ("thb_dplan_build", _int, [_vp, ctypes.POINTER(AttnSpecC), _vp, _vp]),
     ("thb_attn_dplan", _int, [_vp, _u32, _vp, _vp, _vp, _vp]),
     ("thb_attn_append_dplan", _int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
+    ("thb_dplan_set_pos_limit", _int, [_vp, _u32]),
+    ("thb_attn_step_dplan", _int, [_vp, _u32, ctypes.POINTER(AttnIoC), _vp, _vp]),
     ("thb_kv_gather", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_scatter", _int, [_vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     ("thb_kv_gather_batch", _int, [_vp, ctypes.POINTER(KvRangeC), _u32, _vp, _vp, _vp]),

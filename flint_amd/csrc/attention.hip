@@ -1949,7 +1949,8 @@ struct DPlanArgs {
     uint32_t npages_off;
     uint32_t m, seq_fixed, causal, window, G, PL, align, pmax, gmax, page_shift, seqs;
     uint32_t items_off, ranges_off, merge_off;
-    uint32_t append;  // the plan serves thb_attn_append_dplan: check that the append can run in the launch
+    uint32_t append;     // the plan serves thb_attn_append_dplan: check that the append can run in the launch
+    uint32_t pos_limit;  // rows at or past it read nothing (0: none)
 };
 
 // build_plan's partition of a key range [lo, hi) (lo = hi = 0 when empty).
@@ -2006,12 +2007,15 @@ __device__ void dplan_fail(uint32_t* hdr, uint32_t code, uint32_t x, uint32_t y,
 // sequence; one chunk with a fixed seq) into s_ck (chunk of each row) and
 // s_cs (first row of each chunk, then m; *n_chunks), then each row's key
 // range (plan_rows) into s_lo / s_hi and ranges_out; a row its pages do
-// not cover reads nothing and is reported in the allocator's status word.
+// not cover, or whose position is not below pos_limit (the rope tables'
+// rows, when set), reads nothing and is reported in the allocator's status
+// word.
 struct DPlanRows {
     const uint32_t* meta;
     uint32_t* ranges_out;
     uint32_t* state;
     uint32_t npages_off, m, seq_fixed, causal, window, page_shift, seqs;
+    uint32_t pos_limit;  // 0: none
 };
 
 __device__ void dplan_rows(const DPlanRows& a, uint32_t* s_ck, uint32_t* s_cs, uint32_t* s_lo, uint32_t* s_hi,
@@ -2049,7 +2053,10 @@ __device__ void dplan_rows(const DPlanRows& a, uint32_t* s_ck, uint32_t* s_cs, u
         uint64_t h = kv_len;
         if (a.causal && uint64_t(pos) + 1 < h) h = uint64_t(pos) + 1;
         uint32_t lo = static_cast<uint32_t>(ws), hi = static_cast<uint32_t>(min(h, uint64_t(0xFFFFFFFFu)));
-        if (hi > lo) {
+        if (a.pos_limit != 0 && pos >= a.pos_limit) {
+            dplan_fail(a.state, kPageStPosLimit, pos, a.pos_limit, 0u);
+            lo = hi = 0;
+        } else if (hi > lo) {
             const uint32_t seq = seq_of(r);
             if (seq >= a.seqs) {
                 dplan_fail(a.state, kPageStBadSeq, seq, a.seqs, 0u);
@@ -2160,6 +2167,7 @@ __global__ __launch_bounds__(kDPlanThreads) void dplan_kernel(DPlanArgs a) {
         ra.window = a.window;
         ra.page_shift = a.page_shift;
         ra.seqs = a.seqs;
+        ra.pos_limit = a.pos_limit;
         dplan_rows(ra, s_ck, s_cs, s_lo, s_hi, s_red, s_carry);
     }
     if (a.append) dplan_check_fused(a, s_ck, s_cs, s_lo, s_hi);
@@ -2427,6 +2435,10 @@ __global__ __launch_bounds__(kDPlanThreads) void dplan_list_kernel(DListArgs a) 
             if (a.rows.causal && uint64_t(pos) + 1 < h) h = uint64_t(pos) + 1;
             lo[k] = static_cast<uint32_t>(ws);
             hi[k] = static_cast<uint32_t>(min(h, uint64_t(0xFFFFFFFFu)));
+            if (a.rows.pos_limit != 0 && pos >= a.rows.pos_limit) {
+                dplan_fail(a.rows.state, kPageStPosLimit, pos, a.rows.pos_limit, 0u);
+                lo[k] = hi[k] = 0;
+            }
             const uint32_t sq = s_seq[r];
             if (hi[k] > lo[k] && sq < a.rows.seqs) np_seq[k] = npages[sq];
         }
@@ -3587,6 +3599,7 @@ struct thb_dplan {
     // pairs | order].
     bool list = false;
     bool append = false;  // THB_DPLAN_APPEND: each build checks that the append can run in the launch
+    uint32_t pos_limit = 0;  // thb_dplan_set_pos_limit: rows at or past it are reported and read nothing
     uint32_t imax = 0, bmax = 0, wb = 0;
     uint32_t groups_off = 0, bitems_off = 0, pairs_off = 0, order_off = 0;
     bool built = false;
@@ -3644,6 +3657,33 @@ int dplan_call_check(const thb_pool* pool, uint32_t layer, const void* q, const 
     if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u))
         return fail(THB_ERR_INVALID, "q and y must be 16-byte aligned");
     return THB_OK;
+}
+
+// Attention over a work-list device plan: one workgroup per CU claiming the
+// list's entries (decode items with in-launch merges, prefill blocks).
+void dplan_launch_list(thb_pool* pool, uint32_t layer, const thb_attn_io& io, const thb_dplan* plan, hipStream_t s) {
+    const uint32_t* blob = static_cast<const uint32_t*>(plan->blob.get());
+    AttnArgs a;
+    fill_args(pool, layer, io, plan->spec, plan->rows->dev + 8 * static_cast<size_t>(plan->spec.row_off), a);
+    a.groups = blob + plan->groups_off;
+    a.items = blob + plan->items_off;
+    a.ranges = blob + plan->ranges_off;
+    a.bitems = blob + plan->bitems_off;
+    a.bpairs = blob + plan->pairs_off;
+    a.order = blob + plan->order_off;
+    a.merge_groups = blob + plan->merge_off;
+    a.list = const_cast<uint32_t*>(blob);
+    AttnPlan shape;
+    dplan_shape(plan, plan->hd_max, shape);
+    if (shape.split) {
+        uint64_t o_bytes = 0;
+        partial_bytes(pool, shape, &o_bytes);
+        a.part_o = reinterpret_cast<float*>(plan->part.get());
+        a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(plan->part.get()) + o_bytes);
+        a.merge_cnt = static_cast<uint32_t*>(plan->cnt.get());
+    }
+    launch_list(template_hd(pool->geom[layer].head_dim), pool->kv_dtype == THB_KV_F16_RNE, dim3(pool->cus), a, s);
+    THB_HIP(hipGetLastError());
 }
 
 // Attention over a fixed-grid device plan, with the append inside the
@@ -3765,6 +3805,7 @@ int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* 
             la.rows.window = spec->window;
             la.rows.page_shift = pool->page_shift;
             la.rows.seqs = pool->arena.a.seqs();
+            la.rows.pos_limit = plan->pos_limit;
             la.blob = static_cast<uint32_t*>(plan->blob.get());
             la.G = spec->q_heads / pool->kv_heads;
             la.PL = pool->part_len;
@@ -3808,6 +3849,7 @@ int thb_dplan_build(thb_dplan* plan, const thb_attn_spec* spec, const thb_rows* 
         a.ranges_off = plan->ranges_off;
         a.merge_off = plan->merge_off;
         a.append = plan->append ? 1u : 0u;
+        a.pos_limit = plan->pos_limit;
         hipLaunchKernelGGL(dplan_kernel, dim3(1), dim3(kDPlanThreads), 0, s, a);
         THB_HIP(hipGetLastError());
         plan->spec = *spec;
@@ -3822,36 +3864,11 @@ int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q, void* y, const
     return guarded([&]() -> int {
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
-        const uint32_t hd = pool->geom[layer].head_dim;
-        if (plan->list) {
-            // The work list over one workgroup per CU: attn_list claims its
-            // entries (decode items with in-launch merges, prefill blocks).
-            const uint32_t* blob = static_cast<const uint32_t*>(plan->blob.get());
-            const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
-            AttnArgs a;
-            fill_args(pool, layer, io, plan->spec, plan->rows->dev + 8 * static_cast<size_t>(plan->spec.row_off), a);
-            a.groups = blob + plan->groups_off;
-            a.items = blob + plan->items_off;
-            a.ranges = blob + plan->ranges_off;
-            a.bitems = blob + plan->bitems_off;
-            a.bpairs = blob + plan->pairs_off;
-            a.order = blob + plan->order_off;
-            a.merge_groups = blob + plan->merge_off;
-            a.list = const_cast<uint32_t*>(blob);
-            AttnPlan shape;
-            dplan_shape(plan, plan->hd_max, shape);
-            if (shape.split) {
-                uint64_t o_bytes = 0;
-                partial_bytes(pool, shape, &o_bytes);
-                a.part_o = reinterpret_cast<float*>(plan->part.get());
-                a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(plan->part.get()) + o_bytes);
-                a.merge_cnt = static_cast<uint32_t*>(plan->cnt.get());
-            }
-            launch_list(template_hd(hd), pool->kv_dtype == THB_KV_F16_RNE, dim3(pool->cus), a, s);
-            THB_HIP(hipGetLastError());
-            return THB_OK;
-        }
-        dplan_launch_grid(pool, layer, make_io(q, y, nullptr, nullptr, 0, nullptr), plan, s);
+        const thb_attn_io io = make_io(q, y, nullptr, nullptr, 0, nullptr);
+        if (plan->list)
+            dplan_launch_list(pool, layer, io, plan, s);
+        else
+            dplan_launch_grid(pool, layer, io, plan, s);
         return THB_OK;
     });
 }
@@ -3868,6 +3885,53 @@ int thb_attn_append_dplan(thb_pool* pool, uint32_t layer, const void* k_src, con
         hipStream_t s = as_stream(stream);
         pool_flush(pool, s);
         dplan_launch_grid(pool, layer, make_io(q, y, k_src, v_src, src_dtype, nullptr), plan, s);
+        return THB_OK;
+    });
+}
+
+int thb_dplan_set_pos_limit(thb_dplan* plan, uint32_t max_pos) {
+    if (!plan) return fail(THB_ERR_INVALID, "null plan");
+    plan->pos_limit = max_pos;
+    plan->built = false;  // the limit is checked by the next build
+    return THB_OK;
+}
+
+int thb_attn_step_dplan(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_dplan* plan, void* stream) {
+    if (!io) return fail(THB_ERR_INVALID, "null io");
+    if (int rc = dplan_call_check(pool, layer, io->q_dev, io->y_dev, plan)) return rc;
+    const uint32_t hd = pool->geom[layer].head_dim;
+    const uint32_t qes = plan->spec.q_dtype == THB_DT_F32 ? 4u : 2u;
+    if (io->q_stride && (io->q_stride < hd || (io->q_stride * qes) % 16 != 0))
+        return fail(THB_ERR_INVALID, "q_stride " + std::to_string(io->q_stride) +
+                                         " must be 0 or at least head_dim, and a multiple of 16 bytes");
+    if (io->gate_dev && io->gate_stride && io->gate_stride < hd)
+        return fail(THB_ERR_INVALID, "gate_stride " + std::to_string(io->gate_stride) + " below head_dim");
+    if (const thb_rope* rope = io->rope) {
+        if (int rc = check_rope_tables(rope, hd)) return rc;
+        if (plan->pos_limit == 0 || plan->pos_limit > rope->max_pos)
+            return fail(THB_ERR_INVALID, "rotary embedding over a device plan needs the plan's position limit "
+                                         "(thb_dplan_set_pos_limit, then thb_dplan_build) at most the tables' " +
+                                             std::to_string(rope->max_pos) + " positions; the plan has " +
+                                             std::to_string(plan->pos_limit));
+    }
+    const bool append = io->k_src_dev || io->v_src_dev;
+    if (append) {
+        if (!plan->append) return fail(THB_ERR_INVALID, "the plan was not made with THB_DPLAN_APPEND");
+        if (!io->k_src_dev || !io->v_src_dev) return fail(THB_ERR_INVALID, "null source buffer");
+        if (io->src_dtype > THB_DT_BF16)
+            return fail(THB_ERR_INVALID, "unknown src_dtype " + std::to_string(io->src_dtype));
+        if (io->rope && io->src_dtype == THB_DT_BF16)
+            return fail(THB_ERR_INVALID, "rotary append takes f32 or f16 sources (src_dtype 2)");
+        if ((reinterpret_cast<uintptr_t>(io->k_src_dev) & 15u) || (reinterpret_cast<uintptr_t>(io->v_src_dev) & 15u))
+            return fail(THB_ERR_INVALID, "source buffers must be 16-byte aligned");
+    }
+    return guarded([&]() -> int {
+        hipStream_t s = as_stream(stream);
+        pool_flush(pool, s);
+        if (plan->list)
+            dplan_launch_list(pool, layer, *io, plan, s);
+        else
+            dplan_launch_grid(pool, layer, *io, plan, s);
         return THB_OK;
     });
 }

@@ -760,7 +760,7 @@ void launch_store_rope(uint32_t kv, dim3 grid, const RopeStoreArgs& a, hipStream
 
 }  // namespace
 
-int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint32_t row_off, uint32_t m) {
+int check_rope_tables(const thb_rope* r, uint32_t head_dim) {
     if (!r || !r->cos_dev || !r->sin_dev) return fail(THB_ERR_INVALID, "null rope tables");
     if (r->rot == 0 || r->rot % 16 != 0 || r->rot > head_dim)
         return fail(THB_ERR_CONFIG, "rope rot " + std::to_string(r->rot) +
@@ -768,6 +768,11 @@ int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint3
                                         std::to_string(head_dim));
     if (!aligned16(r->cos_dev) || !aligned16(r->sin_dev) || !aligned16(r->q_norm_dev) || !aligned16(r->k_norm_dev))
         return fail(THB_ERR_INVALID, "rope tables and norm weights must be 16-byte aligned");
+    return THB_OK;
+}
+
+int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint32_t row_off, uint32_t m) {
+    if (int rc = check_rope_tables(r, head_dim)) return rc;
     if (static_cast<uint64_t>(row_off) + m > rows->m)
         return fail(THB_ERR_INVALID, "row meta holds " + std::to_string(rows->m) + " rows, call needs " +
                                          std::to_string(static_cast<uint64_t>(row_off) + m));

@@ -44,7 +44,8 @@ enum : uint32_t {
     kStBadSeq = kPageStBadSeq,
     kStCover = kPageStCover,
     kStDupSeq = 7,
-    kStNoFuse = kPageStNoFuse
+    kStNoFuse = kPageStNoFuse,
+    kStPosLimit = kPageStPosLimit
 };
 enum : uint32_t {
     kHdrTop = 0,
@@ -566,6 +567,9 @@ std::string status_message(const uint32_t* hdr) {
         case kStCover:
             return "pages must cover the chunk: sequence " + std::to_string(a) + " holds " + std::to_string(b) +
                    " slots, a row reads " + std::to_string(hdr[kHdrC]);
+        case kStPosLimit:
+            return "row position " + std::to_string(a) + " outside the rope tables (" + std::to_string(b) +
+                   " positions)";
         case kStNoFuse: {
             const uint32_t why = hdr[kHdrC];
             const char* reason = why == kNoFuseChunk   ? "its chunk holds more rows than one group"

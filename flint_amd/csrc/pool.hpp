@@ -54,14 +54,16 @@ enum : uint32_t { kPageOpAlloc = 1, kPageOpFree = 2, kPageOpTruncate = 3, kPageO
 // Device allocator header: the status word (first failure since the last
 // thb_pool_status, then 3 arguments), and the status a device-planned
 // attention call records for a row its sequence's pages do not cover
-// (arguments: sequence, slots held, keys the row reads) or for a call whose
+// (arguments: sequence, slots held, keys the row reads), for a call whose
 // append cannot run inside its attention launch (arguments: row, sequence,
-// reason kNoFuse*).
+// reason kNoFuse*) and for a row past the plan's position limit (arguments:
+// position, limit).
 constexpr uint32_t kPageHdrStatus = 1;
 constexpr uint32_t kPageHdrCopies = 5;  // copy-on-write copies in the device list
 constexpr uint32_t kPageStBadSeq = 5;
 constexpr uint32_t kPageStCover = 6;
 constexpr uint32_t kPageStNoFuse = 8;
+constexpr uint32_t kPageStPosLimit = 9;
 enum : uint32_t { kNoFuseChunk = 1, kNoFuseKeys = 2, kNoFuseSeq = 3, kNoFuseTwice = 4 };
 
 // A page-API call queued for the device allocator (pages.hip): it has run on
@@ -154,6 +156,8 @@ void launch_block_copy_counted(thb_pool* p, const uint32_t* triples_dev, const u
 int sync_mirror(thb_pool* p, hipStream_t stream);
 // Validates a thb_rope for rows [row_off, row_off + m) of head_dim vectors.
 int check_rope(const thb_rope* r, uint32_t head_dim, const thb_rows* rows, uint32_t row_off, uint32_t m);
+// The checks of check_rope that do not read positions (tables, rot, alignment).
+int check_rope_tables(const thb_rope* r, uint32_t head_dim);
 // Launches the block-copy kernel for n non-chaining host triples (passed in
 // the kernel arguments when few, else uploaded through the stager).
 void launch_block_copy(thb_pool* p, const uint32_t* triples, uint32_t n, uint32_t max_tokens, hipStream_t stream);

@@ -15,11 +15,12 @@ struct RopeDev {
     const float* w;    // RMSNorm weight [head_dim], or null: rotation only
     uint32_t rot, half;
     float eps;
+    uint32_t max_pos;  // table rows (> 0)
 };
 
 // The query (or key) view of a validated thb_rope.
 inline RopeDev rope_dev(const thb_rope& r, bool query) {
-    return RopeDev{r.cos_dev, r.sin_dev, query ? r.q_norm_dev : r.k_norm_dev, r.rot, r.rot / 2, r.eps};
+    return RopeDev{r.cos_dev, r.sin_dev, query ? r.q_norm_dev : r.k_norm_dev, r.rot, r.rot / 2, r.eps, r.max_pos};
 }
 
 // x c - y s (the first half of the rotated dims).
@@ -60,10 +61,14 @@ __device__ inline void norm8(float (&x)[8], float inv, const float* w) {
 }
 
 // Rotates the 8 elements x of dims [d0, d0 + 8) given their partners y
-// (dims d0 +- half), at position pos.  d0 < rot, d0 % 8 == 0.
+// (dims d0 +- half), at position pos.  d0 < rot, d0 % 8 == 0.  A position
+// past the tables reads their last row: host calls refuse such rows, and
+// a device-planned call gives them no keys (a NaN output) and reports them,
+// so the clamp only keeps the read inside the tables.
 __device__ inline void rotate8(float (&x)[8], const float (&y)[8], uint32_t d0, uint32_t pos, const RopeDev& r) {
     const bool lo = d0 < r.half;
-    const uint64_t t = static_cast<uint64_t>(pos) * r.half + (lo ? d0 : d0 - r.half);
+    const uint32_t p = pos < r.max_pos ? pos : r.max_pos - 1u;
+    const uint64_t t = static_cast<uint64_t>(p) * r.half + (lo ? d0 : d0 - r.half);
     const f32x4 c0 = *reinterpret_cast<const f32x4*>(r.cos + t), c1 = *reinterpret_cast<const f32x4*>(r.cos + t + 4);
     const f32x4 s0 = *reinterpret_cast<const f32x4*>(r.sin + t), s1 = *reinterpret_cast<const f32x4*>(r.sin + t + 4);
 #pragma unroll

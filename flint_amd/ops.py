@@ -212,6 +212,26 @@ class DevicePlan:
                                           _dtype_code(getattr(k_src, "dtype", None)), _addr("q", q), _addr("y", y),
                                           self._h, _stream_ptr(stream)))
 
+    def set_pos_limit(self, max_pos: int) -> None:
+        """thb_dplan_set_pos_limit: later builds report rows at or past
+        max_pos (the rope tables' rows) and give them no keys; needed by
+        ``step`` with a rope.  Build again before the next launch."""
+        check(lib().thb_dplan_set_pos_limit(self._h, max_pos))
+        self.spec = None
+
+    def step(self, layer: int, q, y, q_stride: int = 0, gate=None, gate_stride: int = 0, k_src=None, v_src=None,
+             rope=None, stream=None) -> None:
+        """thb_attn_step_dplan: ``attn_step``'s extensions over the plan
+        (k_src / v_src appended inside the launch need append=True)."""
+        if self.spec is None:
+            raise ThubanError(_lib.THB_ERR_INVALID, "the plan has not been built")
+        for name, x, dt in (("q", q, self._dt[0]), ("y", y, self._dt[1])):
+            if not isinstance(x, int) and _dtype_name(x) != dt:
+                raise ThubanError(_lib.THB_ERR_INVALID, f"{name}: dtype {_dtype_name(x)} is not the plan's {dt}")
+        io = _attn_io(self.kv, layer, self.spec.m, self.spec.q_heads, q, y, q_stride, gate, gate_stride, k_src, v_src,
+                      rope)
+        check(lib().thb_attn_step_dplan(self.kv.handle, layer, ctypes.byref(io), self._h, _stream_ptr(stream)))
+
     def close(self) -> None:
         if self._h:
             lib().thb_dplan_destroy(self._h)
@@ -236,16 +256,11 @@ def kv_store_attn(k_src, v_src, q, kv: KvPool, layer: int, y, spec: AttnSpec, st
                                 ctypes.byref(c), spec.args.handle, _stream_ptr(stream)))
 
 
-def attn_step(kv: KvPool, layer: int, spec: AttnSpec, q, y, q_stride: int = 0, gate=None, gate_stride: int = 0,
-              k_src=None, v_src=None, rope=None, stream=None) -> None:
-    """thb_attn_step: attention with every extension of the C ABI's
-    thb_attn_io.  q heads are q_stride elements apart (0 = head_dim; pass
-    2 * head_dim and a view of a fused q|gate projection); gate, when given,
-    multiplies the output by sigmoid(gate) (qwen35/layers.rs:231-238); k_src
-    and v_src are appended first; rope (flint_amd.rope.Rope) rotates q and k.
-    q, gate and y are device tensors or raw device addresses."""
+def _attn_io(kv: KvPool, layer: int, m: int, q_heads: int, q, y, q_stride, gate, gate_stride, k_src, v_src,
+             rope) -> _lib.AttnIoC:
+    """The thb_attn_io of a call of m rows, its buffers checked."""
     hd = _head_dim(kv, layer)
-    heads = spec.m * spec.q_heads
+    heads = m * q_heads
     io = _lib.AttnIoC()
     q_ext = (heads - 1) * q_stride + hd if q_stride and heads else None
     _buf("q", q, heads * hd, _ACT, extent=q_ext)
@@ -254,7 +269,7 @@ def attn_step(kv: KvPool, layer: int, spec: AttnSpec, q, y, q_stride: int = 0, g
         g_ext = (heads - 1) * (gate_stride or hd) + hd if heads else 0
         _buf("gate", gate, heads * hd, _ACT, extent=g_ext if gate_stride else None)
     if k_src is not None:
-        _src_bufs(kv, layer, spec.m, k_src, v_src)
+        _src_bufs(kv, layer, m, k_src, v_src)
     io.q_dev, io.y_dev, io.q_stride = _addr("q", q), _addr("y", y), q_stride
     io.gate_dev = _addr("gate", gate) if gate is not None else None
     io.gate_stride = gate_stride
@@ -262,6 +277,18 @@ def attn_step(kv: KvPool, layer: int, spec: AttnSpec, q, y, q_stride: int = 0, g
         io.k_src_dev, io.v_src_dev = _addr("k_src", k_src), _addr("v_src", v_src)
         io.src_dtype = _dtype_code(getattr(k_src, "dtype", None))
     io.rope = ctypes.pointer(rope._c) if rope is not None else None
+    return io
+
+
+def attn_step(kv: KvPool, layer: int, spec: AttnSpec, q, y, q_stride: int = 0, gate=None, gate_stride: int = 0,
+              k_src=None, v_src=None, rope=None, stream=None) -> None:
+    """thb_attn_step: attention with every extension of the C ABI's
+    thb_attn_io.  q heads are q_stride elements apart (0 = head_dim; pass
+    2 * head_dim and a view of a fused q|gate projection); gate, when given,
+    multiplies the output by sigmoid(gate) (qwen35/layers.rs:231-238); k_src
+    and v_src are appended first; rope (flint_amd.rope.Rope) rotates q and k.
+    q, gate and y are device tensors or raw device addresses."""
+    io = _attn_io(kv, layer, spec.m, spec.q_heads, q, y, q_stride, gate, gate_stride, k_src, v_src, rope)
     c = _spec_c(spec, q, y)
     check(lib().thb_attn_step(kv.handle, layer, ctypes.byref(io), ctypes.byref(c), spec.args.handle,
                               _stream_ptr(stream)))

@@ -489,6 +489,22 @@ int thb_attn_dplan(thb_pool* pool, uint32_t layer, const void* q_dev, void* y_de
  * be captured with thb_dplan_build, so a replayed step is two launches. */
 int thb_attn_append_dplan(thb_pool* pool, uint32_t layer, const void* k_src_dev, const void* v_src_dev,
                           uint32_t src_dtype, const void* q_dev, void* y_dev, const thb_dplan* plan, void* stream);
+/* No reference counterpart: the rotary tables' bound for device-planned
+ * calls (thb_rope.max_pos; 0 removes it).  Each later thb_dplan_build
+ * reports a row whose position is not below it ("row position P outside
+ * the rope tables (N positions)", thb_pool_status) and gives that row no
+ * keys (a NaN output; with THB_DPLAN_APPEND the whole call is planned
+ * empty).  The plan must be built again before its next launch. */
+int thb_dplan_set_pos_limit(thb_dplan* plan, uint32_t max_pos);
+/* No reference counterpart: thb_attn_step over a device plan, either form
+ * (ops::attn with the thb_attn_io extensions: query stride, sigmoid gate,
+ * rotary embedding with optional q/k norm, and with k_src/v_src the append
+ * inside the launch, which needs THB_DPLAN_APPEND).  io->rope needs a plan
+ * built with a position limit of at most io->rope->max_pos.  Outputs (and,
+ * with the append, pool bytes) equal thb_attn_step's bit for bit, the
+ * work-list form as thb_attn_dplan describes; it can be captured. */
+int thb_attn_step_dplan(thb_pool* pool, uint32_t layer, const thb_attn_io* io, const thb_dplan* plan,
+                        void* stream);
 
 /* No reference counterpart.  Copies tokens [t0, t0 + n) of seq, layer
  * `layer`, into contiguous k_dst/v_dst [kv_heads, n, head_dim] in the KV type
