@@ -399,11 +399,13 @@ def time_identity_leg(torch, ops, cfg, q, k_new, v_new, steps=5):
 
 def time_rope_step(torch, ops, pool, rows, positions, seqs, q, k_new, v_new, L, B, nq, hd, scale, steps=5):
     """The per-layer step with rotary embedding (Llama-3: theta 500000,
-    rot = head_dim) two ways: the reference's four launches (rope q, rope k,
-    kv_store, attn; transformer/forward.rs:265-336) and thb_attn_append_rope
-    (one launch).  Copies of q and k are rotated, so the main workload's
-    buffers stay as they were.  Events around `steps` passes over the
-    layers; returns us per layer for each."""
+    rot = head_dim) three ways: the reference's four launches (rope q, rope
+    k, kv_store, attn; transformer/forward.rs:265-336), thb_attn_append_rope
+    (one launch), and the step captured in a HIP graph over a device plan
+    (one thb_dplan_build per step, thb_attn_step_dplan with the rope and the
+    append per layer).  Copies of q and k are rotated, so the main
+    workload's buffers stay as they were.  Events around `steps` passes over
+    the layers; returns us per layer for each."""
     from flint_amd.rope import Rope, kv_store_attn_rope, rope_rows
 
     ctx = max(positions) + 1
@@ -424,8 +426,26 @@ def time_rope_step(torch, ops, pool, rows, positions, seqs, q, k_new, v_new, L, 
         for layer in range(L):
             kv_store_attn_rope(k_new[layer], v_new[layer], q[layer], pool, layer, y, spec, rope)
 
+    plan = ops.DevicePlan(pool, max_m=B, q_heads=nq, append=True)
+    plan.set_pos_limit(rope.max_pos)
+
+    def planned():
+        plan.build(spec, q[0], y)
+        for layer in range(L):
+            plan.step(layer, q[layer], y, k_src=k_new[layer], v_src=v_new[layer], rope=rope)
+
+    planned()  # outside the capture first: nothing left to set up
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            planned()
+    torch.cuda.current_stream().wait_stream(side)
+
     out = {}
-    for name, fn in (("unfused", unfused), ("fused", fused)):
+    for name, fn in (("unfused", unfused), ("fused", fused), ("graph", graph.replay)):
         fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -435,6 +455,9 @@ def time_rope_step(torch, ops, pool, rows, positions, seqs, q, k_new, v_new, L, 
         e1.record()
         torch.cuda.synchronize()
         out[name] = e0.elapsed_time(e1) / (steps * L) * 1e3
+    pool.status()  # every replay's plan checks passed
+    del graph
+    plan.close()
     return out
 
 
@@ -945,7 +968,7 @@ def main():
     step()  # re-append the unrotated keys: the pool and y agree again for the CPU baseline
     torch.cuda.synchronize()
     log(f"rope step: reference-shaped 4 launches {rope_us['unfused']:.1f} us/layer, "
-        f"fused {rope_us['fused']:.1f} us/layer")
+        f"fused {rope_us['fused']:.1f} us/layer, captured over a device plan {rope_us['graph']:.1f} us/layer")
     graph_us, graph_same = time_decode_graph(torch, ops, pool, spec, q, k_new, v_new, y, L, B, nq,
                                              max(2, min(args.steps, 10)))
     log(f"captured step: {graph_us:.2f} us/layer (eager {attn_us:.2f}), bit-identical {graph_same}")
@@ -1005,9 +1028,12 @@ def main():
                                  "device, one launch); us_per_layer includes the plan build's share"}
     out["rope"] = {"fused_us_per_layer": round(rope_us["fused"], 2),
                    "unfused_us_per_layer": round(rope_us["unfused"], 2),
+                   "graph_us_per_layer": round(rope_us["graph"], 2),
                    "fused_GBps": round(fused_bytes / (rope_us["fused"] * 1e-6) / 1e9, 1),
                    "note": "step with rotary embedding (theta 5e5, rot = head_dim): rope(q), rope(k), kv_store, "
-                           "attn as four launches vs thb_attn_append_rope as one"}
+                           "attn as four launches vs thb_attn_append_rope as one; graph: the step captured over a "
+                           "device plan (thb_dplan_build + thb_attn_step_dplan with the rope and the append per "
+                           "layer) and replayed"}
     ident_us = time_identity_leg(torch, ops, cfg, q, k_new, v_new)
     log(f"identity block tables: {ident_us:.2f} us/layer vs scattered {attn_us:.2f}")
     out["identity_vs_scattered"] = {
