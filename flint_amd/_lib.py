@@ -12,7 +12,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libthuban_hip.so")
 
-ABI_VERSION = 7  # THB_ABI_VERSION of include/thuban_hip.h
+ABI_VERSION = 8  # THB_ABI_VERSION of include/thuban_hip.h
 
 THB_OK = 0
 THB_ERR_MODEL = -1

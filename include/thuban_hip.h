@@ -15,10 +15,12 @@
  * :57-69), has one owner and is not thread-safe.
  *
  * HIP graph capture (no reference counterpart).  On a capturing stream:
- *  - thb_pool_alloc_rows, thb_kv_store, thb_dplan_build and thb_attn_dplan
- *    read everything a step changes (row meta, page counts, block table)
- *    from device memory, so a graph of them replays correctly while the
- *    rows move and pages are forked, truncated or freed between replays.
+ *  - thb_pool_alloc_rows, thb_kv_store, thb_dplan_build and the attention
+ *    calls over a device plan (thb_attn_dplan, thb_attn_append_dplan,
+ *    thb_attn_step_dplan) read everything a step changes (row meta, page
+ *    counts, block table) from device memory, so a graph of them replays
+ *    correctly while the rows move and pages are forked, truncated or freed
+ *    between replays.
  *    Once thb_pool_alloc_rows has been captured the pool is in graph mode
  *    for good: every later call that reads the host arena (page API,
  *    thb_attn, gather, ...) first waits for the device and reloads the host
@@ -29,7 +31,8 @@
  *    before its pool.  Such a replay is valid while what the call read on
  *    the host at capture time (positions, pages) still holds.
  *  - These refuse with THB_ERR_INVALID: thb_attn and its variants (host
- *    plans), thb_kv_store_rope and thb_rope_rows (host position checks),
+ *    plans; thb_attn_step_dplan is their capturable form), thb_kv_store_rope
+ *    and thb_rope_rows (host position checks),
  *    thb_pool_status / _read_state / _pull (they wait for the stream), any
  *    call while page-API calls queued on the host have not run (flush with
  *    thb_pool_sync before capturing), and any call that would have to grow
@@ -75,7 +78,7 @@ extern "C" {
 const char* thb_last_error(void);
 /* ABI revision of this header. */
 uint32_t thb_abi_version(void);
-#define THB_ABI_VERSION 7u
+#define THB_ABI_VERSION 8u
 
 /* head_dim guard, replaces ops::check_head_dim (ops/attn.rs:83-90) exactly:
  * THB_ERR_CONFIG "head_dim {hd} outside [64, 512]". */

@@ -37,7 +37,7 @@ def test_abi_version_and_struct_layouts(tmp_path):
 
     from flint_amd import _lib
 
-    assert _lib.lib().thb_abi_version() == _lib.ABI_VERSION == 7
+    assert _lib.lib().thb_abi_version() == _lib.ABI_VERSION == 8
     structs = {"thb_pool_desc": _lib.PoolDesc, "thb_attn_spec": _lib.AttnSpecC,
                "thb_layer_info": _lib.LayerInfo, "thb_arena_info": _lib.ArenaInfo, "thb_rope": _lib.RopeC,
                "thb_attn_io": _lib.AttnIoC}
