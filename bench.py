@@ -610,7 +610,10 @@ def measure_secondary(name, args):
         q = torch.randn(B, nq, hd, device=dev, generator=g)
         y = torch.empty_like(q)
         sp = spec(rows, nq, hd, B)
-        us = _time_steps(torch, lambda: ops.kv_store_attn(k, v, q, pool, 0, y, sp), args.steps, args.warmup)
+        # ~8 us steps issued from Python: at least 100 of them, so that a stall of the host
+        # thread does not dominate the average
+        us = _time_steps(torch, lambda: ops.kv_store_attn(k, v, q, pool, 0, y, sp), max(args.steps, 100),
+                         max(args.warmup, 10))
         byts = sum(c + 1 for c in ctx) * nkv * hd * 2 * 2
         # the same step as a serving loop replays it, captured once in a HIP graph (thb_attn plans
         # on the host and cannot be captured), 20 steps per graph: thb_dplan_build +
