@@ -168,7 +168,8 @@ class DevicePlan:
     what ``attn`` computes, bit for bit; in a work-list plan (prefill=True) a
     prefill block whose keys span several partitions runs as decode groups,
     whose sums are ordered differently from ``attn``'s.  ``attn_append``
-    (append=True) is ``kv_store_attn`` over the plan, in one launch."""
+    (append=True) is ``kv_store_attn`` over the plan, in one launch; ``step``
+    is ``attn_step`` over the plan (a rope needs ``set_pos_limit`` first)."""
 
     def __init__(self, kv: KvPool, max_m: int, q_heads: int, prefill: bool = False, append: bool = False):
         """prefill=True: a work-list plan (thb_dplan_create_ex with
