@@ -5,8 +5,10 @@ partitions), random contexts, 1-4 rows per sequence, a random window and
 soft-cap.  Checked against the CPU oracle (exact softmax in double, the
 reference's kv_len / window / causal rules of attn.wgsl:78-88,169), and
 bit for bit between the paths that must agree: the fused append
-(thb_attn_append) against kv_store followed by attn, the device-planned calls
-(thb_dplan_*: the fixed grid and the work list) and the no-allocation call
+(thb_attn_append) against kv_store followed by attn, the device-planned
+append (thb_attn_append_dplan) against both in outputs and pool bytes, the
+device-planned calls (thb_dplan_*: the fixed grid and the work list) and the
+no-allocation call
 (thb_attn_noalloc, whose split groups are combined by the merge kernel after
 the launch) against thb_attn (combined inside the launch).  A second set of
 seeded calls mixes decode rows with prefill chunks (random sizes and
@@ -67,7 +69,7 @@ def test_random_calls_agree(torch_cuda, seed):
     hd, nkv, nq, rps, pl = c["hd"], c["nkv"], c["nq"], c["rps"], c["pl"]
     budget = [n + rps for n in c["lens"]]
     pools = []
-    for _ in range(2):
+    for _ in range(3):
         P = make_pool(budget, kv_heads=nkv, head_dim=hd, page_len=pl, kv_dtype=c["kv"], extra_pages=3,
                       part_len=c["part_len"])
         scattered_alloc(P, budget, random.Random(seed), pl)
@@ -97,6 +99,18 @@ def test_random_calls_agree(torch_cuda, seed):
     ka, va = pools[0].read_layer(0)
     kb, vb = pools[1].read_layer(0)
     assert np.array_equal(ka, kb) and np.array_equal(va, vb), (seed, "appended pages")
+    # the same step over a device plan with the append inside the launch (one
+    # group per sequence, so the plan's checks pass)
+    ye = torch.full_like(q, 7.0)
+    aplan = ops.DevicePlan(pools[2], max_m=m, q_heads=nq, append=True)
+    aplan.build(spec, q, ye)
+    aplan.attn_append(0, k_new, v_new, q, ye)
+    torch.cuda.synchronize()
+    aplan.close()
+    pools[2].status()
+    assert torch.equal(ye, ya), (seed, "device-planned append", float((ye - ya).abs().max()))
+    kc, vc = pools[2].read_layer(0)
+    assert np.array_equal(ka, kc) and np.array_equal(va, vc), (seed, "device-planned appended pages")
 
     want = oracle_layer(torch, pools[0]).attn(q.cpu().numpy(), oracle.row_meta(positions, seqs), m, nq,
                                               1 / math.sqrt(hd), window=c["window"], softcap=c["cap"])
