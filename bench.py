@@ -135,6 +135,65 @@ def time_decode_graph(torch, ops, pool, spec, q, k_new, v_new, y_eager, L, B, nq
     return us, same
 
 
+def time_reference_mode(torch, ops, dev, B, ctx, nq, nkv, hd, layers=4, steps=5):
+    """The headline shape in the reference's compatibility mode: KV stored
+    as bf16 by truncation (kv_store.wgsl:20-22) in pages of 32 tokens, f32
+    queries, outputs and appended rows.  Two dispatch patterns per layer:
+    one batched call (the rows of every sequence, seq taken per row) and the
+    reference's own pattern, kv_store for all rows then one attn per
+    sequence chunk with AttnSpec.seq fixed (transformer/forward.rs:314-336),
+    issued from Python.  A one-sequence call holds only kv_heads groups, so
+    that pattern runs on a pool of 256-key partitions (128 workgroups per
+    call; the default 4096 gives 8); the batched call on the default.  Events
+    around `steps` passes; us per layer."""
+    from flint_amd.pool import ArenaSpec, KvPool, RowMeta
+
+    pl = 32
+
+    def make(part_len):
+        pool = KvPool(ArenaSpec([ctx] * B, B * (-(-ctx // pl))), nkv, hd, layers=layers, page_len=pl,
+                      kv_dtype="bf16", part_len=part_len)
+        scattered_alloc(pool, [ctx] * B, random.Random(1012), pl)
+        pool.sync()
+        gg = torch.Generator(device=dev)
+        gg.manual_seed(1012)
+        for layer in range(layers):
+            for t in pool.layer_tensors(layer):
+                t.view(torch.bfloat16).normal_(generator=gg)
+        return pool
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1013)
+    rows = RowMeta(B)
+    rows.write([ctx - 1] * B, list(range(B)), B)
+    q = torch.randn(B, nq, hd, device=dev, generator=g)
+    k = torch.randn(B, nkv, hd, device=dev, generator=g)
+    v = torch.randn(B, nkv, hd, device=dev, generator=g)
+    y = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(hd)
+    batched = ops.AttnSpec(q_heads=nq, window=0, scale=scale, m=B, causal=True, seq=None, args=rows)
+    per_seq = [ops.AttnSpec(q_heads=nq, window=0, scale=scale, m=1, causal=True, seq=s, args=rows, row_off=s)
+               for s in range(B)]
+
+    def one_call(pool):
+        for layer in range(layers):
+            ops.kv_store_attn(k, v, q, pool, layer, y, batched)
+
+    def reference_pattern(pool):
+        for layer in range(layers):
+            ops.kv_store(k, v, pool, layer, B, rows)
+            for s in range(B):
+                ops.attn(q[s:s + 1], pool, layer, y[s:s + 1], per_seq[s])
+
+    out = {}
+    for name, fn, part_len in (("batched", one_call, 0), ("per_sequence", reference_pattern, 256)):
+        pool = make(part_len)
+        out[name] = _time_steps(torch, lambda: fn(pool), steps, 2) / layers
+        pool.close()
+        torch.cuda.empty_cache()
+    return out
+
+
 def time_hbm_ceiling(torch, dev, mib=1024, reps=5):
     """The device's achievable linear HBM rate, measured next to the 8 TB/s
     specification: thb_hbm_stream over `mib` MiB with 16-byte non-temporal
@@ -1044,6 +1103,18 @@ def main():
         "scattered_over_identity": round(attn_us / ident_us, 4),
         "note": "the same fused append + decode with every sequence on consecutive pages vs pages scattered "
                 "at random (thuban_bench probes/attn.rs:97-133 compares identity and shuffled tables)"}
+    ref_us = time_reference_mode(torch, ops, dev, B, ctx, nq, nkv, hd)
+    ref_bytes = B * nkv * ctx * hd * 2 * 2 + 2 * B * nq * hd * 4 + B * nkv * hd * 4 * 2 + B * nkv * hd * 2 * 2
+    log(f"reference mode (bf16 KV, page 32, f32 q/y): batched {ref_us['batched']:.1f} us/layer, "
+        f"one call per sequence {ref_us['per_sequence']:.1f} us/layer")
+    out["reference_mode"] = {
+        "batched_us_per_layer": round(ref_us["batched"], 2),
+        "batched_GBps": round(ref_bytes / (ref_us["batched"] * 1e-6) / 1e9, 1),
+        "per_sequence_us_per_layer": round(ref_us["per_sequence"], 2),
+        "note": "the headline shape in the reference's storage and layout (bf16 KV by truncation, page 32, f32 q, "
+                "y and appended rows), 4 layers: one batched thb_attn_append per layer, and the reference's "
+                "dispatch pattern (kv_store, then one attn per sequence with AttnSpec.seq fixed, 32 calls "
+                "issued from Python, on a pool of 256-key partitions so that each call fills 128 CUs)"}
     out["o_proj"] = time_o_proj(torch, ops, dev, B, nq, hd, layers=L)
     ceiling = time_hbm_ceiling(torch, dev)
     out["hbm_ceiling"] = ceiling
