@@ -242,3 +242,89 @@ def test_captured_append_plan_replays_like_attn_append(torch_cuda):
     planned.status()
     del graph
     plan.close()
+
+
+N_RANDOM = 24
+
+
+def _random_case(seed):
+    rng = random.Random(seed)
+    hd = rng.choice([64, 128, 256])
+    nkv = rng.choice([1, 2, 4, 8])
+    g = rng.choice([1, 2, 4, 7, 8, 16, 32])
+    rg = 16 // g if g <= 16 else 1  # rows of one chunk that one group holds
+    lens = [rng.randint(24, 1200) for _ in range(rng.randint(1, 5))]
+    rps = [rng.randint(1, min(rg, 4)) for _ in lens]
+    if rng.random() < 0.25:  # one chunk a row longer than a group holds
+        rps[rng.randrange(len(rps))] = rg + 1
+    # the rows of each sequence, in order; sometimes one sequence comes back as a second chunk
+    chunks = [(s, list(range(n - r, n))) for s, (n, r) in enumerate(zip(lens, rps))]
+    if len(chunks) > 1 and rng.random() < 0.25:
+        s, pos = chunks[0]
+        if len(pos) > 1:
+            chunks[0] = (s, pos[:-1])
+            chunks.append((s, pos[-1:]))
+        else:
+            chunks.append((s, [pos[0] - 1]))
+    return dict(hd=hd, nkv=nkv, nq=g * nkv, g=g, lens=lens, chunks=chunks, part_len=rng.choice([128, 512, 4096]),
+                window=rng.choice([0, 0, rng.randint(1, 700)]), cap=rng.choice([0.0, 30.0]),
+                src=rng.choice(["f32", "f16", "bf16"]))
+
+
+@pytest.mark.parametrize("seed", range(N_RANDOM))
+def test_random_append_plan_calls(torch_cuda, seed):
+    """Seeded random decode / verify calls (head_dim, grouping up to 32 query
+    heads per KV head, 1-5 rows per sequence, sometimes a sequence heading
+    two chunks, window, soft-cap, source type) through the append plan, on
+    twin pools.  Where build_plan's rule lets the append run inside the
+    launch (every chunk fits one group, no sequence in two chunks) the
+    outputs and pool bytes equal thb_attn_append's; otherwise the call is
+    planned empty: every output NaN, the pool untouched, the status names
+    the first failing row's reason."""
+    torch = torch_cuda
+    from flint_amd import ThubanError, ops
+    from flint_amd.pool import RowMeta
+
+    c = _random_case(5000 + seed)
+    say("random append plan", seed, {k: v for k, v in c.items() if k != "chunks"}, [len(p) for _, p in c["chunks"]])
+    eager, planned = _twin_pools(torch, f"rnd{seed}", c["lens"], c["nkv"], c["hd"], "f16", c["part_len"], seed=seed)
+    positions = [p for _, pos in c["chunks"] for p in pos]
+    seqs = [s for s, pos in c["chunks"] for _ in pos]
+    m = len(seqs)
+    rows = RowMeta(64)
+    rows.write(positions, seqs, m)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    dt = getattr(torch, _DT[c["src"]])
+    k = torch.randn(m, c["nkv"], c["hd"], device="cuda", generator=gen).to(dt)
+    v = torch.randn(m, c["nkv"], c["hd"], device="cuda", generator=gen).to(dt)
+    q = torch.randn(m, c["nq"], c["hd"], device="cuda", generator=gen)
+    spec = ops.AttnSpec(q_heads=c["nq"], window=c["window"], scale=1.0 / math.sqrt(c["hd"]), m=m, causal=True,
+                        seq=None, args=rows, softcap=c["cap"])
+    rg = 16 // c["g"] if c["g"] <= 16 else 1
+    heads = [s for s, _ in c["chunks"]]
+    fits = all(len(pos) <= rg for _, pos in c["chunks"])
+    fusable = fits and len(set(heads)) == len(heads)
+    got = torch.full_like(q, 7.0)
+    plan = ops.DevicePlan(planned, max_m=m, q_heads=c["nq"], append=True)
+    plan.build(spec, q, got)
+    plan.attn_append(0, k, v, q, got)
+    torch.cuda.synchronize()
+    plan.close()
+    if fusable:
+        want = torch.empty_like(q)
+        ops.kv_store_attn(k, v, q, eager, 0, want, spec)
+        torch.cuda.synchronize()
+        assert torch.isfinite(want).all(), seed
+        assert torch.equal(got, want), (seed, float((got - want).abs().max()))
+        assert _same_bytes(torch, eager, planned), seed
+        planned.status()
+        return
+    assert torch.isnan(got).all(), seed
+    assert _same_bytes(torch, eager, planned), (seed, "a refused call appended")
+    with pytest.raises(ThubanError) as e:
+        planned.status()
+    msg = str(e.value)
+    say("random append plan", seed, "refused:", msg)
+    assert msg.startswith("the append cannot run inside the attention launch"), msg
+    assert ("holds more rows than one group" in msg) if not fits else ("heads an earlier chunk" in msg), msg
