@@ -273,3 +273,72 @@ def test_captured_rope_step_replays_like_attn_step(torch_cuda):
     planned.status()
     del graph
     plan.close()
+
+
+N_RANDOM = 16
+
+
+@pytest.mark.parametrize("seed", range(N_RANDOM))
+def test_random_step_plan_calls(torch_cuda, seed):
+    """Seeded random calls of thb_attn_step_dplan against thb_attn_step on
+    twin pools: head_dim 64/128/256, 1-8 query heads per KV head, one group
+    of 1-4 rows per sequence, rotation of the whole head or its first half,
+    q/k norm or not, a q|gate projection with the gate or not, window and
+    soft-cap; the fixed-grid plan with the append inside the launch, or
+    without the append on either plan form (the keys appended first by
+    thb_kv_store_rope on both pools).  Outputs and pool bytes bit-identical."""
+    torch = torch_cuda
+    from flint_amd import ops
+    from flint_amd.pool import RowMeta
+    from flint_amd.rope import kv_store_rope
+
+    rng = random.Random(7000 + seed)
+    hd = rng.choice([64, 128, 256])
+    nkv = rng.choice([1, 2, 4, 8])
+    g = rng.choice([1, 2, 4, 8])
+    nq = g * nkv
+    rps = rng.randint(1, min(4, 16 // g))
+    lens = [rng.randint(rps + 8, 1500) for _ in range(rng.randint(1, 4))]
+    rot = rng.choice([hd, hd // 2]) if hd // 2 % 16 == 0 else hd
+    norm, gated = rng.random() < 0.5, rng.random() < 0.4
+    window, cap = rng.choice([0, 0, rng.randint(1, 600)]), rng.choice([0.0, 0.0, 30.0])
+    form = rng.choice(["append", "grid", "list"])
+    part_len = rng.choice([128, 512, 4096])
+    say("random step plan", seed, dict(hd=hd, nkv=nkv, g=g, rps=rps, lens=lens, rot=rot, norm=norm, gated=gated,
+                                       window=window, cap=cap, form=form, part_len=part_len))
+    eager, planned = _twins(torch, f"step{seed}", [n + rps for n in lens], nkv, hd, part_len, fill_lens=lens)
+    rope = _rope(hd, rot, norm, max_pos=2048, seed=seed)
+    positions = [p for n in lens for p in range(n, n + rps)]
+    seqs = [s for s, _ in enumerate(lens) for _ in range(rps)]
+    m = len(seqs)
+    rows = RowMeta(64)
+    rows.write(positions, seqs, m)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    k = torch.randn(m, nkv, hd, device="cuda", generator=gen)
+    v = torch.randn(m, nkv, hd, device="cuda", generator=gen)
+    if gated:
+        qg = torch.randn(m, nq, 2 * hd, device="cuda", generator=gen)
+        q, gate, stride = qg[:, :, :hd], qg[:, :, hd:], 2 * hd
+    else:
+        q, gate, stride = torch.randn(m, nq, hd, device="cuda", generator=gen), None, 0
+    spec = ops.AttnSpec(q_heads=nq, window=window, scale=1.0 / math.sqrt(hd), m=m, causal=True, seq=None, args=rows,
+                        softcap=cap)
+    append = form == "append"
+    if not append:  # the keys go in first, rotated, on both pools
+        for P in (eager, planned):
+            kv_store_rope(k, v, P, 0, m, rows, rope)
+    want = torch.empty(m, nq, hd, device="cuda")
+    got = torch.full_like(want, 7.0)
+    src = dict(k_src=k, v_src=v) if append else {}
+    ops.attn_step(eager, 0, spec, q, want, q_stride=stride, gate=gate, gate_stride=stride, rope=rope, **src)
+    plan = ops.DevicePlan(planned, max_m=m, q_heads=nq, prefill=form == "list", append=append)
+    plan.set_pos_limit(rope.max_pos)
+    plan.build(spec, q, got)
+    plan.step(0, q, got, q_stride=stride, gate=gate, gate_stride=stride, rope=rope, **src)
+    torch.cuda.synchronize()
+    plan.close()
+    planned.status()
+    assert torch.isfinite(want).all(), seed
+    assert torch.equal(got, want), (seed, float((got - want).abs().max()))
+    assert _same_bytes(torch, eager, planned), seed
